@@ -1,0 +1,120 @@
+/*
+ * kg_gfx950.h - C ABI of the MI355X (gfx950) backend for kernelcode_generate's
+ * data-parallel hot path: the tiled matmul, conv2d and flash-attention demo kernels.
+ *
+ * Every compute entry point has exactly the signature of the entry that the
+ * reference's execute engine binds through ctypes in a generated shared object:
+ *
+ *     extern "C" int kg_execute_entry(const _ArgSlot* ordered_args,
+ *                                     unsigned long long arg_count);
+ *
+ *   reference: kernel_gen/execute_engine/builtin_strategy/common.py:915-925 (C++ shim),
+ *              kernel_gen/execute_engine/runtime_args.py:217-237 (_CArgSlot, ctypes),
+ *              kernel_gen/execute_engine/runtime_args.py:793-811 (invoke_compiled_kernel)
+ *
+ * A gfx950 generated source (SourceBundle kernel.hip) defines kg_execute_entry as a
+ * forward to one of the entries below, so the reference's CompiledKernel.execute()
+ * contract (slots in DSL parameter order, return 0 on success, non-zero ->
+ * "runtime_throw_or_abort") is unchanged.
+ *
+ * Memory slots carry DEVICE pointers (torch ROCm tensor .data_ptr()), element shapes
+ * and element strides. Kernels allocate nothing per call. Calls are synchronous by
+ * default (the reference's cuda_sm89 launch ends with a device synchronize,
+ * include/cuda_sm89/Arch.h:166-168); kg_gfx950_set_launch_mode() switches to
+ * asynchronous launches on a caller-chosen stream for benchmarking.
+ *
+ * Return codes: 0 ok; -1 slot/shape/dtype validation failure; -2 HIP runtime error;
+ * -3 unsupported configuration. kg_gfx950_last_error() describes the last failure.
+ */
+#ifndef KG_GFX950_H_
+#define KG_GFX950_H_
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Slot kinds: reference builtin_strategy/common.py:910-914 (KG_ARG_MEMORY/INT/FLOAT). */
+enum {
+  KG_ARG_MEMORY = 1,
+  KG_ARG_INT = 2,
+  KG_ARG_FLOAT = 3
+};
+
+/* dtype codes 1-4 are the reference's (runtime_args.py:94-110, common.py:171-194);
+ * 5 (float16) and 6 (bfloat16) are additive extensions for the gfx950 MFMA paths. */
+enum {
+  KG_DTYPE_F32 = 1,
+  KG_DTYPE_F64 = 2,
+  KG_DTYPE_I32 = 3,
+  KG_DTYPE_I64 = 4,
+  KG_DTYPE_F16 = 5,
+  KG_DTYPE_BF16 = 6
+};
+
+/* Byte-for-byte the reference's _ArgSlot / _CArgSlot (runtime_args.py:228-237;
+ * common.py:915-924; include/cuda_sm89/Core.h:156-165). 56 bytes on LP64. */
+typedef struct KgArgSlot {
+  int kind;
+  void* data;
+  const long long* shape;
+  const long long* stride;
+  unsigned long long rank;
+  int dtype_code;
+  long long int_value;
+  double float_value;
+} KgArgSlot;
+
+/*
+ * Matmul demos: kernel/matmul/inputs_static_tile_static.py:56-110,
+ * kernel/matmul/inputs_static_tile_dynamic.py:64-120,
+ * kernel/matmul/inputs_dynamic_tile_dynamic.py:57-113.
+ * Slot order (test/cuda/test_cuda_sm89_kernel_demos_runtime.py:520):
+ *   (out[M,N], lhs[M,K], rhs[K,N], bias[N] | absent [, tile_m, tile_n, tile_k])
+ * 4 or 7 slots. dtypes: all f32, all bf16 or all f16 (bias may be f32 with bf16/f16
+ * operands). Absent bias = memory slot with data == NULL (runtime_args.py:497-516).
+ * Result: out = lhs @ rhs (+ bias[None, :]), fp32 accumulation.
+ */
+int kg_gfx950_matmul_entry(const KgArgSlot* ordered_args, unsigned long long arg_count);
+
+/*
+ * Conv2d demos (NCHW): kernel/conv2d/inputs_static_tile_static.py:115-215,
+ * kernel/conv2d/inputs_static_tile_dynamic.py:120, kernel/conv2d/inputs_dynamic_tile_dynamic.py:102-205.
+ * Slot order is the dynamic demo's (test/cuda/test_cuda_sm89_kernel_demos_runtime.py:380-404):
+ *   (out[N,F,Ho,Wo], input[N,C,H,W], weight[F,C,KH,KW], bias[F] | absent,
+ *    stride_h, stride_w, dilation_h, dilation_w, pad_top, pad_bottom, pad_left, pad_right
+ *    [, tile_f, tile_c, tile_n, tile_ho, tile_wo])
+ * 12 or 17 slots. Static demos bake stride/dilation/pad into their generated entry,
+ * which forwards the constants here. Ho/Wo follow kernel/conv2d/inputs_static_tile_static.py:155-156.
+ */
+int kg_gfx950_conv2d_entry(const KgArgSlot* ordered_args, unsigned long long arg_count);
+
+/*
+ * Flash-attention forward demos: kernel/flash_attention/inputs_static_tile_static.py:90-190,
+ * .../inputs_static_tile_dynamic.py:96, .../inputs_dynamic_tile_dynamic.py:96-195.
+ * Slot order (test/cuda/test_cuda_sm89_kernel_demos_runtime.py:592):
+ *   (out[B,H,S,D], q[B,H,S,D], k[B,H,S,D], v[B,H,S,D] [, br, bc [, scale, causal]])
+ * 4, 6 or 8 slots. The reference computes softmax(Q K^T) V with no scale and no mask;
+ * slots 6-7 are an additive extension: FLOAT scale (default 1.0) and INT causal
+ * (0/1, lower-triangular mask including the diagonal).
+ */
+int kg_gfx950_flash_attention_entry(const KgArgSlot* ordered_args, unsigned long long arg_count);
+
+/*
+ * Launch control (no counterpart in the reference, whose execute() is synchronous and
+ * rejects a stream: compiler.py:286-291). synchronous != 0 (default): every entry
+ * synchronizes its stream before returning. synchronous == 0: entries only enqueue on
+ * `stream` (a hipStream_t; NULL = null stream). Returns 0.
+ */
+int kg_gfx950_set_launch_mode(int synchronous, void* stream);
+
+/* Text of the last failure on the calling thread ("" if none). */
+const char* kg_gfx950_last_error(void);
+
+/* ABI revision of this library (bumped on any slot-contract change). */
+int kg_gfx950_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KG_GFX950_H_ */

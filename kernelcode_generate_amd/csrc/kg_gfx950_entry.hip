@@ -1,0 +1,457 @@
+// extern "C" entry points of libkg_gfx950.so (declared in include/kg_gfx950.h).
+//
+// Each entry validates the reference's slot contract (kind, rank, dtype, shape
+// consistency; kernel_gen/execute_engine/builtin_strategy/common.py:925-931 returns -1 on
+// any mismatch), picks the gfx950 kernel for the dtype/shape, launches it on the
+// configured stream and, in the default synchronous mode, waits for it.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "kg_gfx950.h"
+#include "kg_gfx950/common.h"
+#include "kg_gfx950/conv2d.h"
+#include "kg_gfx950/flash_attn.h"
+#include "kg_gfx950/gemm.h"
+#include "kg_gfx950/conv2d_mfma.h"
+#include "kg_gfx950/flash_attn_mfma.h"
+
+namespace {
+
+using namespace kg_gfx950;
+
+constexpr int kOk = 0;
+constexpr int kInvalid = -1;
+constexpr int kHipFailure = -2;
+constexpr int kUnsupported = -3;
+
+thread_local char g_last_error[512] = "";
+bool g_synchronous = true;
+hipStream_t g_stream = nullptr;
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int finish_launch(const char* what) {
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(kHipFailure, "%s: launch failed: %s", what, hipGetErrorString(err));
+  if (g_synchronous) {
+    err = hipStreamSynchronize(g_stream);
+    if (err != hipSuccess) return fail(kHipFailure, "%s: hip_runtime_failed: %s", what, hipGetErrorString(err));
+  }
+  g_last_error[0] = '\0';
+  return kOk;
+}
+
+// A memory slot viewed with its element shape/strides.
+struct Mem {
+  void* data = nullptr;
+  int rank = 0;
+  long long shape[8] = {0};
+  long long stride[8] = {0};
+  int dtype = 0;
+  bool present = false;
+
+  bool contiguous() const {
+    long long expect = 1;
+    for (int i = rank - 1; i >= 0; --i) {
+      if (shape[i] != 1 && stride[i] != expect) return false;
+      expect *= shape[i];
+    }
+    return true;
+  }
+  long long numel() const {
+    long long n = 1;
+    for (int i = 0; i < rank; ++i) n *= shape[i];
+    return n;
+  }
+};
+
+bool known_dtype(int code) {
+  return code == KG_DTYPE_F32 || code == KG_DTYPE_F16 || code == KG_DTYPE_BF16;
+}
+
+const char* dtype_name(int code) {
+  switch (code) {
+    case KG_DTYPE_F32: return "f32";
+    case KG_DTYPE_F64: return "f64";
+    case KG_DTYPE_I32: return "i32";
+    case KG_DTYPE_I64: return "i64";
+    case KG_DTYPE_F16: return "f16";
+    case KG_DTYPE_BF16: return "bf16";
+    default: return "unknown";
+  }
+}
+
+int read_mem(const KgArgSlot* slots, int idx, int rank, bool allow_absent, const char* name, Mem* out) {
+  const KgArgSlot& s = slots[idx];
+  if (s.kind != KG_ARG_MEMORY) return fail(kInvalid, "slot %d (%s): expected memory slot, got kind %d", idx, name, s.kind);
+  if (s.data == nullptr) {
+    if (!allow_absent) return fail(kInvalid, "slot %d (%s): memory slot has no data", idx, name);
+    out->present = false;
+    out->dtype = s.dtype_code;
+    return kOk;
+  }
+  if ((int)s.rank != rank) return fail(kInvalid, "slot %d (%s): expected rank %d, got %llu", idx, name, rank, s.rank);
+  if (s.shape == nullptr || s.stride == nullptr) return fail(kInvalid, "slot %d (%s): missing shape/stride", idx, name);
+  if (!known_dtype(s.dtype_code))
+    return fail(kInvalid, "slot %d (%s): unsupported dtype_code %d (%s)", idx, name, s.dtype_code, dtype_name(s.dtype_code));
+  out->data = s.data;
+  out->rank = rank;
+  out->dtype = s.dtype_code;
+  out->present = true;
+  bool empty = false;
+  long long last = 0;  // largest element offset addressed by the view
+  for (int i = 0; i < rank; ++i) {
+    if (s.shape[i] < 0) return fail(kInvalid, "slot %d (%s): negative extent", idx, name);
+    if (s.stride[i] < 0) return fail(kInvalid, "slot %d (%s): negative stride", idx, name);
+    out->shape[i] = s.shape[i];
+    out->stride[i] = s.stride[i];
+    if (s.shape[i] == 0) empty = true;
+    else last += (s.shape[i] - 1) * s.stride[i];
+  }
+  if (empty) return kOk;
+  // The kernels dereference these pointers on the GPU: refuse host memory and views that
+  // run past the end of their device allocation instead of faulting the device.
+  hipPointerAttribute_t attr;
+  if (hipPointerGetAttributes(&attr, s.data) != hipSuccess || attr.type != hipMemoryTypeDevice) {
+    (void)hipGetLastError();
+    return fail(kInvalid, "slot %d (%s): data is not a device pointer", idx, name);
+  }
+  hipDeviceptr_t base = nullptr;
+  size_t size = 0;
+  if (hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)s.data) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(kInvalid, "slot %d (%s): cannot query device allocation", idx, name);
+  }
+  const size_t elem = s.dtype_code == KG_DTYPE_F32 ? 4 : 2;
+  const size_t need = (size_t)((const char*)s.data - (const char*)base) + (size_t)(last + 1) * elem;
+  if (need > size)
+    return fail(kInvalid, "slot %d (%s): view needs %zu bytes but the allocation holds %zu", idx, name, need, size);
+  return kOk;
+}
+
+int read_int(const KgArgSlot* slots, int idx, const char* name, long long* out) {
+  const KgArgSlot& s = slots[idx];
+  if (s.kind != KG_ARG_INT) return fail(kInvalid, "slot %d (%s): expected int slot, got kind %d", idx, name, s.kind);
+  *out = s.int_value;
+  return kOk;
+}
+
+int read_float(const KgArgSlot* slots, int idx, const char* name, double* out) {
+  const KgArgSlot& s = slots[idx];
+  if (s.kind == KG_ARG_FLOAT) {
+    *out = s.float_value;
+    return kOk;
+  }
+  if (s.kind == KG_ARG_INT) {
+    *out = (double)s.int_value;
+    return kOk;
+  }
+  return fail(kInvalid, "slot %d (%s): expected float slot, got kind %d", idx, name, s.kind);
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int grid_1d(long long total, int threads) {
+  long long blocks = (total + threads - 1) / threads;
+  if (blocks > (1ll << 20)) blocks = 1ll << 20;
+  if (blocks < 1) blocks = 1;
+  return (int)blocks;
+}
+
+// ---------------------------------------------------------------------------------------
+// matmul
+// ---------------------------------------------------------------------------------------
+
+template <typename TA, typename TBias>
+int launch_gemm_simt(const Mem& out, const Mem& lhs, const Mem& rhs, const Mem& bias, int M, int N, int K) {
+  dim3 grid((N + 63) / 64, (M + 63) / 64);
+  const long long sbias = bias.present ? bias.stride[0] : 0;
+  hipLaunchKernelGGL((gemm_simt_kernel<TA, TA, TA, TBias>), grid, dim3(256), 0, g_stream,
+                     static_cast<const TA*>(lhs.data), static_cast<const TA*>(rhs.data), static_cast<TA*>(out.data),
+                     static_cast<const TBias*>(bias.present ? bias.data : nullptr), M, N, K, lhs.stride[0],
+                     lhs.stride[1], rhs.stride[0], rhs.stride[1], out.stride[0], out.stride[1], sbias);
+  return finish_launch("matmul(simt)");
+}
+
+template <typename Tag>
+int launch_gemm_mfma(const Mem& out, const Mem& lhs, const Mem& rhs, const Mem& bias, int M, int N, int K) {
+  const bool masked = (M % gemm::kBM) || (N % gemm::kBN) || (K % gemm::kBK);
+  const int tiles = ((M + gemm::kBM - 1) / gemm::kBM) * ((N + gemm::kBN - 1) / gemm::kBN);
+  const uint16_t* A = static_cast<const uint16_t*>(lhs.data);
+  const uint16_t* B = static_cast<const uint16_t*>(rhs.data);
+  uint16_t* C = static_cast<uint16_t*>(out.data);
+  const void* bp = bias.present ? bias.data : nullptr;
+  const int bias_kind = !bias.present ? 0 : (bias.dtype == KG_DTYPE_F32 ? 1 : 2);
+  const long long lda = lhs.stride[0], ldb = rhs.stride[0], ldc = out.stride[0];
+#define KG_GEMM_LAUNCH(MASKED, BIAS)                                                                     \
+  hipLaunchKernelGGL((gemm_mfma_kernel<Tag, MASKED, BIAS>), dim3(tiles), dim3(gemm::kThreads), 0, g_stream, A, \
+                     B, C, bp, M, N, K, lda, ldb, ldc)
+  if (masked) {
+    if (bias_kind == 0) KG_GEMM_LAUNCH(true, 0);
+    else if (bias_kind == 1) KG_GEMM_LAUNCH(true, 1);
+    else KG_GEMM_LAUNCH(true, 2);
+  } else {
+    if (bias_kind == 0) KG_GEMM_LAUNCH(false, 0);
+    else if (bias_kind == 1) KG_GEMM_LAUNCH(false, 1);
+    else KG_GEMM_LAUNCH(false, 2);
+  }
+#undef KG_GEMM_LAUNCH
+  return finish_launch("matmul(mfma)");
+}
+
+int matmul_impl(const KgArgSlot* args, unsigned long long n) {
+  if (args == nullptr) return fail(kInvalid, "ordered_args is null");
+  if (n != 4 && n != 7) return fail(kInvalid, "matmul expects 4 or 7 slots, got %llu", n);
+  Mem out, lhs, rhs, bias;
+  int rc;
+  if ((rc = read_mem(args, 0, 2, false, "out", &out))) return rc;
+  if ((rc = read_mem(args, 1, 2, false, "lhs", &lhs))) return rc;
+  if ((rc = read_mem(args, 2, 2, false, "rhs", &rhs))) return rc;
+  if ((rc = read_mem(args, 3, 1, true, "bias", &bias))) return rc;
+  if (n == 7) {
+    long long t;
+    const char* names[3] = {"tile_m", "tile_n", "tile_k"};
+    for (int i = 0; i < 3; ++i) {
+      if ((rc = read_int(args, 4 + i, names[i], &t))) return rc;
+      if (t <= 0) return fail(kInvalid, "%s must be positive, got %lld", names[i], t);
+    }
+  }
+  const long long M = lhs.shape[0], K = lhs.shape[1], N = rhs.shape[1];
+  if (rhs.shape[0] != K) return fail(kInvalid, "matmul: lhs K=%lld != rhs K=%lld", K, rhs.shape[0]);
+  if (out.shape[0] != M || out.shape[1] != N)
+    return fail(kInvalid, "matmul: out shape [%lld,%lld] != [%lld,%lld]", out.shape[0], out.shape[1], M, N);
+  if (bias.present && bias.shape[0] != N) return fail(kInvalid, "matmul: bias extent %lld != N=%lld", bias.shape[0], N);
+  if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff) return fail(kUnsupported, "matmul: extent exceeds int32");
+  if (lhs.dtype != out.dtype || rhs.dtype != out.dtype)
+    return fail(kInvalid, "matmul: lhs/rhs/out dtypes must match (%s, %s, %s)", dtype_name(lhs.dtype),
+                dtype_name(rhs.dtype), dtype_name(out.dtype));
+  if (bias.present && bias.dtype != out.dtype && bias.dtype != KG_DTYPE_F32)
+    return fail(kInvalid, "matmul: bias dtype %s must be f32 or match out", dtype_name(bias.dtype));
+  if (M == 0 || N == 0) return finish_launch("matmul(empty)");
+  const int m = (int)M, nn = (int)N, k = (int)K;
+
+  if (out.dtype == KG_DTYPE_F32) {
+    return launch_gemm_simt<float, float>(out, lhs, rhs, bias, m, nn, k);
+  }
+  const bool mfma_ok = k > 0 && (k % 8 == 0) && (nn % 8 == 0) && lhs.stride[1] == 1 && rhs.stride[1] == 1 &&
+                       out.stride[1] == 1 && lhs.stride[0] % 8 == 0 && rhs.stride[0] % 8 == 0 &&
+                       out.stride[0] % 8 == 0 && aligned16(lhs.data) && aligned16(rhs.data) && aligned16(out.data) &&
+                       (!bias.present || bias.stride[0] == 1);
+  if (out.dtype == KG_DTYPE_BF16) {
+    if (mfma_ok) return launch_gemm_mfma<Bf16Tag>(out, lhs, rhs, bias, m, nn, k);
+    if (bias.present && bias.dtype == KG_DTYPE_F32) return launch_gemm_simt<__bf16, float>(out, lhs, rhs, bias, m, nn, k);
+    return launch_gemm_simt<__bf16, __bf16>(out, lhs, rhs, bias, m, nn, k);
+  }
+  if (mfma_ok) return launch_gemm_mfma<F16Tag>(out, lhs, rhs, bias, m, nn, k);
+  if (bias.present && bias.dtype == KG_DTYPE_F32) return launch_gemm_simt<_Float16, float>(out, lhs, rhs, bias, m, nn, k);
+  return launch_gemm_simt<_Float16, _Float16>(out, lhs, rhs, bias, m, nn, k);
+}
+
+// ---------------------------------------------------------------------------------------
+// conv2d
+// ---------------------------------------------------------------------------------------
+
+template <typename T, typename TB>
+int launch_conv_direct(const Mem& out, const Mem& x, const Mem& w, const Mem& bias, const ConvShape& s) {
+  const long long total = out.numel();
+  hipLaunchKernelGGL((conv2d_direct_kernel<T, T, T, TB>), dim3(grid_1d(total, 256)), dim3(256), 0, g_stream,
+                     static_cast<const T*>(x.data), static_cast<const T*>(w.data), static_cast<T*>(out.data),
+                     static_cast<const TB*>(bias.present ? bias.data : nullptr), s);
+  return finish_launch("conv2d(direct)");
+}
+
+int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
+  if (args == nullptr) return fail(kInvalid, "ordered_args is null");
+  if (n != 12 && n != 17) return fail(kInvalid, "conv2d expects 12 or 17 slots, got %llu", n);
+  Mem out, x, w, bias;
+  int rc;
+  if ((rc = read_mem(args, 0, 4, false, "out", &out))) return rc;
+  if ((rc = read_mem(args, 1, 4, false, "input", &x))) return rc;
+  if ((rc = read_mem(args, 2, 4, false, "weight", &w))) return rc;
+  if ((rc = read_mem(args, 3, 1, true, "bias", &bias))) return rc;
+  long long p[8];
+  const char* names[8] = {"stride_h", "stride_w", "dilation_h", "dilation_w", "pad_top", "pad_bottom", "pad_left", "pad_right"};
+  for (int i = 0; i < 8; ++i)
+    if ((rc = read_int(args, 4 + i, names[i], &p[i]))) return rc;
+  for (int i = 0; i < 4; ++i)
+    if (p[i] <= 0) return fail(kInvalid, "conv2d: %s must be positive, got %lld", names[i], p[i]);
+  for (int i = 4; i < 8; ++i)
+    if (p[i] < 0) return fail(kInvalid, "conv2d: %s must be non-negative, got %lld", names[i], p[i]);
+  if (n == 17) {
+    const char* tnames[5] = {"tile_f", "tile_c", "tile_n", "tile_ho", "tile_wo"};
+    for (int i = 0; i < 5; ++i) {
+      long long t;
+      if ((rc = read_int(args, 12 + i, tnames[i], &t))) return rc;
+      if (t <= 0) return fail(kInvalid, "conv2d: %s must be positive, got %lld", tnames[i], t);
+    }
+  }
+  if (!x.contiguous() || !w.contiguous() || !out.contiguous() || (bias.present && bias.stride[0] != 1))
+    return fail(kInvalid, "conv2d: memory args must be contiguous");
+  if (x.dtype != out.dtype || w.dtype != out.dtype) return fail(kInvalid, "conv2d: input/weight/out dtypes must match");
+  if (bias.present && bias.dtype != out.dtype && bias.dtype != KG_DTYPE_F32)
+    return fail(kInvalid, "conv2d: bias dtype must be f32 or match out");
+  ConvShape s;
+  s.n = (int)x.shape[0];
+  s.c = (int)x.shape[1];
+  s.h = (int)x.shape[2];
+  s.w = (int)x.shape[3];
+  s.f = (int)w.shape[0];
+  s.kh = (int)w.shape[2];
+  s.kw = (int)w.shape[3];
+  s.sh = (int)p[0];
+  s.sw = (int)p[1];
+  s.dh = (int)p[2];
+  s.dw = (int)p[3];
+  s.pt = (int)p[4];
+  s.pl = (int)p[6];
+  if (w.shape[1] != x.shape[1]) return fail(kInvalid, "conv2d: weight C=%lld != input C=%lld", w.shape[1], x.shape[1]);
+  const long long ho = (x.shape[2] + p[4] + p[5] - p[2] * (w.shape[2] - 1) - 1) / p[0] + 1;
+  const long long wo = (x.shape[3] + p[6] + p[7] - p[3] * (w.shape[3] - 1) - 1) / p[1] + 1;
+  if (ho <= 0 || wo <= 0) return fail(kInvalid, "conv2d: empty output window (Ho=%lld, Wo=%lld)", ho, wo);
+  s.ho = (int)ho;
+  s.wo = (int)wo;
+  if (out.shape[0] != x.shape[0] || out.shape[1] != w.shape[0] || out.shape[2] != ho || out.shape[3] != wo)
+    return fail(kInvalid, "conv2d: out shape [%lld,%lld,%lld,%lld] != [%lld,%lld,%lld,%lld]", out.shape[0], out.shape[1],
+                out.shape[2], out.shape[3], x.shape[0], w.shape[0], ho, wo);
+  if (bias.present && bias.shape[0] != w.shape[0]) return fail(kInvalid, "conv2d: bias extent != F");
+  if (out.numel() == 0) return finish_launch("conv2d(empty)");
+
+  if (out.dtype == KG_DTYPE_F16 && conv_mfma_supported(s) && aligned16(x.data) && aligned16(out.data)) {
+    const int bias_kind = !bias.present ? 0 : (bias.dtype == KG_DTYPE_F32 ? 1 : 2);
+    hipError_t e = launch_conv2d_mfma<F16Tag>(static_cast<const uint16_t*>(x.data), static_cast<const uint16_t*>(w.data),
+                                              static_cast<uint16_t*>(out.data), bias.present ? bias.data : nullptr,
+                                              bias_kind, s, g_stream);
+    if (e != hipSuccess) return fail(kHipFailure, "conv2d(mfma): %s", hipGetErrorString(e));
+    return finish_launch("conv2d(mfma)");
+  }
+  if (out.dtype == KG_DTYPE_BF16 && conv_mfma_supported(s) && aligned16(x.data) && aligned16(out.data)) {
+    const int bias_kind = !bias.present ? 0 : (bias.dtype == KG_DTYPE_F32 ? 1 : 2);
+    hipError_t e = launch_conv2d_mfma<Bf16Tag>(static_cast<const uint16_t*>(x.data), static_cast<const uint16_t*>(w.data),
+                                               static_cast<uint16_t*>(out.data), bias.present ? bias.data : nullptr,
+                                               bias_kind, s, g_stream);
+    if (e != hipSuccess) return fail(kHipFailure, "conv2d(mfma): %s", hipGetErrorString(e));
+    return finish_launch("conv2d(mfma)");
+  }
+  const bool f32_bias = bias.present && bias.dtype == KG_DTYPE_F32;
+  switch (out.dtype) {
+    case KG_DTYPE_F32: return launch_conv_direct<float, float>(out, x, w, bias, s);
+    case KG_DTYPE_BF16:
+      return f32_bias ? launch_conv_direct<__bf16, float>(out, x, w, bias, s) : launch_conv_direct<__bf16, __bf16>(out, x, w, bias, s);
+    default:
+      return f32_bias ? launch_conv_direct<_Float16, float>(out, x, w, bias, s)
+                      : launch_conv_direct<_Float16, _Float16>(out, x, w, bias, s);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// flash attention
+// ---------------------------------------------------------------------------------------
+
+template <typename T>
+int launch_fa_simt(const Mem& out, const Mem& q, const Mem& k, const Mem& v, const FaShape& s) {
+  dim3 grid(s.s_q, s.bh);
+  hipLaunchKernelGGL((fa_fwd_simt_kernel<T>), grid, dim3(128), 0, g_stream, static_cast<const T*>(q.data),
+                     static_cast<const T*>(k.data), static_cast<const T*>(v.data), static_cast<T*>(out.data), s);
+  return finish_launch("flash_attention(simt)");
+}
+
+int flash_attention_impl(const KgArgSlot* args, unsigned long long n) {
+  if (args == nullptr) return fail(kInvalid, "ordered_args is null");
+  if (n != 4 && n != 6 && n != 8) return fail(kInvalid, "flash_attention expects 4, 6 or 8 slots, got %llu", n);
+  Mem out, q, k, v;
+  int rc;
+  if ((rc = read_mem(args, 0, 4, false, "out", &out))) return rc;
+  if ((rc = read_mem(args, 1, 4, false, "q", &q))) return rc;
+  if ((rc = read_mem(args, 2, 4, false, "k", &k))) return rc;
+  if ((rc = read_mem(args, 3, 4, false, "v", &v))) return rc;
+  double scale = 1.0;
+  long long causal = 0;
+  if (n >= 6) {
+    long long br, bc;
+    if ((rc = read_int(args, 4, "br", &br))) return rc;
+    if ((rc = read_int(args, 5, "bc", &bc))) return rc;
+    if (br <= 0 || bc <= 0) return fail(kInvalid, "flash_attention: br/bc must be positive");
+  }
+  if (n == 8) {
+    if ((rc = read_float(args, 6, "scale", &scale))) return rc;
+    if ((rc = read_int(args, 7, "causal", &causal))) return rc;
+    if (causal != 0 && causal != 1) return fail(kInvalid, "flash_attention: causal must be 0 or 1");
+    if (!std::isfinite(scale)) return fail(kInvalid, "flash_attention: scale must be finite");
+  }
+  for (int i = 0; i < 4; ++i) {
+    if (q.shape[i] != out.shape[i]) return fail(kInvalid, "flash_attention: q/out shape mismatch at dim %d", i);
+    if (k.shape[i] != v.shape[i]) return fail(kInvalid, "flash_attention: k/v shape mismatch at dim %d", i);
+  }
+  if (k.shape[0] != q.shape[0] || k.shape[1] != q.shape[1] || k.shape[3] != q.shape[3])
+    return fail(kInvalid, "flash_attention: k batch/head/dim must match q");
+  if (!out.contiguous() || !q.contiguous() || !k.contiguous() || !v.contiguous())
+    return fail(kInvalid, "flash_attention: memory args must be contiguous");
+  if (q.dtype != out.dtype || k.dtype != out.dtype || v.dtype != out.dtype)
+    return fail(kInvalid, "flash_attention: q/k/v/out dtypes must match");
+  FaShape s;
+  s.bh = (int)(q.shape[0] * q.shape[1]);
+  s.s_q = (int)q.shape[2];
+  s.s_kv = (int)k.shape[2];
+  s.d = (int)q.shape[3];
+  s.scale = (float)scale;
+  s.causal = (int)causal;
+  if (out.numel() == 0) return finish_launch("flash_attention(empty)");
+  if (s.d > 512) return fail(kUnsupported, "flash_attention: head dim %d > 512", s.d);
+  if (s.causal && s.s_kv != s.s_q) return fail(kUnsupported, "flash_attention: causal mask needs S_q == S_kv");
+
+  if ((out.dtype == KG_DTYPE_BF16 || out.dtype == KG_DTYPE_F16) && fa_mfma_supported(s) && aligned16(q.data) &&
+      aligned16(k.data) && aligned16(v.data) && aligned16(out.data)) {
+    hipError_t e = out.dtype == KG_DTYPE_BF16
+                       ? launch_fa_fwd_mfma<Bf16Tag>(static_cast<const uint16_t*>(q.data), static_cast<const uint16_t*>(k.data),
+                                                     static_cast<const uint16_t*>(v.data), static_cast<uint16_t*>(out.data), s,
+                                                     g_stream)
+                       : launch_fa_fwd_mfma<F16Tag>(static_cast<const uint16_t*>(q.data), static_cast<const uint16_t*>(k.data),
+                                                    static_cast<const uint16_t*>(v.data), static_cast<uint16_t*>(out.data), s,
+                                                    g_stream);
+    if (e != hipSuccess) return fail(kHipFailure, "flash_attention(mfma): %s", hipGetErrorString(e));
+    return finish_launch("flash_attention(mfma)");
+  }
+  switch (out.dtype) {
+    case KG_DTYPE_F32: return launch_fa_simt<float>(out, q, k, v, s);
+    case KG_DTYPE_BF16: return launch_fa_simt<__bf16>(out, q, k, v, s);
+    default: return launch_fa_simt<_Float16>(out, q, k, v, s);
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int kg_gfx950_matmul_entry(const KgArgSlot* ordered_args, unsigned long long arg_count) {
+  return matmul_impl(ordered_args, arg_count);
+}
+
+int kg_gfx950_conv2d_entry(const KgArgSlot* ordered_args, unsigned long long arg_count) {
+  return conv2d_impl(ordered_args, arg_count);
+}
+
+int kg_gfx950_flash_attention_entry(const KgArgSlot* ordered_args, unsigned long long arg_count) {
+  return flash_attention_impl(ordered_args, arg_count);
+}
+
+int kg_gfx950_set_launch_mode(int synchronous, void* stream) {
+  g_synchronous = synchronous != 0;
+  g_stream = static_cast<hipStream_t>(stream);
+  return kOk;
+}
+
+const char* kg_gfx950_last_error(void) { return g_last_error; }
+
+int kg_gfx950_abi_version(void) { return 1; }
+
+}  // extern "C"
