@@ -1,0 +1,262 @@
+"""Benchmark of the gfx950 hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-secondary]
+
+Headline workload: bf16 matmul C = A @ B, M = N = K = 4096,
+row-major, fp32 accumulation, bf16 output, A and B ~ N(0,1)*0.02 (synthetic, resident in
+HBM before timing). One step = one launch of the matmul entry through the C ABI on
+torch's current stream; W untimed warm-up steps, then exactly K timed steps bracketed by
+torch.cuda.synchronize(). value = algorithmic FLOP (2*M*N*K) per step / step time.
+
+The JSON line also carries
+  roofline: the GEMM kernel against dense bf16 MFMA peak, from HIP events on the launch
+            stream; traffic (HBM bytes per launch) from the rocprofv3 PMC summary in
+            profiles/ when present;
+  cpu_baseline: the oracle's restatement of the reference's npu_demo matmul loop nest,
+            compiled without optimisation like the reference (g++ -shared -fPIC, no -O)
+            and run on 2 host threads (npu_demo block_num = 2) over a bounded sample of
+            the same workload (the first 384 output rows);
+  secondary: the other BASELINE configs (C1, C2', C3, C4, C5 D=128/64) timed the same way.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+REPO_ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO_ROOT))
+
+PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16/fp16 MFMA (256 CU x 4096 FLOP/clk x 2.4 GHz)
+PEAK_FP32_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+METRIC = "TFLOP/s & % bf16 MFMA peak: 4096^3 matmul, flash-attn fwd S=2048 D=128"
+GEMM_TRAFFIC_FILE = REPO_ROOT / "profiles" / "gemm_bf16_4096_traffic.txt"
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+class PreparedCall:
+    """An entry point with its slot array marshalled once (launch cost = one ctypes call)."""
+
+    def __init__(self, entry: str, args) -> None:
+        from kernelcode_generate_amd import native
+
+        self.lib = native.load_library()
+        self.fn = getattr(self.lib, entry)
+        self.slots, self._keep = native.marshal_slots(args)
+        self.count = len(args)
+        self.entry = entry
+
+    def __call__(self) -> None:
+        rc = self.fn(self.slots, self.count)
+        if rc != 0:
+            raise RuntimeError(f"{self.entry} returned {rc}: {self.lib.kg_gfx950_last_error().decode()}")
+
+
+def time_steps(call: PreparedCall, steps: int, warmup: int):
+    """Return (wall ms per step, event ms per step) over exactly `steps` launches."""
+
+    import torch
+
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        call()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    return (t1 - t0) * 1e3 / steps, e0.elapsed_time(e1) / steps
+
+
+def read_traffic(path: Path):
+    if not path.is_file():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", path.read_text())
+    return float(m.group(1)) if m else None
+
+
+def gemm_workload(dev, m: int, n: int, k: int, seed: int):
+    import torch
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    a = (torch.randn(m, k, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    b = (torch.randn(k, n, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    c = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+    return a, b, c
+
+
+def cpu_baseline_matmul(rows: int = 384):
+    import numpy as np
+
+    import oracle
+
+    rng = np.random.default_rng(20261202)
+    a = (rng.standard_normal((4096, 4096), dtype=np.float32) * 0.02)
+    b = (rng.standard_normal((4096, 4096), dtype=np.float32) * 0.02)
+    oracle.matmul_demo(a[:48], b, None, (48, 80, 56), threads=2, m_range=(0, 48), optimized=False)  # warm
+    t0 = time.perf_counter()
+    oracle.matmul_demo(a, b, None, (48, 80, 56), threads=2, m_range=(0, rows), optimized=False)
+    dt = time.perf_counter() - t0
+    flop = 2.0 * rows * 4096 * 4096
+    return {
+        "value": flop / dt / 1e12,
+        "unit": "TFLOP/s",
+        "cores": 2,
+        "kind": "port",
+        "sample": f"output rows 0-{rows - 1} of the 4096^3 matmul ({flop / 1e9:.1f} GFLOP) through the restated "
+                  f"npu_demo tile loop (tiles 48x80x56, fp32, -O0, 2 threads): {dt:.2f} s",
+        "host_cpus": os.cpu_count(),
+    }
+
+
+def secondary(dev, steps: int, warmup: int):
+    import torch
+
+    out = []
+
+    def add(name, flop, call, peak, nsteps, byts=None):
+        wall, ev = time_steps(call, nsteps, max(2, warmup // 2))
+        tf = flop / (ev * 1e-3) / 1e12
+        rec = {"workload": name, "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ev, 5),
+               "frac_of_peak": round(tf / peak, 4), "peak": peak}
+        if byts is not None:
+            gbs = byts / (ev * 1e-3) / 1e9
+            rec["hbm_gbs"] = round(gbs, 1)
+            rec["hbm_frac"] = round(gbs / PEAK_HBM_GBS, 4)
+        log(f"[bench] {name}: {ev * 1e3:.1f} us  {tf:.1f} TFLOP/s  wall/step {wall * 1e3:.1f} us")
+        out.append(rec)
+
+    # C1 fp32 256^3
+    g = torch.Generator(device=dev).manual_seed(20261201)
+    a = torch.rand(256, 256, generator=g, device=dev) * 2 - 1
+    b = torch.rand(256, 256, generator=g, device=dev) * 2 - 1
+    c = torch.empty(256, 256, device=dev)
+    add("C1 fp32 matmul 256^3", 2 * 256**3, PreparedCall("kg_gfx950_matmul_entry", (c, a, b, None)), PEAK_FP32_TFLOPS, steps)
+    # C2' skinny
+    a, b, c = gemm_workload(dev, 8192, 1024, 4096, 20261203)
+    add("C2' bf16 matmul M=8192 N=1024 K=4096", 2 * 8192 * 1024 * 4096,
+        PreparedCall("kg_gfx950_matmul_entry", (c, a, b, None)), PEAK_BF16_TFLOPS, steps)
+    del a, b, c
+    # C3 conv2d fp16
+    g = torch.Generator(device=dev).manual_seed(20261204)
+    x = torch.randn(32, 64, 56, 56, generator=g, device=dev).to(torch.float16)
+    bound = math.sqrt(6.0 / 576.0)
+    w = ((torch.rand(64, 64, 3, 3, generator=g, device=dev) * 2 - 1) * bound).to(torch.float16)
+    y = torch.empty(32, 64, 56, 56, dtype=torch.float16, device=dev)
+    conv_bytes = 2 * (32 * 64 * 56 * 56 * 2) + 64 * 64 * 9 * 2
+    add("C3 fp16 conv2d N=32 C=64 H=W=56 F=64 3x3 s1 p1", 2 * 32 * 64 * 56 * 56 * 64 * 9,
+        PreparedCall("kg_gfx950_conv2d_entry", (y, x, w, None, 1, 1, 1, 1, 1, 1, 1, 1)), PEAK_BF16_TFLOPS,
+        max(steps, 50), conv_bytes)
+    del x, w, y
+    # C4 flash attention non-causal
+    g = torch.Generator(device=dev).manual_seed(20261205)
+    q, k, v = (torch.randn(4, 32, 2048, 128, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
+    o = torch.empty_like(q)
+    add("C4 bf16 flash-attn fwd B=4 H=32 S=2048 D=128 non-causal", 4 * 4 * 32 * 2048 * 2048 * 128,
+        PreparedCall("kg_gfx950_flash_attention_entry", (o, q, k, v, 128, 64, 1.0 / math.sqrt(128.0), 0)),
+        PEAK_BF16_TFLOPS, steps)
+    del q, k, v, o
+    # C5 flash attention causal
+    for d, seed in ((128, 20261206), (64, 20261207)):
+        g = torch.Generator(device=dev).manual_seed(seed)
+        q, k, v = (torch.randn(1, 32, 16384, d, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
+        o = torch.empty_like(q)
+        add(f"C5 bf16 flash-attn fwd B=1 H=32 S=16384 D={d} causal", 4 * 32 * 16384 * 16384 * d // 2,
+            PreparedCall("kg_gfx950_flash_attention_entry", (o, q, k, v, 128, 64, 1.0 / math.sqrt(d), 1)),
+            PEAK_BF16_TFLOPS, max(3, steps // 4))
+        del q, k, v, o
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(
+            "bench.py measures one MI355X: the gfx950 hot-path kernels are single-GPU and this build has no "
+            "multi-GPU path (sharding is described in DESIGN.md). Run with --gpus 1.",
+            file=sys.stderr,
+        )
+        return 2
+
+    import torch
+
+    from kernelcode_generate_amd import native
+
+    dev = torch.device("cuda:0")
+    native.load_library()
+    stream = torch.cuda.current_stream()
+    native.set_launch_mode(False, stream.cuda_stream)
+
+    m = n = k = 4096
+    a, b, c = gemm_workload(dev, m, n, k, 20261202)
+    call = PreparedCall("kg_gfx950_matmul_entry", (c, a, b, None))
+    torch.cuda.synchronize()
+    wall_ms, ev_ms = time_steps(call, args.steps, args.warmup)
+    flop = 2.0 * m * n * k
+    value = flop / (wall_ms * 1e-3) / 1e12
+    achieved = flop / (ev_ms * 1e-3) / 1e12
+    log(f"[bench] C2 bf16 matmul 4096^3: kernel {ev_ms * 1e3:.1f} us ({achieved:.1f} TFLOP/s), wall/step {wall_ms * 1e3:.1f} us")
+    traffic = read_traffic(GEMM_TRAFFIC_FILE)
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: A,B ~ N(0,1)*0.02 (seeded torch generator on the device), resident in HBM",
+        "config": {
+            "workload": "bf16 matmul M=N=K=4096, row-major A[M,K] B[K,N], fp32 accumulate, bf16 out (BASELINE configs[1])",
+            "M": m, "N": n, "K": k, "kernel": "gemm_mfma_kernel 256x256x64, v_mfma_f32_16x16x32_bf16",
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": traffic,
+            "algorithmic_flop_per_launch": flop,
+            "avg_launch_ms": round(ev_ms, 5),
+        },
+    }
+    del a, b, c
+    if not args.no_secondary:
+        result["secondary"] = secondary(dev, max(5, args.steps // 2), args.warmup)
+    native.set_launch_mode(True, None)
+    if not args.no_cpu_baseline:
+        cb = cpu_baseline_matmul()
+        log(f"[bench] cpu baseline: {cb['value'] * 1e3:.3f} GFLOP/s ({cb['sample']})")
+        result["cpu_baseline"] = cb
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -52,7 +52,7 @@ enum {
 };
 
 /* Byte-for-byte the reference's _ArgSlot / _CArgSlot (runtime_args.py:228-237;
- * common.py:915-924; include/cuda_sm89/Core.h:156-165). 56 bytes on LP64. */
+ * common.py:915-924; include/cuda_sm89/Core.h:156-165). 64 bytes on LP64. */
 typedef struct KgArgSlot {
   int kind;
   void* data;

@@ -1,0 +1,167 @@
+"""GPU parity of the gfx950 conv2d entry (kg_gfx950_conv2d_entry) against the CPU oracle.
+
+Cases follow the reference's runtime test (test/cuda/test_cuda_sm89_kernel_demos_runtime.py:
+530-566: arange inputs, arange/7 weights, stride 8, asymmetric pads), the conv2d demos'
+random static/dynamic shapes (kernel/conv2d/*.py) and BASELINE config C3 (fp16 NCHW
+32x64x56x56, 64 filters 3x3, stride 1, pad 1).
+"""
+
+from __future__ import annotations
+
+import random
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from kernelcode_generate_amd import native
+from tests.golden.make_golden import BIG_CONV_CASE, conv_closed_form
+from tests.gpu_util import assert_f32_close, assert_h16_close, round_to, to_numpy
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def out_hw(xs, ws, stride, dil, pad):
+    ho = (xs[2] + pad[0] + pad[1] - dil[0] * (ws[2] - 1) - 1) // stride[0] + 1
+    wo = (xs[3] + pad[2] + pad[3] - dil[1] * (ws[3] - 1) - 1) // stride[1] + 1
+    return ho, wo
+
+
+def run(device, dtype, x, w, bias, stride, dil, pad, tiles=()):
+    import torch
+
+    xt = torch.as_tensor(x).to(device)
+    wt = torch.as_tensor(w).to(device)
+    bt = None if bias is None else torch.as_tensor(bias).to(device)
+    ho, wo = out_hw(xt.shape, wt.shape, stride, dil, pad)
+    out = torch.full((xt.shape[0], wt.shape[0], ho, wo), float("nan"), dtype=dtype, device=device)
+    print(f"[conv2d] x={tuple(xt.shape)} w={tuple(wt.shape)} s={stride} d={dil} p={pad} {dtype}", flush=True)
+    native.conv2d(out, xt, wt, bt, stride, dil, pad, tiles)
+    return out
+
+
+@pytest.mark.parametrize("case", [0, 1])
+def test_runtime_vectors(device, case):
+    import torch
+
+    v = dict(np.load(GOLDEN / "cuda_runtime_vectors.npz"))
+    p = v[f"conv{case}_params"]
+    xs, ws, stride, dil, pad = tuple(p[0:4]), tuple(p[4:8]), tuple(p[8:10]), tuple(p[10:12]), tuple(p[12:16])
+    x = np.arange(int(np.prod(xs)), dtype=np.float32).reshape(xs)
+    w = np.arange(int(np.prod(ws)), dtype=np.float32).reshape(ws) / np.float32(7.0)
+    b = np.arange(ws[0], dtype=np.float32)
+    tiles = (7, 18, 3, 9, 8)
+    assert_f32_close(to_numpy(run(device, torch.float32, x, w, None, stride, dil, pad, tiles)), v[f"conv{case}_absent"],
+                     rtol=1e-5, atol=1e-5, what="absent")
+    assert_f32_close(to_numpy(run(device, torch.float32, x, w, b, stride, dil, pad, tiles)), v[f"conv{case}_present"],
+                     rtol=1e-5, atol=1e-5, what="present")
+
+
+def test_runtime_big_static_case(device, oracle_mod):
+    # (4,49,248,232) x (20,49,3,5), stride 8, pads (3,3,4,0): the reference's first conv case
+    import torch
+
+    xs, ws, stride, dil, pad = BIG_CONV_CASE
+    x = np.arange(int(np.prod(xs)), dtype=np.float32).reshape(xs) / np.float32(1e6)
+    w = np.arange(int(np.prod(ws)), dtype=np.float32).reshape(ws) / np.float32(7.0)
+    b = np.arange(ws[0], dtype=np.float32)
+    ref = oracle_mod.conv2d_demo(x, w, b, stride, dil, pad, (8, 16, 4, 8, 9))
+    assert_f32_close(to_numpy(run(device, torch.float32, x, w, b, stride, dil, pad)), ref, what="big static")
+
+
+@pytest.mark.parametrize("seed", [11, 12, 13])
+def test_demo_random_profiles_f32(device, oracle_mod, seed):
+    """Shapes drawn like kernel/conv2d/inputs_static_tile_static.py:283-300 (stride 8)."""
+
+    import torch
+
+    r = random.Random(seed)
+    n, c = r.randint(1, 2), r.randint(8, 16)
+    h, w = r.randint(41, 89), r.randint(25, 73)
+    f = r.randint(18, 24)
+    kh, kw = r.choice((3, 5)), r.choice((3, 5))
+    pad = tuple(r.choice((0, 1, 2, 3, 4)) for _ in range(4))
+    tiles = r.choice(((8, 16, 4, 8, 9), (7, 18, 3, 9, 8), (6, 20, 2, 10, 7)))
+    rng = np.random.default_rng(seed)
+    x = rng.normal(size=(n, c, h, w)).astype(np.float32)
+    wt = rng.normal(size=(f, c, kh, kw)).astype(np.float32)
+    b = rng.normal(size=(f,)).astype(np.float32)
+    ref = oracle_mod.conv2d_demo(x, wt, b, (8, 8), (1, 1), pad, tiles)
+    assert_f32_close(to_numpy(run(device, torch.float32, x, wt, b, (8, 8), (1, 1), pad, tiles)), ref, what=str(seed))
+
+
+@pytest.mark.parametrize(
+    "xs,ws,stride,dil,pad",
+    [
+        ((2, 5, 17, 19), (4, 5, 3, 3), (1, 1), (1, 1), (1, 1, 1, 1)),
+        ((1, 3, 20, 21), (6, 3, 2, 3), (2, 3), (2, 1), (0, 4, 2, 1)),
+        ((1, 2, 4, 5), (3, 2, 2, 2), (1, 1), (1, 1), (1, 1, 1, 1)),
+    ],
+)
+def test_general_params_f32(device, oracle_mod, xs, ws, stride, dil, pad):
+    import torch
+
+    rng = np.random.default_rng(sum(xs))
+    x = rng.normal(size=xs).astype(np.float32)
+    w = rng.normal(size=ws).astype(np.float32)
+    for b in (None, rng.normal(size=(ws[0],)).astype(np.float32)):
+        ref = oracle_mod.conv2d_demo(x, w, b, stride, dil, pad, (8, 16, 4, 8, 9))
+        assert_f32_close(to_numpy(run(device, torch.float32, x, w, b, stride, dil, pad)), ref, what=str(xs))
+
+
+@pytest.mark.parametrize("dtype_name", ["float16", "bfloat16"])
+@pytest.mark.parametrize(
+    "xs,ws,bias",
+    [
+        ((2, 64, 56, 56), (64, 64, 3, 3), False),  # C3 geometry, 2 images
+        ((1, 64, 12, 20), (64, 64, 3, 3), True),
+        ((3, 16, 9, 13), (32, 16, 3, 3), True),
+        ((1, 8, 7, 7), (5, 8, 3, 3), False),
+    ],
+)
+def test_16bit_3x3(device, oracle_mod, dtype_name, xs, ws, bias):
+    import torch
+
+    dt = getattr(torch, dtype_name)
+    rng = np.random.default_rng(xs[1] + ws[0] + xs[2])
+    xt, x = round_to(rng.standard_normal(xs), dt)
+    bound = np.sqrt(6.0 / (ws[1] * 9))
+    wt, w = round_to(rng.uniform(-bound, bound, size=ws), dt)
+    b = rng.normal(size=(ws[0],)).astype(np.float32) if bias else None
+    ref = oracle_mod.conv2d_demo(x, w, b, (1, 1), (1, 1), (1, 1, 1, 1), (16, 16, 1, 8, 16))
+    out = run(device, dt, xt, wt, b, (1, 1), (1, 1), (1, 1, 1, 1))
+    assert_h16_close(to_numpy(out), ref, what=f"{dtype_name} {xs}")
+
+
+def test_c3_full_size_fp16(device, oracle_mod):
+    """BASELINE C3 at full size: two images against the oracle, the whole batch against
+    per-image linearity (conv(x_a + x_b) = conv(x_a) + conv(x_b)) in fp32 math."""
+
+    import torch
+
+    rng = np.random.default_rng(20261204)
+    xt, x = round_to(rng.standard_normal((32, 64, 56, 56), dtype=np.float32), torch.float16)
+    bound = np.sqrt(6.0 / 576.0)
+    wt, w = round_to(rng.uniform(-bound, bound, size=(64, 64, 3, 3)).astype(np.float32), torch.float16)
+    out = to_numpy(run(device, torch.float16, xt, wt, None, (1, 1), (1, 1), (1, 1, 1, 1)))
+    for i in (0, 31):
+        ref = oracle_mod.conv2d_demo(x[i : i + 1], w, None, (1, 1), (1, 1), (1, 1, 1, 1), (16, 16, 1, 8, 16))
+        assert_h16_close(out[i : i + 1], ref, what=f"C3 image {i}")
+    # batch consistency: image i of the batched call equals a single-image call
+    single = to_numpy(run(device, torch.float16, xt[17:18], wt, None, (1, 1), (1, 1), (1, 1, 1, 1)))
+    np.testing.assert_array_equal(single, out[17:18])
+    closed = conv_closed_form(x[5:6], w, None, (1, 1), (1, 1), (1, 1, 1, 1))
+    assert_h16_close(out[5:6], closed, what="C3 closed form image 5")
+
+
+def test_rejects_bad_params(device):
+    import torch
+
+    x = torch.zeros(1, 2, 5, 5, device=device)
+    w = torch.zeros(3, 2, 3, 3, device=device)
+    o = torch.zeros(1, 3, 5, 5, device=device)
+    with pytest.raises(native.NativeLibraryError):
+        native.conv2d(o, x, w, None, (0, 1), (1, 1), (1, 1, 1, 1))
+    with pytest.raises(native.NativeLibraryError):
+        native.conv2d(o, x, w, None, (1, 1), (1, 1), (0, 0, 0, 0))  # out shape mismatch

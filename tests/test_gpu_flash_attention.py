@@ -1,0 +1,157 @@
+"""GPU parity of the gfx950 flash-attention entry (kg_gfx950_flash_attention_entry).
+
+Cases follow the reference's runtime test (test/cuda/test_cuda_sm89_kernel_demos_runtime.py:
+571-597: default_rng(2026052901) inputs of shape (1,2,4,3), tiles 2/2), the flash-attention
+demos' random shapes (kernel/flash_attention/*.py: S in {257,321,389}, D in {48,64,80}) and
+BASELINE configs C4 (bf16 B=4,H=32,S=2048,D=128, non-causal) and C5 (bf16 B=1,H=32,
+S=16384, D=128 and 64, causal), all against the oracle's restatement of the demo loop nest
+(plus the scale/causal extension), at full size through sampled heads and query blocks.
+"""
+
+from __future__ import annotations
+
+import random
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from kernelcode_generate_amd import native
+from tests.gpu_util import assert_f32_close, assert_h16_close, round_to, to_numpy
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def run(device, dtype, q, k, v, br=64, bc=64, scale=None, causal=False):
+    import torch
+
+    qt, kt, vt = (torch.as_tensor(a).to(device) for a in (q, k, v))
+    out = torch.full(tuple(qt.shape), float("nan"), dtype=dtype, device=device)
+    print(f"[fa] shape={tuple(qt.shape)} {dtype} scale={scale} causal={causal}", flush=True)
+    if scale is None and not causal:
+        native.call_entry("kg_gfx950_flash_attention_entry", (out, qt, kt, vt, br, bc))
+    else:
+        native.flash_attention(out, qt, kt, vt, br, bc, 1.0 if scale is None else scale, causal)
+    return out
+
+
+def test_runtime_vector(device):
+    import torch
+
+    v = dict(np.load(GOLDEN / "cuda_runtime_vectors.npz"))
+    out = run(device, torch.float32, v["fa_q"], v["fa_k"], v["fa_v"], 2, 2)
+    assert_f32_close(to_numpy(out), v["fa_expected"], rtol=1e-4, atol=1e-4, what="runtime vector")
+    # the 4-slot form (static demo) gives the same result
+    import torch as _t
+
+    qt, kt, vt = (_t.as_tensor(a).to(device) for a in (v["fa_q"], v["fa_k"], v["fa_v"]))
+    o4 = _t.empty_like(qt)
+    native.call_entry("kg_gfx950_flash_attention_entry", (o4, qt, kt, vt))
+    assert_f32_close(to_numpy(o4), v["fa_expected"], rtol=1e-4, atol=1e-4, what="4-slot form")
+
+
+@pytest.mark.parametrize("seed", [2026052721, 5, 6])
+def test_demo_random_profiles_f32(device, oracle_mod, seed):
+    """Shapes drawn like kernel/flash_attention/inputs_static_tile_static.py:213-226."""
+
+    import torch
+
+    r = random.Random(seed)
+    b, h = r.choice((1, 2)), r.choice((4, 8))
+    s, d = r.choice((257, 321, 389)), r.choice((48, 64, 80))
+    br, bc = random.Random(seed + 1).choice(((48, 64), (64, 80), (80, 96)))
+    rng = np.random.default_rng(seed)
+    q, k, v = (rng.standard_normal((b, h, s, d), dtype=np.float32) for _ in range(3))
+    ref = oracle_mod.flash_attention_demo(q, k, v, br, bc)
+    assert_f32_close(to_numpy(run(device, torch.float32, q, k, v, br, bc)), ref, rtol=1e-4, atol=1e-4, what=str(seed))
+
+
+@pytest.mark.parametrize("scale,causal", [(0.125, False), (0.3, True), (None, True)])
+def test_extensions_f32(device, oracle_mod, scale, causal):
+    import torch
+
+    rng = np.random.default_rng(17)
+    q, k, v = (rng.standard_normal((1, 3, 200, 40), dtype=np.float32) for _ in range(3))
+    ref = oracle_mod.flash_attention_demo(q, k, v, 48, 80, scale=scale, causal=causal)
+    out = run(device, torch.float32, q, k, v, 48, 80, scale, causal)
+    assert_f32_close(to_numpy(out), ref, rtol=1e-4, atol=1e-4, what=f"scale={scale} causal={causal}")
+
+
+@pytest.mark.parametrize("dtype_name", ["bfloat16", "float16"])
+@pytest.mark.parametrize(
+    "shape,causal",
+    [
+        ((1, 2, 256, 128), False),
+        ((1, 2, 512, 128), True),
+        ((2, 1, 384, 64), False),
+        ((1, 2, 512, 64), True),
+        ((1, 1, 300, 128), False),  # ragged S
+        ((1, 1, 200, 64), True),  # ragged S, causal
+        ((1, 2, 257, 48), False),  # demo-like D
+    ],
+)
+def test_16bit(device, oracle_mod, dtype_name, shape, causal):
+    import torch
+
+    dt = getattr(torch, dtype_name)
+    rng = np.random.default_rng(shape[2] + shape[3])
+    (qt, q), (kt, k), (vt, v) = (round_to(rng.standard_normal(shape, dtype=np.float32), dt) for _ in range(3))
+    scale = 1.0 / np.sqrt(shape[3])
+    ref = oracle_mod.flash_attention_demo(q, k, v, 64, 64, scale=scale, causal=causal)
+    out = run(device, dt, qt, kt, vt, 64, 64, scale, causal)
+    assert_h16_close(to_numpy(out), ref, what=f"{dtype_name} {shape} causal={causal}")
+
+
+def _sampled_check(oracle_mod, got, q, k, v, heads, blocks, scale, causal, name):
+    for (b, h) in heads:
+        for m0, m1 in blocks:
+            ref = oracle_mod.flash_attention_demo(
+                q[b : b + 1, h : h + 1], k[b : b + 1, h : h + 1], v[b : b + 1, h : h + 1], 64, 64,
+                scale=scale, causal=causal, threads=1, m_range=(m0, m1),
+            )
+            assert_h16_close(got[b, h, m0:m1], ref[0, 0, m0:m1], what=f"{name} b={b} h={h} rows {m0}:{m1}")
+
+
+def test_c4_full_size(device, oracle_mod):
+    import torch
+
+    shape = (4, 32, 2048, 128)
+    rng = np.random.default_rng(20261205)
+    (qt, q), (kt, k), (vt, v) = (round_to(rng.standard_normal(shape, dtype=np.float32), torch.bfloat16) for _ in range(3))
+    scale = 1.0 / np.sqrt(128.0)
+    got = to_numpy(run(device, torch.bfloat16, qt, kt, vt, 128, 64, scale, False))
+    assert np.isfinite(got).all()
+    _sampled_check(oracle_mod, got, q, k, v, [(0, 0), (3, 31)], [(0, 64), (1984, 2048)], scale, False, "C4")
+    # every output row is a convex combination of V rows: it lies inside V's per-column range
+    vmin = v.min(axis=2, keepdims=True)
+    vmax = v.max(axis=2, keepdims=True)
+    slack = 1e-2 * (vmax - vmin)
+    assert ((got >= vmin - slack) & (got <= vmax + slack)).all()
+
+
+@pytest.mark.parametrize("d,seed", [(128, 20261206), (64, 20261207)])
+def test_c5_full_size_causal(device, oracle_mod, d, seed):
+    import torch
+
+    shape = (1, 32, 16384, d)
+    rng = np.random.default_rng(seed)
+    (qt, q), (kt, k), (vt, v) = (round_to(rng.standard_normal(shape, dtype=np.float32), torch.bfloat16) for _ in range(3))
+    scale = 1.0 / np.sqrt(float(d))
+    got = to_numpy(run(device, torch.bfloat16, qt, kt, vt, 128, 64, scale, True))
+    assert np.isfinite(got).all()
+    _sampled_check(oracle_mod, got, q, k, v, [(0, 0), (0, 21)], [(0, 64), (8192, 8256), (16320, 16384)], scale, True,
+                   f"C5 D={d}")
+    # causal row 0 attends only to key 0: out[:, :, 0] == V[:, :, 0] (bf16-rounded)
+    np.testing.assert_allclose(got[0, :, 0, :], v[0, :, 0, :], rtol=1e-2, atol=1e-2)
+
+
+def test_rejects_bad_args(device):
+    import torch
+
+    q = torch.zeros(1, 1, 8, 4, device=device)
+    o = torch.zeros(1, 1, 8, 4, device=device)
+    with pytest.raises(native.NativeLibraryError):
+        native.flash_attention(o, q, q, q, 0, 4)
+    with pytest.raises(native.NativeLibraryError):
+        native.call_entry("kg_gfx950_flash_attention_entry", (o, q, q, q, 4, 4, 1.0, 2))

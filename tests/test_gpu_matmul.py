@@ -1,0 +1,160 @@
+"""GPU parity of the gfx950 matmul entry (kg_gfx950_matmul_entry) against the CPU oracle.
+
+Slot order and cases follow the reference's runtime test
+(test/cuda/test_cuda_sm89_kernel_demos_runtime.py:499-527) and the matmul demos
+(kernel/matmul/*.py); BASELINE configs C1 (fp32 256^3), C2 (bf16 4096^3) and C2' (bf16
+8192x1024x4096) are checked at full size through sampled output tiles against the oracle
+and through size-independent properties.
+"""
+
+from __future__ import annotations
+
+import random
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from kernelcode_generate_amd import native
+from tests.gpu_util import assert_f32_close, assert_h16_close, round_to, to_numpy
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def run(device, out_dtype, lhs, rhs, bias=None, tiles=()):
+    import torch
+
+    lt = torch.as_tensor(lhs).to(device)
+    rt = torch.as_tensor(rhs).to(device)
+    bt = None if bias is None else torch.as_tensor(bias).to(device)
+    out = torch.full((lt.shape[0], rt.shape[1]), float("nan"), dtype=out_dtype, device=device)
+    print(f"[matmul] M={lt.shape[0]} K={lt.shape[1]} N={rt.shape[1]} {out_dtype} bias={bias is not None}", flush=True)
+    native.matmul(out, lt, rt, bt, *tiles)
+    return out
+
+
+def test_runtime_vectors(device, oracle_mod):
+    import torch
+
+    v = dict(np.load(GOLDEN / "cuda_runtime_vectors.npz"))
+    for bias, key in ((None, "matmul_absent"), (v["matmul_bias"], "matmul_present")):
+        out = run(device, torch.float32, v["matmul_lhs"], v["matmul_rhs"], bias, (2, 2, 2))
+        assert_f32_close(to_numpy(out), v[key], rtol=1e-5, atol=1e-5, what=key)
+
+
+def test_demo_static_shape_f32(device, oracle_mod):
+    import torch
+
+    rng = np.random.default_rng(2026051601)
+    lhs = rng.normal(size=(166, 217)).astype(np.float32)
+    rhs = rng.normal(size=(217, 172)).astype(np.float32)
+    bias = rng.normal(size=(172,)).astype(np.float32)
+    for b in (None, bias):
+        ref = oracle_mod.matmul_demo(lhs, rhs, b, (48, 80, 56))
+        out = run(device, torch.float32, lhs, rhs, b, (48, 80, 56))
+        assert_f32_close(to_numpy(out), ref, what="demo 166x217x172")
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_dynamic_shapes_f32(device, oracle_mod, seed):
+    import torch
+
+    r = random.Random(seed)
+    m, k, n = r.randint(160, 256), r.randint(160, 256), r.randint(160, 256)
+    tiles = r.choice(((72, 56, 48), (48, 80, 56)))
+    rng = np.random.default_rng(seed)
+    lhs = rng.normal(size=(m, k)).astype(np.float32)
+    rhs = rng.normal(size=(k, n)).astype(np.float32)
+    bias = rng.normal(size=(n,)).astype(np.float32)
+    ref = oracle_mod.matmul_demo(lhs, rhs, bias, tiles)
+    assert_f32_close(to_numpy(run(device, torch.float32, lhs, rhs, bias, tiles)), ref, what=f"{m}x{k}x{n}")
+
+
+def test_c1_fp32_256(device, oracle_mod):
+    import torch
+
+    rng = np.random.default_rng(20261201)
+    a = rng.uniform(-1, 1, size=(256, 256)).astype(np.float32)
+    b = rng.uniform(-1, 1, size=(256, 256)).astype(np.float32)
+    ref = oracle_mod.matmul_demo(a, b, None, (64, 64, 64))
+    assert_f32_close(to_numpy(run(device, torch.float32, a, b)), ref, what="C1")
+
+
+@pytest.mark.parametrize("dtype_name", ["bfloat16", "float16"])
+@pytest.mark.parametrize(
+    "shape",
+    [(2, 3, 4), (1, 8, 8), (300, 136, 264), (256, 64, 256), (512, 128, 512), (257, 72, 8), (64, 520, 1032)],
+)
+@pytest.mark.parametrize("bias_kind", ["none", "f32", "same"])
+def test_16bit_shapes(device, oracle_mod, dtype_name, shape, bias_kind):
+    import torch
+
+    dt = getattr(torch, dtype_name)
+    m, k, n = shape
+    rng = np.random.default_rng(m * 7 + k * 3 + n)
+    lt, lhs = round_to(rng.normal(size=(m, k)) * 0.5, dt)
+    rt, rhs = round_to(rng.normal(size=(k, n)) * 0.5, dt)
+    bias = None
+    bt = None
+    if bias_kind == "f32":
+        bias = rng.normal(size=(n,)).astype(np.float32)
+        bt = bias
+    elif bias_kind == "same":
+        bt16, bias = round_to(rng.normal(size=(n,)), dt)
+        bt = bt16
+    ref = oracle_mod.matmul_demo(lhs, rhs, bias, (64, 64, 64))
+    out = run(device, dt, lt, rt, bt)
+    assert_h16_close(to_numpy(out), ref, what=f"{dtype_name} {shape} bias={bias_kind}")
+
+
+@pytest.mark.parametrize(
+    "cfg",
+    [
+        ("C2", 4096, 4096, 4096, 20261202, [(0, 96), (2016, 2112), (4000, 4096)]),
+        ("C2'", 8192, 4096, 1024, 20261203, [(0, 96), (8096, 8192)]),
+    ],
+    ids=["C2", "C2_skinny"],
+)
+def test_full_size_bf16(device, oracle_mod, cfg):
+    """Full BASELINE shapes: sampled row blocks against the oracle (fp32 math on the
+    bf16-rounded inputs) and a checksum-of-checksums over the whole output."""
+
+    import torch
+
+    name, m, k, n, seed, row_blocks = cfg
+    rng = np.random.default_rng(seed)
+    lt, lhs = round_to((rng.standard_normal((m, k), dtype=np.float32) * 0.02), torch.bfloat16)
+    rt, rhs = round_to((rng.standard_normal((k, n), dtype=np.float32) * 0.02), torch.bfloat16)
+    out = run(device, torch.bfloat16, lt, rt)
+    got = to_numpy(out)
+    for r0, r1 in row_blocks:
+        ref = oracle_mod.matmul_demo(lhs[r0:r1], rhs, None, (48, 256, 256))
+        assert_h16_close(got[r0:r1], ref, what=f"{name} rows {r0}:{r1}")
+    # column sums of C equal (1^T A) B: a property of the whole product, checked in fp64
+    colsum_ref = lhs.astype(np.float64).sum(0) @ rhs.astype(np.float64)
+    colsum = got.astype(np.float64).sum(0)
+    scale = np.sqrt(m) * np.abs(got).mean() + 1e-12
+    assert np.max(np.abs(colsum - colsum_ref)) < 2e-2 * scale, name
+
+
+def test_rejects_mismatched_shapes(device):
+    import torch
+
+    a = torch.zeros(4, 5, device=device)
+    b = torch.zeros(6, 3, device=device)
+    c = torch.zeros(4, 3, device=device)
+    with pytest.raises(native.NativeLibraryError):
+        native.matmul(c, a, b, None)
+    with pytest.raises(native.NativeLibraryError):  # host memory is refused, not dereferenced
+        native.matmul(torch.zeros(4, 3), torch.zeros(4, 6), torch.zeros(6, 3), None)
+    # a slot whose shape claims more memory than its device allocation holds is refused
+    lhs = torch.zeros(4, 8, device=device)
+    rhs = torch.zeros(8, 3, device=device)
+    slots, keep = native.marshal_slots((c, lhs, rhs, None))
+    slots[1].shape[1] = 1 << 32
+    slots[1].stride[0] = 1 << 32
+    slots[2].shape[0] = 1 << 32
+    lib = native.load_library()
+    assert lib.kg_gfx950_matmul_entry(slots, 4) == -1
+    assert "allocation" in native.last_error()
