@@ -12,6 +12,9 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Element tags: the MFMA paths move 16-bit data as raw bits and only the MFMA
@@ -45,6 +48,10 @@ struct Half16<Bf16Tag> {
   static __device__ __forceinline__ float to_float(uint32_t bits) {
     return __builtin_bit_cast(float, bits << 16);
   }
+  // Two floats -> two bf16 (RNE) in one dword: v_cvt_pk_bf16_f32; `a` in the low half.
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+  }
 };
 
 template <>
@@ -63,6 +70,10 @@ struct Half16<F16Tag> {
   }
   static __device__ __forceinline__ float to_float(uint32_t bits) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+  }
+  // Two floats -> two fp16 (RNE) in one dword: v_cvt_pk_f16_f32; `a` in the low half.
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
   }
 };
 
