@@ -326,7 +326,7 @@ int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
   if (bias.present && bias.shape[0] != w.shape[0]) return fail(kInvalid, "conv2d: bias extent != F");
   if (out.numel() == 0) return finish_launch("conv2d(empty)");
 
-  if (out.dtype == KG_DTYPE_F16 && conv_mfma_supported(s) && aligned16(x.data) && aligned16(out.data)) {
+  if (out.dtype == KG_DTYPE_F16 && conv_mfma_supported(s) && aligned16(x.data) && aligned16(w.data) && aligned16(out.data)) {
     const int bias_kind = !bias.present ? 0 : (bias.dtype == KG_DTYPE_F32 ? 1 : 2);
     hipError_t e = launch_conv2d_mfma<F16Tag>(static_cast<const uint16_t*>(x.data), static_cast<const uint16_t*>(w.data),
                                               static_cast<uint16_t*>(out.data), bias.present ? bias.data : nullptr,
@@ -334,7 +334,7 @@ int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
     if (e != hipSuccess) return fail(kHipFailure, "conv2d(mfma): %s", hipGetErrorString(e));
     return finish_launch("conv2d(mfma)");
   }
-  if (out.dtype == KG_DTYPE_BF16 && conv_mfma_supported(s) && aligned16(x.data) && aligned16(out.data)) {
+  if (out.dtype == KG_DTYPE_BF16 && conv_mfma_supported(s) && aligned16(x.data) && aligned16(w.data) && aligned16(out.data)) {
     const int bias_kind = !bias.present ? 0 : (bias.dtype == KG_DTYPE_F32 ? 1 : 2);
     hipError_t e = launch_conv2d_mfma<Bf16Tag>(static_cast<const uint16_t*>(x.data), static_cast<const uint16_t*>(w.data),
                                                static_cast<uint16_t*>(out.data), bias.present ? bias.data : nullptr,
