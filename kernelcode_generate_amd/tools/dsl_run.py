@@ -1,0 +1,136 @@
+"""``dsl_run(func_obj, real_args, pipeline)`` for the gfx950 target
+(kernel_gen/tools/dsl_run.py:578-653): check the configured target and the arity against
+the kernel's signature, recognise the kernel (in place of mlir_gen), run the pipeline,
+generate the SourceBundle, compile it through ``ExecutionEngine("gfx950")`` and execute
+it with the real arguments.
+
+Memory arguments may be ROCm torch tensors (used in place) or host numpy arrays /
+CPU tensors, which are staged to the device and copied back after the call -- what the
+reference's cuda_sm89 entry does per call (source_bundle.py:647-707). ``None`` is
+allowed for the bias slot only; ints and floats are passed as INT / FLOAT slots.
+"""
+
+from __future__ import annotations
+
+import atexit
+import inspect
+from dataclasses import dataclass
+from numbers import Integral, Real
+from pathlib import Path
+from typing import Any, Callable
+
+from ..core.config import get_dump_dir, get_target
+from ..core.error import ErrorKind, ErrorModule, KernelCodeError
+from ..execute_engine import CompiledKernel, ExecuteResult, ExecutionEngine
+from ..gen_kernel import KernelPattern, gen_kernel, recognise
+from ..pipeline import PassManager, get_pipeline
+from ..pipeline.gfx950_lowering import LoweredKernel
+
+ARITY_ERROR = "DslRunArityMismatch: real_args count must match the kernel's positional parameters"
+_COMPILED: dict[str, CompiledKernel] = {}
+
+
+@atexit.register
+def _close_cached() -> None:
+    for kernel in _COMPILED.values():
+        try:
+            kernel.close()
+        except Exception:
+            pass
+    _COMPILED.clear()
+
+
+@dataclass(frozen=True)
+class DslRunResult:
+    pattern: KernelPattern
+    module: LoweredKernel
+    source: str
+    compiled_kernel: CompiledKernel
+    execute_result: ExecuteResult
+    runtime_args: tuple
+
+
+def _error(message: str) -> KernelCodeError:
+    return KernelCodeError(ErrorKind.CONTRACT, ErrorModule.TOOLS, message)
+
+
+def _dtype_name(value: Any) -> str:
+    return str(getattr(value, "dtype", "")).replace("torch.", "")
+
+
+def _stage(arg: Any):
+    """Return (device tensor, writeback callable or None) for one memory argument."""
+
+    import numpy as np
+    import torch
+
+    if isinstance(arg, np.ndarray):
+        if arg.dtype.name not in ("float32", "float16"):
+            raise _error(f"unsupported numpy dtype {arg.dtype}")
+        dev = torch.from_numpy(np.ascontiguousarray(arg)).to("cuda")
+
+        def back(host=arg, d=dev):
+            host[...] = d.cpu().numpy()
+
+        return dev, back
+    if isinstance(arg, torch.Tensor) and arg.device.type != "cuda":
+        dev = arg.contiguous().to("cuda")
+
+        def back(host=arg, d=dev):
+            host.copy_(d.cpu())
+
+        return dev, back
+    return arg, None
+
+
+def _resolve_pipeline(pipeline: str | PassManager) -> PassManager:
+    if isinstance(pipeline, PassManager):
+        return pipeline
+    if isinstance(pipeline, str):
+        return get_pipeline(pipeline)
+    raise _error("pipeline must be a registered name or a PassManager")
+
+
+def dsl_run(func_obj: Callable, real_args: tuple | list, pipeline: str | PassManager) -> DslRunResult:
+    target = get_target()
+    if target != "gfx950":
+        raise _error(f"DslRunInvalidTarget: core config target must be 'gfx950' for this backend, got {target!r}")
+    if not isinstance(real_args, (tuple, list)):
+        raise _error("real_args must be a tuple or list")
+    args = tuple(real_args)
+    params = [p for p in inspect.signature(func_obj).parameters.values()
+              if p.kind in (inspect.Parameter.POSITIONAL_ONLY, inspect.Parameter.POSITIONAL_OR_KEYWORD)]
+    if len(args) != len(params):
+        raise _error(ARITY_ERROR)
+    pm = _resolve_pipeline(pipeline)
+    memory = [a for a in args if a is not None and not isinstance(a, (Integral, Real))]
+    dtype = _dtype_name(memory[0]) if memory else "float32"
+    pattern = recognise(func_obj, dtype)
+    if len(pattern.params) != len(args):
+        raise _error(f"{pattern.function}: expected {len(pattern.params)} args, got {len(args)}")
+    lowered = pm.run(pattern)
+    source = gen_kernel(lowered.pattern)
+    dump = get_dump_dir()
+    if dump is not None:
+        out_dir = Path(dump) / pattern.function
+        out_dir.mkdir(parents=True, exist_ok=True)
+        (out_dir / "source.hip").write_text(source)
+    compiled = _COMPILED.get(source)
+    if compiled is None:
+        compiled = ExecutionEngine(target="gfx950").compile(source=source, function=pattern.function)
+        _COMPILED[source] = compiled
+    staged = []
+    writebacks = []
+    for a in args:
+        if a is None or isinstance(a, (Integral, Real)):
+            staged.append(a)
+            continue
+        dev, back = _stage(a)
+        staged.append(dev)
+        if back is not None:
+            writebacks.append(back)
+    result = compiled.execute(args=tuple(staged))
+    for back in writebacks:
+        back()
+    return DslRunResult(pattern=pattern, module=lowered, source=source, compiled_kernel=compiled,
+                        execute_result=result, runtime_args=tuple(staged))

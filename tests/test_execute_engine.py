@@ -1,0 +1,240 @@
+"""CPU tests of the gfx950 drop-in boundary: target registry, strategy registry, the
+SourceBundle emitter, the gfx950 compile strategy (real hipcc cross-compile and a fake
+compiler that records its command line, as test/execute_engine/test_cuda_sm89_strategy.py
+does with a fake nvcc) and the stable failure phrases of the execute engine."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import stat
+from pathlib import Path
+
+import pytest
+
+from kernelcode_generate_amd import native
+from kernelcode_generate_amd.core.config import restore_config, set_target, snapshot_config
+from kernelcode_generate_amd.core.error import KernelCodeError
+from kernelcode_generate_amd.execute_engine import (
+    CompileRequest,
+    ExecuteRequest,
+    ExecutionEngine,
+    get_compile_strategy,
+    register_compile_strategy,
+)
+from kernelcode_generate_amd.execute_engine.compiler import CompiledKernel
+from kernelcode_generate_amd.execute_engine.gfx950_strategy import Gfx950CompileStrategy, unbundle
+from kernelcode_generate_amd.execute_engine.runtime_args import parse_allow_absent, validate_args
+from kernelcode_generate_amd.gen_kernel import gen_kernel, known_patterns, recognise
+from kernelcode_generate_amd.kernel.conv2d.inputs_dynamic_tile_dynamic import conv2d_inputs_dynamic_tile_dynamic_kernel
+from kernelcode_generate_amd.kernel.conv2d.inputs_static_tile_dynamic import conv2d_inputs_static_tile_dynamic_kernel
+from kernelcode_generate_amd.kernel.conv2d.inputs_static_tile_static import conv2d_inputs_static_tile_static_kernel
+from kernelcode_generate_amd.kernel.flash_attention.inputs_dynamic_tile_dynamic import (
+    flash_attention_inputs_dynamic_tile_dynamic_kernel,
+)
+from kernelcode_generate_amd.kernel.flash_attention.inputs_static_tile_static import (
+    flash_attention_inputs_static_tile_static_kernel,
+)
+from kernelcode_generate_amd.kernel.flash_attention.scaled import flash_attention_scaled_causal_kernel
+from kernelcode_generate_amd.kernel.matmul.inputs_static_tile_dynamic import matmul_inputs_static_tile_dynamic_kernel
+from kernelcode_generate_amd.kernel.matmul.inputs_static_tile_static import matmul_inputs_static_tile_static_kernel
+from kernelcode_generate_amd.kernel.runner import run_lowering_demo
+from kernelcode_generate_amd.pipeline import build_gfx950_lowering_pipeline, get_pipeline
+from kernelcode_generate_amd.target import get_target_hardware, is_arch_op_supported
+from kernelcode_generate_amd.tools import dsl_run
+
+ALL_DEMOS = [
+    matmul_inputs_static_tile_static_kernel,
+    matmul_inputs_static_tile_dynamic_kernel,
+    conv2d_inputs_static_tile_static_kernel,
+    conv2d_inputs_static_tile_dynamic_kernel,
+    conv2d_inputs_dynamic_tile_dynamic_kernel,
+    flash_attention_inputs_static_tile_static_kernel,
+    flash_attention_inputs_dynamic_tile_dynamic_kernel,
+    flash_attention_scaled_causal_kernel,
+]
+
+
+def test_gfx950_target_spec():
+    assert get_target_hardware("gfx950", "block_num") == 256
+    assert get_target_hardware("gfx950", "subthread_num") == 64
+    assert get_target_hardware("gfx950", "sm_memory_size") == 160 * 1024
+    assert is_arch_op_supported("gfx950", "arch.barrier")
+    assert not is_arch_op_supported("gfx950", "arch.launch_kernel")
+    assert get_target_hardware("npu_demo", "block_num") == 2
+
+
+def test_strategy_registry_phrases():
+    assert isinstance(get_compile_strategy("gfx950"), Gfx950CompileStrategy)
+    with pytest.raises(KernelCodeError) as err:
+        get_compile_strategy("npu_demo")  # registered target, no strategy here
+    assert err.value.failure_phrase == "target_header_mismatch"
+    with pytest.raises(KernelCodeError) as err:
+        get_compile_strategy("not_a_target")
+    assert err.value.failure_phrase == "target_header_mismatch"
+    with pytest.raises(KernelCodeError) as err:
+        register_compile_strategy("gfx950", Gfx950CompileStrategy())
+    assert err.value.failure_phrase == "compile_failed"  # duplicate without override
+
+
+def test_every_demo_has_a_pattern():
+    names = set(known_patterns())
+    for fn in ALL_DEMOS:
+        assert fn.__name__ in names
+        with pytest.raises(KernelCodeError):
+            fn(None, None, None, None) if fn.__code__.co_argcount == 4 else fn(*([None] * fn.__code__.co_argcount))
+
+
+@pytest.mark.parametrize("fn", ALL_DEMOS, ids=lambda f: f.__name__)
+def test_generated_sources(fn):
+    lowered, source = run_lowering_demo("case", fn)
+    assert source.startswith("// __KG_BUNDLE_FILE__:kernel.hip")
+    assert 'extern "C" int kg_execute_entry(const KgArgSlot* ordered_args, unsigned long long arg_count)' in source
+    assert lowered.pattern.library_entry in source
+    assert f"arg_count != {len(lowered.pattern.params)}ULL" in source
+    assert lowered.hardware["subthread_num"] == 64
+    files = unbundle(source)
+    assert set(files) == {"kernel.hip"}
+
+
+def test_static_demo_constants_are_baked():
+    src = gen_kernel(recognise(conv2d_inputs_static_tile_static_kernel))
+    # stride 8 and the seeded pads/tiles of kernel/conv2d/inputs_static_tile_static.py
+    assert "slots[4].int_value = 8LL;" in src and "slots[5].int_value = 8LL;" in src
+    p = recognise(conv2d_inputs_static_tile_static_kernel)
+    baked = dict(p.baked)
+    assert (baked["pad_top"], baked["pad_bottom"], baked["pad_left"], baked["pad_right"]) == (3, 3, 4, 0)
+    assert (baked["tile_f"], baked["tile_c"], baked["tile_n"], baked["tile_ho"], baked["tile_wo"]) == (7, 18, 3, 9, 8)
+    mm = dict(recognise(matmul_inputs_static_tile_static_kernel).baked)
+    assert (mm["tile_m"], mm["tile_n"], mm["tile_k"]) == (48, 80, 56)
+    fa = gen_kernel(recognise(flash_attention_scaled_causal_kernel, "bfloat16"))
+    assert "slots[7].int_value = 1LL;" in fa  # causal flag appended after the scale slot
+
+
+def test_allow_absent_metadata_roundtrip():
+    src = gen_kernel(recognise(matmul_inputs_static_tile_static_kernel))
+    specs = parse_allow_absent(src)
+    assert len(specs) == 1 and specs[0].index == 3 and specs[0].dtype == "float32" and specs[0].rank == 1
+    with pytest.raises(KernelCodeError) as err:
+        validate_args((1, 2, None), ())
+    assert err.value.failure_phrase == "runtime_throw_or_abort"
+
+
+def test_pipeline_registry_and_options():
+    assert get_pipeline("gfx950-lowering").name == "gfx950-lowering"
+    with pytest.raises(KernelCodeError):
+        build_gfx950_lowering_pipeline({"target": "cuda_sm89"})
+    with pytest.raises(KernelCodeError):
+        build_gfx950_lowering_pipeline({"fold": "true"})
+
+
+@pytest.mark.parametrize(
+    "bad",
+    [
+        "// __KG_BUNDLE_FILE__:../escape.hip\nint x;",
+        "// __KG_BUNDLE_FILE__:/abs.hip\nint x;",
+        "// __KG_BUNDLE_FILE__:kernel.hip\nint x;\n// __KG_BUNDLE_FILE__:kernel.hip\nint y;",
+        "// __KG_BUNDLE_FILE__:other.hip\nint x;",
+    ],
+)
+def test_malformed_bundles(bad):
+    with pytest.raises(KernelCodeError) as err:
+        unbundle(bad)
+    assert err.value.failure_phrase == "source_empty_or_invalid"
+
+
+def test_engine_rejects_empty_source():
+    with pytest.raises(KernelCodeError) as err:
+        ExecutionEngine("gfx950").compile(source="   ", function="f")
+    assert err.value.failure_phrase == "source_empty_or_invalid"
+
+
+def _fake_hipcc(tmp_path: Path, rc: int = 0) -> Path:
+    log = tmp_path / "argv.log"
+    script = tmp_path / "fake-hipcc"
+    script.write_text(
+        "#!/bin/bash\n"
+        f'echo "$@" >> {log}\n'
+        'out=""; prev=""; for a in "$@"; do if [ "$prev" = "-o" ]; then out="$a"; fi; prev="$a"; done\n'
+        f'if [ {rc} -ne 0 ]; then echo "fake failure" >&2; exit {rc}; fi\n'
+        'touch "$out"\n'
+    )
+    script.chmod(script.stat().st_mode | stat.S_IEXEC)
+    return script
+
+
+def test_fake_compiler_command_line(tmp_path):
+    fake = _fake_hipcc(tmp_path)
+    src = gen_kernel(recognise(matmul_inputs_static_tile_dynamic_kernel))
+    kernel = ExecutionEngine("gfx950", compiler=str(fake)).compile(source=src, function="matmul")
+    argv = (tmp_path / "argv.log").read_text()
+    assert "--offload-arch=gfx950" in argv and "-shared" in argv and "-fPIC" in argv and "-std=c++17" in argv
+    assert "kernel.hip" in argv and "libkg_gfx950.so" in argv and "-Wl,-rpath," in argv
+    assert kernel.target == "gfx950" and kernel.entry_point == "kg_execute_entry"
+    work = Path(kernel.soname_path).parent
+    assert work.is_dir()
+    kernel.close()
+    assert not work.exists()
+    kernel.close()  # idempotent
+
+
+def test_fake_compiler_failure_phrase(tmp_path):
+    fake = _fake_hipcc(tmp_path, rc=3)
+    with pytest.raises(KernelCodeError) as err:
+        ExecutionEngine("gfx950", compiler=str(fake)).compile(source="int x;", function="f")
+    assert err.value.failure_phrase == "compile_failed"
+
+
+def test_real_hipcc_builds_generated_source():
+    """hipcc cross-compiles the generated glue for gfx950 here (no GPU needed) and the
+    shared object exports kg_execute_entry; it is loaded but not executed."""
+
+    src = gen_kernel(recognise(flash_attention_inputs_static_tile_static_kernel))
+    kernel = ExecutionEngine("gfx950").compile(source=src, function="fa")
+    try:
+        lib = ctypes.CDLL(kernel.soname_path)
+        assert hasattr(lib, "kg_execute_entry")
+        fn = lib.kg_execute_entry
+        fn.restype = ctypes.c_int
+        fn.argtypes = [ctypes.POINTER(native.KgArgSlot), ctypes.c_ulonglong]
+        slots = (native.KgArgSlot * 3)()
+        assert fn(slots, 3) == -1  # arity check in the generated shim, before any GPU work
+    finally:
+        kernel.close()
+
+
+def test_execute_phrases_without_gpu(tmp_path):
+    fake = _fake_hipcc(tmp_path)
+    kernel = ExecutionEngine("gfx950", compiler=str(fake)).compile(source="int x;", function="f")
+    with pytest.raises(KernelCodeError) as err:
+        kernel.execute(args=None)
+    assert err.value.failure_phrase == "runtime_throw_or_abort"
+    with pytest.raises(KernelCodeError) as err:
+        kernel.execute(args=[1])
+    assert err.value.failure_phrase == "runtime_throw_or_abort"
+    with pytest.raises(KernelCodeError) as err:
+        kernel.execute(args=(), entry_point="other")
+    assert err.value.failure_phrase == "symbol_resolve_failed"
+    with pytest.raises(KernelCodeError) as err:
+        kernel.execute(request=ExecuteRequest(args=(), capture_function_output=True))
+    assert err.value.failure_phrase == "function_output_capture_not_supported"
+    other = CompiledKernel(target="npu_demo", soname_path=kernel.soname_path, function="f", entry_point="kg_execute_entry")
+    with pytest.raises(KernelCodeError) as err:
+        other.execute(args=())
+    assert err.value.failure_phrase == "execution_unsupported"
+    kernel.close()
+
+
+def test_dsl_run_contract_checks():
+    snap = snapshot_config()
+    try:
+        set_target("npu_demo")
+        with pytest.raises(KernelCodeError):
+            dsl_run(matmul_inputs_static_tile_static_kernel, (1, 2, 3, None), "gfx950-lowering")
+        set_target("gfx950")
+        with pytest.raises(KernelCodeError):
+            dsl_run(matmul_inputs_static_tile_static_kernel, (1, 2, 3), "gfx950-lowering")  # arity
+        with pytest.raises(KernelCodeError):
+            dsl_run(matmul_inputs_static_tile_static_kernel, (1, 2, 3, None), "no-such-pipeline")
+    finally:
+        restore_config(snap)
