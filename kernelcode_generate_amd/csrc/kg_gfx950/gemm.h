@@ -1,10 +1,12 @@
 // GEMM kernels for the matmul demos: out[M,N] = lhs[M,K] @ rhs[K,N] (+ bias[N]),
 // row-major, fp32 accumulation.
 //
-// gemm_mfma_kernel: bf16/f16 operands on gfx950 MFMA (v_mfma_f32_16x16x32_{bf16,f16}).
-//   Macro tile 256x256x64, 256 threads = 4 waves in a 2x2 layout, 128x128 per wave
-//   (8x8 MFMA blocks, 256 fp32 accumulators per lane). LDS double buffer, 2 x 64 KiB.
-//   lhs tiles are K-contiguous in HBM and land in LDS as [m][k]; rhs tiles are
+// gemm_mfma_kernel: bf16/f16 operands on gfx950 MFMA (v_mfma_f32_32x32x16_{bf16,f16}; the
+//   32x32x16 form is the one that reaches full matrix-core rate on gfx950, the 16x16x32
+//   form issues at half of it). Macro tile 256x256x64, 256 threads = 4 waves in a 2x2
+//   layout, 128x128 per wave (4x4 MFMA blocks, 256 fp32 accumulators per lane). LDS
+//   double buffer, 2 x 64 KiB. lhs tiles are K-contiguous in HBM and land in LDS as [m][k]
+//   (aligned shapes: global_load_lds_dwordx4 straight into LDS, no registers); rhs tiles are
 //   N-contiguous, so each thread loads an 8(k) x 8(n) block with 16-byte loads and
 //   transposes it in registers (v_perm_b32) before writing [n][k] rows to LDS. Both LDS
 //   arrays use 128-byte rows whose 16-byte chunks are XOR-swizzled so that the MFMA
@@ -49,7 +51,7 @@ __global__ __launch_bounds__(gemm::kThreads, 1) void gemm_mfma_kernel(
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1;
   const int wn = wave & 1;
 
@@ -68,10 +70,13 @@ __global__ __launch_bounds__(gemm::kThreads, 1) void gemm_mfma_kernel(
   const int m0 = tm * kBM;
   const int n0 = tn * kBN;
 
-  // Global load assignment.
-  // lhs: 8 loads per thread, row = i*32 + tid/8, chunk = tid%8.
+  // lhs, masked path: 8 register loads per thread, row = i*32 + tid/8, chunk = tid%8.
   const int a_row = tid >> 3;
   const int a_chunk = tid & 7;
+  // lhs, aligned path: 8 direct HBM->LDS copies per wave; slab s = 8 rows x 8 chunks, lane l
+  // fetches the chunk that the swizzle places at LDS slot s*64 + l.
+  const int d_row = lane >> 3;
+  const int d_pc = lane & 7;
   // rhs: one 8x8 block per thread: n-block nb = tid%32, k-block kb = tid/32.
   const int b_nb = tid & 31;
   const int b_kb = tid >> 5;
@@ -79,19 +84,25 @@ __global__ __launch_bounds__(gemm::kThreads, 1) void gemm_mfma_kernel(
   const uint16_t* a_ptr = A + (long long)(m0 + a_row) * lda + a_chunk * 8;
   const uint16_t* b_ptr = B + (long long)(b_kb * 8) * ldb + n0 + b_nb * 8;
 
-  u32x4 a_pref[8];
+  u32x4 a_pref[kMasked ? 8 : 1];
   u32x4 b_pref[8];
 
-  auto load_tile = [&](int kt) {
+  auto load_tile = [&](int kt, int buf) {
     const int k0 = kt * kBK;
+    if constexpr (kMasked) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if constexpr (kMasked) {
+      for (int i = 0; i < 8; ++i) {
         const int m = m0 + i * 32 + a_row;
         const int k = k0 + a_chunk * 8;
         a_pref[i] = (m < M && k < K) ? ld16(a_ptr + (long long)i * 32 * lda + k0) : u32x4{0, 0, 0, 0};
-      } else {
-        a_pref[i] = ld16(a_ptr + (long long)i * 32 * lda + k0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int slab = wave * 8 + i;
+        const int row = slab * 8 + d_row;
+        const uint16_t* src = A + (long long)(m0 + row) * lda + k0 + 8 * (d_pc ^ (row & 7));
+        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)&lds[buf][0][slab * 64], 16, 0, 0);
       }
     }
 #pragma unroll
@@ -107,10 +118,12 @@ __global__ __launch_bounds__(gemm::kThreads, 1) void gemm_mfma_kernel(
   };
 
   auto store_tile = [&](int buf) {
+    if constexpr (kMasked) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int row = i * 32 + a_row;
-      lds[buf][0][swz_a(row, a_chunk)] = a_pref[i];
+      for (int i = 0; i < 8; ++i) {
+        const int row = i * 32 + a_row;
+        lds[buf][0][swz_a(row, a_chunk)] = a_pref[i];
+      }
     }
     u32x4 bt[8];
     transpose8x8_b16(b_pref, bt);
@@ -121,70 +134,365 @@ __global__ __launch_bounds__(gemm::kThreads, 1) void gemm_mfma_kernel(
     }
   };
 
-  f32x4 acc[8][8];
+  // 32x32 blocks: acc[i][j] covers rows wm*128 + 32i .., cols wn*128 + 32j ..
+  f32x16 acc[4][4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
   const int ktiles = (K + kBK - 1) / kBK;
-  load_tile(0);
+  load_tile(0, 0);
   store_tile(0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
-  const int frag_row = lane & 15;
-  const int frag_chunk = lane >> 4;
+  const int frag_row = lane & 31;
+  const int frag_half = lane >> 5;
 
   for (int kt = 0; kt < ktiles; ++kt) {
     const int cur = kt & 1;
-    if (kt + 1 < ktiles) load_tile(kt + 1);
+    if (kt + 1 < ktiles) load_tile(kt + 1, cur ^ 1);
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const int c = kk * 4 + frag_chunk;
-      u32x4 af[8];
-      u32x4 bf[8];
+    for (int ks = 0; ks < kBK / 16; ++ks) {
+      const int c = 2 * ks + frag_half;
+      u32x4 af[4];
+      u32x4 bf[4];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) af[i] = lds[cur][0][swz_a(wm * 128 + i * 16 + frag_row, c)];
+      for (int i = 0; i < 4; ++i) af[i] = lds[cur][0][swz_a(wm * 128 + i * 32 + frag_row, c)];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) bf[j] = lds[cur][1][swz_b(wn * 128 + j * 16 + frag_row, c)];
+      for (int j = 0; j < 4; ++j) bf[j] = lds[cur][1][swz_b(wn * 128 + j * 32 + frag_row, c)];
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = H::mfma16(bf[j], af[i], acc[i][j]);
+        for (int j = 0; j < 4; ++j) acc[i][j] = H::mfma32(bf[j], af[i], acc[i][j]);
     }
     if (kt + 1 < ktiles) store_tile(cur ^ 1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
   }
 
-  // Epilogue: lane owns C[m][n..n+3] of every 16x16 block.
+  // Epilogue: the MFMA ran as C^T = B^T A^T, so lane l holds C[m][n..n+3] with
+  // m = row block + l%32 and n = col block + 8q + 4*(l/32), q = 0..3.
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int m = m0 + wm * 128 + i * 16 + frag_row;
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + wm * 128 + i * 32 + frag_row;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int n = n0 + wn * 128 + j * 16 + frag_chunk * 4;
-      f32x4 v = acc[i][j];
-      if constexpr (kBias == 1) {
-        const float* bp = static_cast<const float*>(bias);
-        if (!kMasked || n < N) {
-          v[0] += bp[n];
-          v[1] += bp[n + 1];
-          v[2] += bp[n + 2];
-          v[3] += bp[n + 3];
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + wn * 128 + j * 32 + 8 * q + 4 * frag_half;
+        float v0 = acc[i][j][4 * q], v1 = acc[i][j][4 * q + 1], v2 = acc[i][j][4 * q + 2], v3 = acc[i][j][4 * q + 3];
+        if constexpr (kBias == 1) {
+          const float* bp = static_cast<const float*>(bias);
+          if (!kMasked || n < N) {
+            v0 += bp[n];
+            v1 += bp[n + 1];
+            v2 += bp[n + 2];
+            v3 += bp[n + 3];
+          }
+        } else if constexpr (kBias == 2) {
+          const uint16_t* bp = static_cast<const uint16_t*>(bias);
+          if (!kMasked || n < N) {
+            v0 += H::to_float(bp[n]);
+            v1 += H::to_float(bp[n + 1]);
+            v2 += H::to_float(bp[n + 2]);
+            v3 += H::to_float(bp[n + 3]);
+          }
         }
-      } else if constexpr (kBias == 2) {
-        const uint16_t* bp = static_cast<const uint16_t*>(bias);
-        if (!kMasked || n < N) {
-          v[0] += H::to_float(bp[n]);
-          v[1] += H::to_float(bp[n + 1]);
-          v[2] += H::to_float(bp[n + 2]);
-          v[3] += H::to_float(bp[n + 3]);
-        }
+        u32x2 packed;
+        packed[0] = H::pack2(v0, v1);
+        packed[1] = H::pack2(v2, v3);
+        if (!kMasked || (m < M && n < N)) st8(C + (long long)m * ldc + n, packed);
       }
-      u32x2 packed;
-      packed[0] = pack16(H::from_float(v[0]), H::from_float(v[1]));
-      packed[1] = pack16(H::from_float(v[2]), H::from_float(v[3]));
-      if (!kMasked || (m < M && n < N)) st8(C + (long long)m * ldc + n, packed);
+    }
+  }
+}
+
+// gemm_pipe_kernel: the aligned-shape path (M % 256 == 0, N % 256 == 0, K % 32 == 0).
+//   Same 256x256 tile and 2x2 waves of 128x128 with 32x32x16 MFMAs, but both operands are
+//   copied HBM -> LDS by global_load_lds_dwordx4 (no registers, no VALU work) through a
+//   4-stage ring of 32-deep K slices (4 x 32 KiB), so loads are issued three slices ahead
+//   of their use. lhs slices are [m][k] rows of 64 bytes; rhs slices stay [k][n] as in HBM
+//   and the MFMA operand (8 consecutive k of one n) is read with two ds_read_b64_tr_b16:
+//   within each 16-lane group, lane j addresses 4 consecutive n of k-row j/4 and lane i
+//   receives k-rows 0..3 of column i. Chunk swizzles: lhs p = c ^ ((row >> 2) & 3),
+//   rhs p = c ^ 4(k & 3) -- the fragment reads hit distinct banks of the 64-bank LDS.
+//   Fragments are double-buffered in registers: while the MFMAs of one 16-deep half of a
+//   slice run, the other half (or the next slice's first half) is being read, and the
+//   per-slice barrier sits between the two halves.
+namespace gemmp {
+constexpr int kBM = 256;
+constexpr int kBN = 256;
+constexpr int kBK = 32;
+constexpr int kStages = 4;
+constexpr int kThreads = 256;
+constexpr int kAVecs = kBM * kBK / 8;  // 1024 u32x4 per lhs stage
+constexpr int kBVecs = kBK * kBN / 8;  // 1024 u32x4 per rhs stage
+// LDS has 64 banks of 4 bytes: ds_read_b128 serves 16 lanes per cycle, 64-bit reads 32.
+// The swizzles are XOR masks, so the same mask maps an LDS slot back to its HBM chunk.
+__device__ __forceinline__ int a_mask(int row) { return (row >> 2) & 3; }
+__device__ __forceinline__ int b_mask(int k) { return 4 * (k & 3); }
+__device__ __forceinline__ int a_slot(int row, int c) { return row * 4 + (c ^ a_mask(row)); }
+__device__ __forceinline__ int b_slot(int k, int c) { return k * 32 + (c ^ b_mask(k)); }
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+template <int S>
+struct StageIdx {
+  static constexpr int value = S;
+};
+}  // namespace gemmp
+
+// Wait until at most N of this wave's vector-memory ops (including HBM->LDS copies) are
+// outstanding and all of its LDS ops are done, then meet the other waves. The copies are
+// issued through inline asm (g2lds16), so the compiler neither tracks nor waits for them;
+// these explicit waits are the only synchronisation, and the empty asm statements keep
+// LDS reads from being moved across the barrier.
+template <int N>
+__device__ __forceinline__ void wait_and_barrier() {
+  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  else if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
+  else if constexpr (N == 16) asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)" ::: "memory");
+  else if constexpr (N == 24) asm volatile("s_waitcnt vmcnt(24) lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// 16 bytes per lane HBM -> LDS: lane l's data lands at LDS byte lds_base + 16*l
+// (lds_base must be wave-uniform; it goes through M0).
+__device__ __forceinline__ void g2lds16(const void* gptr, const void* lds_base) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_base;
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, off"
+      :
+      : "v"(gptr), "s"(m0)
+      : "memory", "m0");
+}
+
+// 16 bytes per lane HBM -> LDS with a wave-uniform 64-bit base (SGPRs) and a per-lane
+// 32-bit byte offset: lane l's data lands at LDS byte m0 + 16*l.
+__device__ __forceinline__ void g2lds16_s(uint32_t voff, const void* sbase, uint32_t m0) {
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %1"
+      :
+      : "v"(voff), "s"(sbase), "s"(m0)
+      : "memory", "m0");
+}
+
+template <typename Tag, int kBias>
+__global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
+    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, uint16_t* __restrict__ C,
+    const void* __restrict__ bias, int M, int N, int K, long long lda, long long ldb, long long ldc) {
+  using namespace gemmp;
+  using H = Half16<Tag>;
+  __shared__ u32x4 lds_a[kStages][kAVecs];
+  __shared__ u32x4 lds_b[kStages][kBVecs];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1;
+  const int wn = wave & 1;
+
+  const int tiles_n = N / kBN;
+  const int tiles_m = M / kBM;
+  const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
+  constexpr int kGroupM = 4;
+  const int group_size = kGroupM * tiles_n;
+  const int group = logical / group_size;
+  const int first_m = group * kGroupM;
+  const int gm = min(tiles_m - first_m, kGroupM);
+  const int in_group = logical - group * group_size;
+  const int m0 = (first_m + in_group % gm) * kBM;
+  const int n0 = (in_group / gm) * kBN;
+
+  // ---- HBM -> LDS copies ----
+  // Copy piece p < 4: lhs rows (wave*4+p)*16 + lane/4; the swizzle mask of a row depends on
+  // row>>2 & 3 only, so all four pieces share one per-lane offset and differ by 16 rows.
+  // Copy piece 4+p: rhs k-rows (wave*4+p)*2 + lane/32; the mask depends on k & 3, so pieces
+  // 0/2 and 1/3 share offsets and differ by 4 k-rows.
+  const int a_row0 = wave * 64 + (lane >> 2);
+  const uint32_t a_goff = (uint32_t)((a_row0 * lda + 8 * ((lane & 3) ^ a_mask(a_row0))) * 2);
+  uint32_t b_goff[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int k = (wave * 4 + i) * 2 + (lane >> 5);
+    b_goff[i] = (uint32_t)((k * ldb + 8 * ((lane & 31) ^ b_mask(k))) * 2);
+  }
+  const char* a_tile = reinterpret_cast<const char*>(A + (long long)m0 * lda);
+  const char* b_tile = reinterpret_cast<const char*>(B + n0);
+  const long long a_piece = 16 * lda * 2;
+  const long long b_piece = 4 * ldb * 2;
+  const long long b_step = (long long)kBK * ldb * 2;
+  const uint32_t lds_a0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)&lds_a[0][0];
+  const uint32_t lds_b0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)&lds_b[0][0];
+  constexpr uint32_t kStageBytes = kAVecs * 16;  // == kBVecs * 16
+
+  auto issue_piece = [&](int kt, int s, int piece) {  // piece 0..7: 4 lhs then 4 rhs
+    if (piece < 4) {
+      g2lds16_s(a_goff, a_tile + (long long)kt * kBK * 2 + piece * a_piece,
+                lds_a0 + s * kStageBytes + (wave * 4 + piece) * 1024);
+    } else {
+      const int i = piece - 4;
+      g2lds16_s(b_goff[i & 1], b_tile + kt * b_step + (i >> 1) * b_piece,
+                lds_b0 + s * kStageBytes + (wave * 4 + i) * 1024);
+    }
+  };
+
+  // ---- fragment reads ----
+  // lhs block i is 32 rows below block 0 (same mask): +2048 bytes; rhs k-rows +4 (t) and
+  // +16 (ks) keep the mask: +2048 / +8192 bytes. Per-lane byte addresses, LDS base included.
+  const int frag_row = lane & 31;
+  const int frag_half = lane >> 5;
+  const int g = lane >> 4;
+  const int j16 = lane & 15;
+  const int b_nofs = 16 * (g & 1) + 4 * (j16 & 3);
+  const int b_kofs = 8 * (g >> 1) + (j16 >> 2);
+  uint32_t a_rd[2], b_rd[4];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) a_rd[ks] = lds_a0 + a_slot(wm * 128 + frag_row, 2 * ks + frag_half) * 16;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int n = wn * 128 + j * 32 + b_nofs;
+    b_rd[j] = lds_b0 + b_slot(b_kofs, n >> 3) * 16 + (n & 7) * 2;
+  }
+
+  struct Frag {
+    u32x4 a[4];
+    u32x4 b[4];
+  };
+  // read #r (0..11) of a fragment set: 4 lhs b128 reads, then 8 rhs transposed reads
+  auto read_piece = [&](int s, int ks, Frag& f, int r) {
+    if (r < 4) {
+      f.a[r] = *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(a_rd[ks] + s * kStageBytes + r * 2048);
+    } else {
+      const int j = (r - 4) >> 1, t = (r - 4) & 1;
+      const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4*)(uintptr_t)(b_rd[j] + s * kStageBytes + t * 2048 + ks * 8192));
+      const u32x2 w = __builtin_bit_cast(u32x2, v);
+      f.b[j][2 * t] = w[0];
+      f.b[j][2 * t + 1] = w[1];
+    }
+  };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  const int ktiles = K / kBK;
+#pragma unroll
+  for (int st = 0; st < kStages; ++st)
+    if (st < ktiles)
+#pragma unroll
+      for (int piece = 0; piece < 8; ++piece) issue_piece(st, st, piece);
+  {
+    const int younger = min(kStages - 1, ktiles - 1);
+    if (younger >= 3) wait_and_barrier<24>();
+    else if (younger == 2) wait_and_barrier<16>();
+    else if (younger == 1) wait_and_barrier<8>();
+    else wait_and_barrier<0>();
+  }
+  Frag f0, f1;
+#pragma unroll
+  for (int r = 0; r < 12; ++r) read_piece(0, 0, f0, r);
+
+  // One 32-deep slice in stage S: MFMAs of half 0 with the reads of half 1 slotted in
+  // between, barrier, MFMAs of half 1 with the next slice's first reads and this stage's
+  // refill copies slotted in between. kSteady: more slices follow and a refill is due.
+  auto slice = [&](int kt, auto stage_tag, auto steady_tag) {
+    constexpr int S = decltype(stage_tag)::value;
+    constexpr bool kSteady = decltype(steady_tag)::value != 0;
+#pragma unroll
+    for (int idx = 0; idx < 16; ++idx) {
+      const int i = idx >> 2, j = idx & 3;
+      acc[i][j] = H::mfma32(f0.b[j], f0.a[i], acc[i][j]);
+      if (idx < 12) read_piece(S, 1, f1, idx);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const bool more = kSteady || kt + 1 < ktiles;
+    const bool refill = kSteady || kt + kStages < ktiles;
+    if (kSteady) {
+      wait_and_barrier<16>();
+    } else if (more) {
+      const int younger = min(kStages - 2, ktiles - 2 - kt);
+      if (younger >= 2) wait_and_barrier<16>();
+      else if (younger == 1) wait_and_barrier<8>();
+      else wait_and_barrier<0>();
+    }
+    if (kSteady) {
+#pragma unroll
+      for (int idx = 0; idx < 16; ++idx) {
+        const int i = idx >> 2, j = idx & 3;
+        acc[i][j] = H::mfma32(f1.b[j], f1.a[i], acc[i][j]);
+        if (idx < 12) read_piece((S + 1) % kStages, 0, f0, idx);
+        if (idx >= 4 && idx < 12) issue_piece(kt + kStages, S, idx - 4);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+      if (refill)
+#pragma unroll
+        for (int piece = 0; piece < 8; ++piece) issue_piece(kt + kStages, S, piece);
+      if (more)
+#pragma unroll
+        for (int r = 0; r < 12; ++r) read_piece((S + 1) % kStages, 0, f0, r);
+#pragma unroll
+      for (int idx = 0; idx < 16; ++idx) {
+        const int i = idx >> 2, j = idx & 3;
+        acc[i][j] = H::mfma32(f1.b[j], f1.a[i], acc[i][j]);
+      }
+    }
+  };
+
+  int kt = 0;
+  for (; kt + 2 * kStages <= ktiles; kt += kStages) {  // every slice refills its stage
+    slice(kt, StageIdx<0>{}, StageIdx<1>{});
+    slice(kt + 1, StageIdx<1>{}, StageIdx<1>{});
+    slice(kt + 2, StageIdx<2>{}, StageIdx<1>{});
+    slice(kt + 3, StageIdx<3>{}, StageIdx<1>{});
+  }
+  for (; kt < ktiles; kt += kStages) {
+    slice(kt, StageIdx<0>{}, StageIdx<0>{});
+    if (kt + 1 < ktiles) slice(kt + 1, StageIdx<1>{}, StageIdx<0>{});
+    if (kt + 2 < ktiles) slice(kt + 2, StageIdx<2>{}, StageIdx<0>{});
+    if (kt + 3 < ktiles) slice(kt + 3, StageIdx<3>{}, StageIdx<0>{});
+  }
+
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + wm * 128 + i * 32 + frag_row;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + wn * 128 + j * 32 + 8 * q + 4 * frag_half;
+        float v0 = acc[i][j][4 * q], v1 = acc[i][j][4 * q + 1], v2 = acc[i][j][4 * q + 2], v3 = acc[i][j][4 * q + 3];
+        if constexpr (kBias == 1) {
+          const float* bp = static_cast<const float*>(bias);
+          v0 += bp[n];
+          v1 += bp[n + 1];
+          v2 += bp[n + 2];
+          v3 += bp[n + 3];
+        } else if constexpr (kBias == 2) {
+          const uint16_t* bp = static_cast<const uint16_t*>(bias);
+          v0 += H::to_float(bp[n]);
+          v1 += H::to_float(bp[n + 1]);
+          v2 += H::to_float(bp[n + 2]);
+          v3 += H::to_float(bp[n + 3]);
+        }
+        u32x2 packed;
+        packed[0] = H::pack2(v0, v1);
+        packed[1] = H::pack2(v2, v3);
+        st8(C + (long long)m * ldc + n, packed);
+      }
     }
   }
 }

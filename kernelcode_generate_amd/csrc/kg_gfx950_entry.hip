@@ -196,6 +196,16 @@ int launch_gemm_mfma(const Mem& out, const Mem& lhs, const Mem& rhs, const Mem& 
 #define KG_GEMM_LAUNCH(MASKED, BIAS)                                                                     \
   hipLaunchKernelGGL((gemm_mfma_kernel<Tag, MASKED, BIAS>), dim3(tiles), dim3(gemm::kThreads), 0, g_stream, A, \
                      B, C, bp, M, N, K, lda, ldb, ldc)
+  if (!masked && K % gemmp::kBK == 0) {
+#define KG_GEMM_PIPE(BIAS)                                                                                     \
+  hipLaunchKernelGGL((gemm_pipe_kernel<Tag, BIAS>), dim3(tiles), dim3(gemmp::kThreads), 0, g_stream, A, B, C, bp, M, N, \
+                     K, lda, ldb, ldc)
+    if (bias_kind == 0) KG_GEMM_PIPE(0);
+    else if (bias_kind == 1) KG_GEMM_PIPE(1);
+    else KG_GEMM_PIPE(2);
+#undef KG_GEMM_PIPE
+    return finish_launch("matmul(mfma-pipe)");
+  }
   if (masked) {
     if (bias_kind == 0) KG_GEMM_LAUNCH(true, 0);
     else if (bias_kind == 1) KG_GEMM_LAUNCH(true, 1);
