@@ -124,10 +124,14 @@ def cpu_baseline_matmul(rows: int = 384):
     }
 
 
-def secondary(dev, steps: int, warmup: int):
+SECONDARY_KEYS = ("c1", "c2s", "c3", "c4", "c5d128", "c5d64")
+
+
+def secondary(dev, steps: int, warmup: int, only=None):
     import torch
 
     out = []
+    keys = set(SECONDARY_KEYS if only is None else only)
 
     def add(name, flop, call, peak, nsteps, byts=None):
         wall, ev = time_steps(call, nsteps, max(2, warmup // 2))
@@ -142,17 +146,39 @@ def secondary(dev, steps: int, warmup: int):
         out.append(rec)
 
     # C1 fp32 256^3
+    if "c1" in keys:
+        c1(dev, add, steps)
+    if "c2s" in keys:
+        c2s(dev, add, steps)
+    if "c3" in keys:
+        c3(dev, add, steps)
+    if "c4" in keys:
+        c4(dev, add, steps)
+    for d, key in ((128, "c5d128"), (64, "c5d64")):
+        if key in keys:
+            c5(dev, add, steps, d)
+    return out
+
+
+def c1(dev, add, steps):
+    import torch
+
     g = torch.Generator(device=dev).manual_seed(20261201)
     a = torch.rand(256, 256, generator=g, device=dev) * 2 - 1
     b = torch.rand(256, 256, generator=g, device=dev) * 2 - 1
     c = torch.empty(256, 256, device=dev)
     add("C1 fp32 matmul 256^3", 2 * 256**3, PreparedCall("kg_gfx950_matmul_entry", (c, a, b, None)), PEAK_FP32_TFLOPS, steps)
-    # C2' skinny
+
+
+def c2s(dev, add, steps):
     a, b, c = gemm_workload(dev, 8192, 1024, 4096, 20261203)
     add("C2' bf16 matmul M=8192 N=1024 K=4096", 2 * 8192 * 1024 * 4096,
         PreparedCall("kg_gfx950_matmul_entry", (c, a, b, None)), PEAK_BF16_TFLOPS, steps)
-    del a, b, c
-    # C3 conv2d fp16
+
+
+def c3(dev, add, steps):
+    import torch
+
     g = torch.Generator(device=dev).manual_seed(20261204)
     x = torch.randn(32, 64, 56, 56, generator=g, device=dev).to(torch.float16)
     bound = math.sqrt(6.0 / 576.0)
@@ -162,25 +188,29 @@ def secondary(dev, steps: int, warmup: int):
     add("C3 fp16 conv2d N=32 C=64 H=W=56 F=64 3x3 s1 p1", 2 * 32 * 64 * 56 * 56 * 64 * 9,
         PreparedCall("kg_gfx950_conv2d_entry", (y, x, w, None, 1, 1, 1, 1, 1, 1, 1, 1)), PEAK_BF16_TFLOPS,
         max(steps, 50), conv_bytes)
-    del x, w, y
-    # C4 flash attention non-causal
+
+
+def c4(dev, add, steps):
+    import torch
+
     g = torch.Generator(device=dev).manual_seed(20261205)
     q, k, v = (torch.randn(4, 32, 2048, 128, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
     o = torch.empty_like(q)
     add("C4 bf16 flash-attn fwd B=4 H=32 S=2048 D=128 non-causal", 4 * 4 * 32 * 2048 * 2048 * 128,
         PreparedCall("kg_gfx950_flash_attention_entry", (o, q, k, v, 128, 64, 1.0 / math.sqrt(128.0), 0)),
         PEAK_BF16_TFLOPS, steps)
-    del q, k, v, o
-    # C5 flash attention causal
-    for d, seed in ((128, 20261206), (64, 20261207)):
-        g = torch.Generator(device=dev).manual_seed(seed)
-        q, k, v = (torch.randn(1, 32, 16384, d, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
-        o = torch.empty_like(q)
-        add(f"C5 bf16 flash-attn fwd B=1 H=32 S=16384 D={d} causal", 4 * 32 * 16384 * 16384 * d // 2,
-            PreparedCall("kg_gfx950_flash_attention_entry", (o, q, k, v, 128, 64, 1.0 / math.sqrt(d), 1)),
-            PEAK_BF16_TFLOPS, max(3, steps // 4))
-        del q, k, v, o
-    return out
+
+
+def c5(dev, add, steps, d):
+    import torch
+
+    seed = 20261206 if d == 128 else 20261207
+    g = torch.Generator(device=dev).manual_seed(seed)
+    q, k, v = (torch.randn(1, 32, 16384, d, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
+    o = torch.empty_like(q)
+    add(f"C5 bf16 flash-attn fwd B=1 H=32 S=16384 D={d} causal", 4 * 32 * 16384 * 16384 * d // 2,
+        PreparedCall("kg_gfx950_flash_attention_entry", (o, q, k, v, 128, 64, 1.0 / math.sqrt(d), 1)),
+        PEAK_BF16_TFLOPS, max(3, steps // 4))
 
 
 def main() -> int:
@@ -190,6 +220,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--only", nargs="+", choices=SECONDARY_KEYS,
+                    help="profiling aid: run only these secondary workloads (no headline GEMM, no CPU baseline)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (reference point for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -209,6 +241,10 @@ def main() -> int:
     native.load_library()
     stream = torch.cuda.current_stream()
     native.set_launch_mode(False, stream.cuda_stream)
+    if args.only:
+        print(json.dumps({"secondary": secondary(dev, args.steps, args.warmup, args.only)}), flush=True)
+        native.set_launch_mode(True, None)
+        return 0
 
     m = n = k = 4096
     a, b, c = gemm_workload(dev, m, n, k, 20261202)

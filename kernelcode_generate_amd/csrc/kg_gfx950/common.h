@@ -16,6 +16,7 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 // Element tags: the MFMA paths move 16-bit data as raw bits and only the MFMA
 // instruction and the final conversion depend on the format.
@@ -52,6 +53,11 @@ struct Half16<Bf16Tag> {
   static __device__ __forceinline__ uint32_t pack2(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
   }
+  // acc + (both halves of a packed pair), fp32 accumulate: v_dot2c_f32_bf16 with (1, 1).
+  static __device__ __forceinline__ float sum2(uint32_t packed, float acc) {
+    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, packed), one, acc, false);
+  }
 };
 
 template <>
@@ -74,6 +80,11 @@ struct Half16<F16Tag> {
   // Two floats -> two fp16 (RNE) in one dword: v_cvt_pk_f16_f32; `a` in the low half.
   static __device__ __forceinline__ uint32_t pack2(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
+  }
+  // acc + (both halves of a packed pair), fp32 accumulate: v_dot2c_f32_f16 with (1, 1).
+  static __device__ __forceinline__ float sum2(uint32_t packed, float acc) {
+    const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, packed), one, acc, false);
   }
 };
 
@@ -112,6 +123,24 @@ __device__ __forceinline__ void transpose8x8_b16(const u32x4 in[8], u32x4 out[8]
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 __device__ __forceinline__ void st8(void* p, u32x2 v) { *reinterpret_cast<u32x2*>(p) = v; }
+
+// Lane l and lane l ^ 32 combined, in every lane. v_permlane32_swap(a, b) swaps the high
+// half of a with the low half of b, so with a = b = x it returns x of the low half in
+// every lane (first result) and x of the high half in every lane (second result).
+// (The results are copied to scalars before any bit cast: __builtin_bit_cast of an
+// ext-vector element subscript reads element 0.)
+__device__ __forceinline__ float halves_max(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const uint32_t lo = r[0], hi = r[1];
+  return __builtin_elementwise_maximum(__builtin_bit_cast(float, lo), __builtin_bit_cast(float, hi));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const uint32_t lo = r[0], hi = r[1];
+  return __builtin_bit_cast(float, lo) + __builtin_bit_cast(float, hi);
+}
 
 // Wave64 butterfly reductions through ds_swizzle/ds_bpermute (via __shfl_xor).
 __device__ __forceinline__ float wave_max(float v) {

@@ -2,30 +2,43 @@
 // fp32 online softmax, optional scale and causal mask.
 //
 // Work split: one workgroup = 128 query rows of one (b,h), 4 waves x 32 queries; key/value
-// tiles of 64 keys are staged through LDS (double buffered) and shared by the 4 waves.
+// tiles of 64 keys are copied HBM -> LDS (two buffers each for K and V) and shared by the
+// four waves. Workgroup ids are dealt to the 8 XCDs round-robin; they are remapped so that
+// each XCD runs the query blocks of the same (b,h) together and its L2 serves their K/V.
 //
 // Per wave and key tile the kernel computes S^T = K Q^T with v_mfma_f32_32x32x16 (operand A
 // = 32 keys x 16 d from LDS, operand B = Q^T kept in registers for the whole kernel). In
 // the 32x32 MFMA result lane l holds column l%32 (one query) and rows {8j + 4(l/32) + r};
 // the K rows are read in the permuted order pi(8j + 4h + r) = 16h + 4j + r, so lane l ends
 // up with the scores of ITS query against 16 CONSECUTIVE keys (16h .. 16h+15 of the
-// 32-key block). The row max/sum are therefore lane-local plus one exchange with lane
-// l^32, and P (converted to 16-bit) is already laid out as the B operand of
-// O^T += V^T P^T: lane half h supplies keys 16h+8t .. 16h+8t+7 of MFMA t, which is one
-// 16-byte read of the transposed V tile. O^T keeps one query per lane column as well, so
-// the rescale by exp(m_old - m_new) is lane-local.
+// 32-key block). Row max/sum are lane-local plus one exchange with lane l^32
+// (v_permlane32_swap), and P (rounded to 16 bits) is already laid out as the B operand of
+// O^T += V^T P^T: lane half h supplies keys 16h+8t .. 16h+8t+7 of MFMA t. The V^T operand
+// (8 consecutive keys of one d per lane) comes from the key-major V tile through two
+// ds_read_b64_tr_b16: within each 16-lane group, lane j addresses 4 consecutive d of key
+// row j/4 and lane i receives key rows 0..3 of column i.
 //
 // Softmax works in base 2: p = exp2(s * scale*log2(e) - m) with m tracked in the same
-// units; exp2 is v_exp_f32. P is rounded to the input format before the PV product.
+// units (v_exp_f32). The running max is raised only when a tile's max exceeds it by more
+// than kRescaleSlack, so the O rescale is skipped on most tiles; numerator and denominator
+// use the same m, so the result does not depend on it. Row sums add the rounded P pairs
+// with v_dot2c_f32_{bf16,f16}: the same P values the PV product uses.
 //
-// K tiles are copied HBM -> LDS by global_load_lds_dwordx4 (no registers); each lane
-// fetches the 16-byte chunk that belongs at its LDS slot under the swizzle. V arrives
-// key-major; each thread loads a 4-key x 8-d block with 16-byte loads, transposes it in
-// registers (v_perm_b32) and writes d-major 8-byte pieces to LDS. Both LDS tiles use
-// XOR-swizzled 16-byte chunks so the fragment reads are bank-conflict free.
+// Software pipeline per wave, tile j (S(j) computed and its max known on entry):
+//   block 1: the S(j+1) MFMAs, with the exp/pack of 3/4 of S(j) and the K(j+1) fragment
+//            reads slotted between them;
+//   block 2: the PV(j) MFMAs, with the last quarter of softmax(j), the V(j) fragment reads
+//            and the max of S(j+1) slotted between them.
+// Copies of K(j+2) and V(j+1) are issued at the start of iteration j into the buffers that
+// iteration j-1 finished with; one wait + barrier ends the iteration.
+//
+// LDS chunk swizzles (16-byte chunks, 64 banks of 4 bytes; ds_read_b128 serves 16 lanes per
+// cycle, 64-bit reads 32): K chunk c of key row r sits at slot c ^ k_mask(r) and V chunk c
+// at c ^ v_mask(r). Each copy lane fetches the HBM chunk that belongs at its LDS slot.
 #pragma once
 
 #include "flash_attn.h"
+#include "lds_dma.h"
 
 namespace kg_gfx950 {
 
@@ -34,13 +47,51 @@ namespace fa {
 constexpr int kBM = 128;  // queries per workgroup
 constexpr int kBC = 64;   // keys per tile
 constexpr int kThreads = 256;
+// Running-max slack (log2 units): P <= 2^8 between rescales.
+constexpr float kRescaleSlack = 8.0f;
 
 // Row of the K tile that MFMA row r reads (see header comment).
-__device__ __forceinline__ int key_perm(int r) { return 16 * ((r >> 2) & 1) + 4 * (r >> 3) + (r & 3); }
-// 16-byte chunk swizzle of the K tile: distinct for each group of 8 MFMA rows.
-__device__ __forceinline__ int k_swz(int key) { return (key & 3) | ((key >> 2) & 4); }
-// 16-byte chunk swizzle of the V^T tile (8 key-chunks per d row).
-__device__ __forceinline__ int v_swz(int d) { return (d & 7) ^ ((d >> 3) & 7); }
+__host__ __device__ constexpr int key_perm(int r) { return 16 * ((r >> 2) & 1) + 4 * (r >> 3) + (r & 3); }
+// The 16 lanes of one b128 read cycle read keys pi(0..15) = {0-3, 16-19, 4-7, 20-23} (+8)
+// at the same chunk; D=128 rows are 256 bytes (one bank row), D=64 rows 128 bytes.
+template <int D>
+__host__ __device__ constexpr int k_mask(int key) {
+  return D == 128 ? ((key & 7) | ((key >> 1) & 8)) : (((key >> 1) & 3) | ((key >> 2) & 4));
+}
+// Transposed reads: the 32 lanes of a cycle read 4 key rows x two 32-byte pieces.
+template <int D>
+__host__ __device__ constexpr int v_mask(int key) {
+  return D == 128 ? 4 * (key & 3) : 4 * ((key >> 1) & 1);
+}
+
+// Copy instruction p of wave w covers tile rows (w*PW + p)*RPP + lane/DCH. Per-lane HBM
+// offsets are kept for p = 0 and 1 (K) or p = 0 (V); the other instructions move the
+// wave-uniform base by whole KiB, which needs the masks of their rows to repeat.
+template <int D>
+constexpr bool copy_masks_repeat() {
+  constexpr int RB = 2 * D, PW = kBC * RB / 1024 / 4, RPP = 1024 / RB, DCH = D / 8;
+  for (int w = 0; w < 4; ++w)
+    for (int lane = 0; lane < 64; ++lane)
+      for (int p = 0; p < PW; ++p) {
+        const int row = (w * PW + p) * RPP + lane / DCH;
+        if (k_mask<D>(row) != k_mask<D>((w * PW + (p & 1)) * RPP + lane / DCH)) return false;
+        if (v_mask<D>(row) != v_mask<D>((w * PW) * RPP + lane / DCH)) return false;
+      }
+  return true;
+}
+static_assert(copy_masks_repeat<128>() && copy_masks_repeat<64>(), "copy offsets");
+
+// Bijection of workgroup ids: XCD x (ids with id % 8 == x) gets one contiguous range.
+__device__ __forceinline__ int xcd_block(int pid, int total) {
+  constexpr int kX = 8;
+  const int q = total / kX, r = total % kX;
+  const int x = pid % kX;
+  return x * q + min(x, r) + pid / kX;
+}
+
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
+}
 
 }  // namespace fa
 
@@ -52,14 +103,17 @@ __global__ __launch_bounds__(fa::kThreads, 2) void fa_fwd_mfma_kernel(const uint
                                                                       int s_kv, float scale_log2) {
   using namespace fa;
   using H = Half16<Tag>;
-  constexpr int DCH = D / 8;           // 16-byte chunks per K row
-  constexpr int KVEC = kBC * DCH;      // u32x4 per K tile
-  constexpr int VVEC = D * (kBC / 8);  // u32x4 per V^T tile
-  constexpr int NDB = D / 32;          // 32-wide d blocks of O^T
-  constexpr int NKK = D / 16;          // 16-wide d steps of S^T
+  constexpr int RB = 2 * D;          // bytes per K/V row
+  constexpr int TB = kBC * RB;       // bytes per K or V tile
+  constexpr int DCH = D / 8;         // 16-byte chunks per row
+  constexpr int NKK = D / 16;        // S^T MFMAs per 32-key block
+  constexpr int NDB = D / 32;        // 32-row d blocks of O^T
+  constexpr int NS = 2 * NKK;        // S^T MFMAs per tile
+  constexpr int NP = 4 * NDB;        // PV MFMAs per tile
+  constexpr int PW = TB / 1024 / 4;  // copy instructions per wave, tile and operand
+  constexpr int RPP = 1024 / RB;     // rows per copy instruction
 
-  __shared__ u32x4 k_lds[2][KVEC];
-  __shared__ u32x4 v_lds[2][VVEC];
+  __shared__ __attribute__((aligned(1024))) u32x4 lds[4 * TB / 16];  // K0 K1 V0 V1
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -68,14 +122,15 @@ __global__ __launch_bounds__(fa::kThreads, 2) void fa_fwd_mfma_kernel(const uint
   const int ql = lane & 31;
 
   const int nmb = (s_q + kBM - 1) / kBM;
-  const int pid = blockIdx.x;
-  const int bh = pid % bh_count;
-  int mb = pid / bh_count;
-  if (kCausal) mb = nmb - 1 - mb;  // longest query blocks first
+  const int lin = xcd_block(blockIdx.x, nmb * bh_count);
+  const int bh = lin / nmb;
+  int mb = lin - bh * nmb;
+  if (kCausal) mb = nmb - 1 - mb;  // longest query blocks of a (b,h) first
   const int m0 = mb * kBM;
+  const long long kv_base = (long long)bh * s_kv * D;
   const uint16_t* Qh = Q + (long long)bh * s_q * D;
-  const uint16_t* Kh = K + (long long)bh * s_kv * D;
-  const uint16_t* Vh = V + (long long)bh * s_kv * D;
+  const char* Kb = reinterpret_cast<const char*>(K + kv_base);
+  const char* Vb = reinterpret_cast<const char*>(V + kv_base);
   uint16_t* Oh = O + (long long)bh * s_q * D;
 
   const int q_row = m0 + 32 * wave + ql;
@@ -84,158 +139,259 @@ __global__ __launch_bounds__(fa::kThreads, 2) void fa_fwd_mfma_kernel(const uint
   for (int kk = 0; kk < NKK; ++kk)
     qf[kk] = (!kMasked || q_row < s_q) ? ld16(Qh + (long long)q_row * D + 16 * kk + 8 * half) : u32x4{0, 0, 0, 0};
 
+  const int n_end = kCausal ? min(s_kv, m0 + kBM) : s_kv;
+  const int ntiles = (n_end + kBC - 1) / kBC;
+  const int wave_q_lo = m0 + 32 * wave;
+
+  // ---- HBM -> LDS copies: K tile t into K buffer b (LDS bytes b*TB), V into 2*TB + b*TB ----
+  const uint32_t lds0 = lds_addr(&lds[0]);
+  const int c_row0 = wave * PW * RPP + lane / DCH;
+  const int c_slot = lane % DCH;
+  uint32_t k_goff[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int row = c_row0 + p * RPP;
+    k_goff[p] = (uint32_t)(row * RB + 16 * (c_slot ^ k_mask<D>(row)));
+  }
+  const uint32_t v_goff = (uint32_t)(c_row0 * RB + 16 * (c_slot ^ v_mask<D>(c_row0)));
+
+  auto copy_tile = [&](const char* src, int t, uint32_t lds_buf, auto is_v) {
+    constexpr bool kV = decltype(is_v)::value != 0;
+    const int n0 = t * kBC;
+    const uint32_t mw = lds_buf + wave * PW * 1024;
+    if (kMasked && n0 + kBC > s_kv) {  // tail tile: rows past s_kv repeat the last key (masked in S)
+#pragma unroll
+      for (int p = 0; p < PW; ++p) {
+        const int row = c_row0 + p * RPP;
+        const int mask = kV ? v_mask<D>(row) : k_mask<D>(row);
+        g2lds16_m(src + (long long)min(n0 + row, s_kv - 1) * RB + 16 * (c_slot ^ mask), mw + p * 1024);
+      }
+    } else {
+      const char* base = src + (long long)n0 * RB;
+      static_for<PW>([&](auto pc) {
+        constexpr int p = decltype(pc)::value;
+        if constexpr (kV) g2lds16_s(v_goff, base + p * 1024, mw + p * 1024);
+        else g2lds16_s(k_goff[p & 1], base + (p & ~1) * 1024, mw + p * 1024);
+      });
+    }
+  };
+  auto copy_k = [&](int t, int buf) { copy_tile(Kb, t, lds0 + buf * TB, Int<0>{}); };
+  auto copy_v = [&](int t, int buf) { copy_tile(Vb, t, lds0 + (2 + buf) * TB, Int<1>{}); };
+
+  // ---- fragment reads ----
+  // K: MFMA step i (block kb = i&1, d step kk = i>>1) reads key key_perm(ql) + 32kb, chunk
+  // 2kk + half; k_mask(key + 32) == k_mask(key), so kb is an immediate offset.
+  uint32_t k_rd[NKK];
+  {
+    const int key = key_perm(ql);
+    const int km = k_mask<D>(key);
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) k_rd[kk] = lds0 + key * RB + 16 * ((2 * kk + half) ^ km);
+  }
+  // V^T: PV MFMA i = (2kb + t)*NDB + db; lane group g = lane/16 reads key rows
+  // 32kb + 16*half + 8t + {0..3} (then +4) and d columns 32db + 16(g&1) .. +15. v_mask of
+  // those rows equals that of row 16*half + (j>>2), so kb and t are immediate offsets.
+  uint32_t v_rd[NDB];
+  {
+    const int g = lane >> 4, jj = lane & 15;
+    const int row = 16 * half + (jj >> 2);
+    const int vm = v_mask<D>(row);
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const int c16 = 4 * db + 2 * (g & 1) + ((jj & 3) >> 1);
+      v_rd[db] = lds0 + 2 * TB + row * RB + 16 * (c16 ^ vm) + 8 * (jj & 1);
+    }
+  }
+  auto read_k = [&](int buf, int i) -> u32x4 {
+    return *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(k_rd[i >> 1] + buf * TB + (i & 1) * 32 * RB);
+  };
+  auto read_v = [&](int buf, int i) -> u32x4 {
+    const int grp = i / NDB, db = i % NDB;
+    const uint32_t a = v_rd[db] + buf * TB + (32 * (grp >> 1) + 8 * (grp & 1)) * RB;
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(uintptr_t)a);
+    const s16x4 hi =
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(uintptr_t)(a + 4 * RB));
+    const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+    return u32x4{l2[0], l2[1], h2[0], h2[1]};
+  };
+
+  // ---- softmax state ----
   f32x16 o[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
-  float m_run = -INFINITY;
-  float l_run = 0.f;
+  float m_run = -INFINITY;  // max used by exp2 (log2 units)
+  float l_run = 0.f;        // this lane's share of the row sum
+  float m_cur = -INFINITY;  // max of the S tile about to be exponentiated (log2 units)
+  u32x4 pp[4];              // P of group 2kb + t (keys 32kb + 16*half + 8t + 0..7)
+  const f32x16 zero16 = {};
 
-  const int n_end = kCausal ? min(s_kv, m0 + kBM) : s_kv;
-  const int ntiles = (n_end + kBC - 1) / kBC;
-
-  // V: each thread owns a 4-key x 8-d block: key group va (0..15), d chunk ve.
-  constexpr int VTHREADS = (kBC / 4) * (D / 8);
-  const int ve = tid % (D / 8);
-  const int va = tid / (D / 8);
-  // K: wave-level direct global->LDS copies, KROWS rows of the tile per instruction.
-  constexpr int KROWS = 64 / DCH;
-  constexpr int KINST = kBC / KROWS / 4;  // instructions per wave
-  static_assert(kBC % (KROWS * 4) == 0, "K tile must split over 4 waves");
-
-  u32x4 vpre[4];
-
-  auto load_tile = [&](int j, int buf) {
-    const int n0 = j * kBC;
-#pragma unroll
-    for (int i = 0; i < KINST; ++i) {
-      const int slab = wave * KINST + i;  // KROWS rows per slab
-      const int row = slab * KROWS + lane / DCH;
-      const int pc = lane % DCH;
-      int grow = n0 + row;
-      if (kMasked) grow = min(grow, s_kv - 1);  // clamped rows are masked out of S below
-      const uint16_t* src = Kh + (long long)grow * D + 8 * (pc ^ k_swz(row));
-      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)&k_lds[buf][slab * 64], 16, 0, 0);
-    }
-    if (tid < VTHREADS) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = n0 + 4 * va + r;
-        vpre[r] = (!kMasked || row < s_kv) ? ld16(Vh + (long long)row * D + 8 * ve) : u32x4{0, 0, 0, 0};
-      }
-    }
+  auto need_mask = [&](int t) {
+    const int n0 = t * kBC;
+    return (kMasked && n0 + kBC > s_kv) || (kCausal && n0 + kBC - 1 > wave_q_lo);
   };
-  auto store_v = [&](int buf) {
-    if (tid < VTHREADS) {
-      uint32_t* vrow = reinterpret_cast<uint32_t*>(&v_lds[buf][0]);
+  auto apply_mask = [&](f32x16(&s)[2], int t) {
+    const int key0 = t * kBC + 16 * half;
 #pragma unroll
-      for (int jd = 0; jd < 8; ++jd) {
-        const int dw = jd >> 1;
-        u32x2 col;
-        if (jd & 1) {
-          col[0] = hi_halves(vpre[0][dw], vpre[1][dw]);
-          col[1] = hi_halves(vpre[2][dw], vpre[3][dw]);
-        } else {
-          col[0] = lo_halves(vpre[0][dw], vpre[1][dw]);
-          col[1] = lo_halves(vpre[2][dw], vpre[3][dw]);
-        }
-        const int d = 8 * ve + jd;
-        const int chunk = (va >> 1) ^ v_swz(d);
-        *reinterpret_cast<u32x2*>(vrow + (d * 8 + chunk) * 4 + (va & 1) * 2) = col;
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = key0 + 32 * kb + i;
+        const bool dead = (kMasked && key >= s_kv) || (kCausal && key > q_row);
+        if (dead) s[kb][i] = -INFINITY;
       }
-    }
   };
-
-  load_tile(0, 0);
-  store_v(0);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-
-  const int wave_q_lo = m0 + 32 * wave;
-  const int wave_q_hi = wave_q_lo + 31;
-
-  for (int j = 0; j < ntiles; ++j) {
-    const int cur = j & 1;
-    const int n0 = j * kBC;
-    if (j + 1 < ntiles) load_tile(j + 1, cur ^ 1);
-
-    // A causal tile that starts past every query of this wave contributes nothing.
-    const bool active = !kCausal || n0 <= wave_q_hi;
-    if (active) {
-      f32x16 s[2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) s[kb][i] = 0.f;
-        const int key = kb * 32 + key_perm(ql);
-        const int sw = k_swz(key);
-#pragma unroll
-        for (int kk = 0; kk < NKK; ++kk) {
-          const u32x4 kf = k_lds[cur][key * DCH + ((2 * kk + half) ^ sw)];
-          s[kb] = H::mfma32(kf, qf[kk], s[kb]);
-        }
-      }
-      // lane holds S[q_row][n0 + 32kb + 16*half + i]
-      const bool need_mask = (kMasked && n0 + kBC > s_kv) || (kCausal && n0 + kBC - 1 > wave_q_lo);
-      if (need_mask) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int key = n0 + 32 * kb + 16 * half + i;
-            const bool dead = (kMasked && key >= s_kv) || (kCausal && key > q_row);
-            if (dead) s[kb][i] = -INFINITY;
-          }
-      }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run, mx * scale_log2);
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-      float rs = 0.f;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][i], scale_log2, -m_new));
-          s[kb][i] = p;
-          rs += p;
-        }
-      l_run = l_run * alpha + rs;
-      m_run = m_new;
+  // max op k (0..15) over the 32 scores of a lane: v_maximum3_f32 chains
+  auto max_op = [&](const f32x16(&s)[2], int k, float& mx) {
+    auto e = [&](int x) { return s[x >> 4][x & 15]; };
+    if (k == 0) mx = max3f(e(0), e(1), e(2));
+    else if (k < 15) mx = max3f(mx, e(1 + 2 * k), e(2 + 2 * k));
+    else mx = __builtin_elementwise_maximum(mx, e(31));
+  };
+  auto rescale = [&]() {
+    const bool raise = m_cur > m_run + kRescaleSlack;
+    if (__builtin_amdgcn_ballot_w64(raise)) {
+      const float alpha = raise ? __builtin_amdgcn_exp2f(m_run - m_cur) : 1.f;  // 0 on the first tile
+      m_run = raise ? m_cur : m_run;
+      l_run *= alpha;
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
-
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          u32x4 pp;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) pp[e] = H::pack2(s[kb][8 * t + 2 * e], s[kb][8 * t + 2 * e + 1]);
-          const int kc = 4 * kb + 2 * half + t;
-#pragma unroll
-          for (int db = 0; db < NDB; ++db) {
-            const int d = 32 * db + ql;
-            const u32x4 vf = v_lds[cur][d * 8 + (kc ^ v_swz(d))];
-            o[db] = H::mfma32(vf, pp, o[db]);
-          }
-        }
-      }
     }
-    if (j + 1 < ntiles) store_v(cur ^ 1);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+  };
+  auto sm_elem = [&](f32x16(&s)[2], int e) {
+    s[e >> 4][e & 15] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e >> 4][e & 15], scale_log2, -m_run));
+  };
+  auto sm_pack = [&](const f32x16(&s)[2], int g) {
+    const int kb = g >> 1, t = g & 1;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      pp[g][q] = H::pack2(s[kb][8 * t + 2 * q], s[kb][8 * t + 2 * q + 1]);
+      l_run = H::sum2(pp[g][q], l_run);
+    }
+  };
+  auto pv = [&](int i, u32x4 vf) {
+    const int db = i % NDB;
+    o[db] = H::mfma32(vf, pp[i / NDB], o[db]);
+  };
+  auto s_mfma = [&](f32x16(&s)[2], int i, u32x4 kf) {
+    s[i & 1] = H::mfma32(kf, qf[i >> 1], i < 2 ? zero16 : s[i & 1]);
+  };
+
+  // One key tile. par = j & 1 (K(j+1) sits in K buffer par^1, V(j) in V buffer par);
+  // kNext: tile j+1 exists, its S is computed here into sn.
+  auto iteration = [&](int j, auto par_tag, auto next_tag, f32x16(&sc)[2], f32x16(&sn)[2]) {
+    constexpr int par = decltype(par_tag)::value;
+    constexpr bool kNext = decltype(next_tag)::value != 0;
+    if (j + 2 < ntiles) copy_k(j + 2, par);
+    if constexpr (kNext) copy_v(j + 1, par ^ 1);
+    rescale();
+    if constexpr (!kNext) {
+      u32x4 vf[NP];
+#pragma unroll
+      for (int i = 0; i < NP; ++i) vf[i] = read_v(par, i);
+#pragma unroll
+      for (int e = 0; e < 32; ++e) {
+        sm_elem(sc, e);
+        if ((e & 7) == 7) sm_pack(sc, e >> 3);
+      }
+#pragma unroll
+      for (int i = 0; i < NP; ++i) pv(i, vf[i]);
+    } else {
+      u32x4 kf[NS];
+      u32x4 vf[NP];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) kf[i] = read_k(par ^ 1, i);
+      __builtin_amdgcn_sched_barrier(0);
+      // block 1: S(j+1) MFMAs; softmax elements 0..23 of S(j)
+#pragma unroll
+      for (int i = 0; i < NS; ++i) {
+        s_mfma(sn, i, kf[i]);
+        if (i + 3 < NS) kf[i + 3] = read_k(par ^ 1, i + 3);
+        if (i == NS - 2) vf[0] = read_v(par, 0);
+        if (i == NS - 1) vf[1] = read_v(par, 1);
+        const int lo = 24 * i / NS, hi = 24 * (i + 1) / NS;
+#pragma unroll
+        for (int e = lo; e < hi; ++e) sm_elem(sc, e);
+#pragma unroll
+        for (int g = 0; g < 3; ++g)
+          if (8 * (g + 1) > lo && 8 * (g + 1) <= hi) sm_pack(sc, g);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // block 2, first half: PV of key block 0; softmax elements 24..31
+#pragma unroll
+      for (int i = 0; i < 2 * NDB; ++i) {
+        pv(i, vf[i]);
+        vf[i + 2] = read_v(par, i + 2);
+        const int lo = 24 + 8 * i / (2 * NDB), hi = 24 + 8 * (i + 1) / (2 * NDB);
+#pragma unroll
+        for (int e = lo; e < hi; ++e) sm_elem(sc, e);
+        if (i == 2 * NDB - 1) sm_pack(sc, 3);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // block 2, second half: PV of key block 1; max of S(j+1)
+      float mx = 0.f;
+      if (!need_mask(j + 1)) {
+#pragma unroll
+        for (int i = 2 * NDB; i < NP; ++i) {
+          pv(i, vf[i]);
+          if (i + 2 < NP) vf[i + 2] = read_v(par, i + 2);
+          const int r = i - 2 * NDB;
+          const int lo = 16 * r / (2 * NDB), hi = 16 * (r + 1) / (2 * NDB);
+#pragma unroll
+          for (int k = lo; k < hi; ++k) max_op(sn, k, mx);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+#pragma unroll
+        for (int i = 2 * NDB; i < NP; ++i) {
+          pv(i, vf[i]);
+          if (i + 2 < NP) vf[i + 2] = read_v(par, i + 2);
+        }
+        apply_mask(sn, j + 1);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) max_op(sn, k, mx);
+      }
+      m_cur = halves_max(mx) * scale_log2;
+      wait_and_barrier<0>();
+    }
+  };
+
+  // ---- prologue: tiles 0 (K, V) and 1 (K); S(0) and its max ----
+  copy_k(0, 0);
+  copy_v(0, 0);
+  if (ntiles > 1) copy_k(1, 1);
+  wait_and_barrier<0>();
+  f32x16 sa[2], sb[2];
+  {
+    u32x4 kf[NS];
+#pragma unroll
+    for (int i = 0; i < NS; ++i) kf[i] = read_k(0, i);
+#pragma unroll
+    for (int i = 0; i < NS; ++i) s_mfma(sa, i, kf[i]);
+    if (need_mask(0)) apply_mask(sa, 0);
+    float mx = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) max_op(sa, k, mx);
+    m_cur = halves_max(mx) * scale_log2;
+  }
+  wait_and_barrier<0>();  // every wave is done with K(0) before K(2) replaces it
+
+  int j = 0;
+  for (; j + 2 < ntiles; j += 2) {
+    iteration(j, Int<0>{}, Int<1>{}, sa, sb);
+    iteration(j + 1, Int<1>{}, Int<1>{}, sb, sa);
+  }
+  if (j + 1 < ntiles) {
+    iteration(j, Int<0>{}, Int<1>{}, sa, sb);
+    iteration(j + 1, Int<1>{}, Int<0>{}, sb, sa);
+  } else {
+    iteration(j, Int<0>{}, Int<0>{}, sa, sb);
   }
 
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-  const float inv = 1.f / l_tot;
+  const float inv = 1.f / halves_sum(l_run);
   if (!kMasked || q_row < s_q) {
     uint16_t* orow = Oh + (long long)q_row * D;
 #pragma unroll

@@ -20,6 +20,7 @@
 #pragma once
 
 #include "common.h"
+#include "lds_dma.h"
 
 namespace kg_gfx950 {
 
@@ -237,52 +238,11 @@ __device__ __forceinline__ int a_mask(int row) { return (row >> 2) & 3; }
 __device__ __forceinline__ int b_mask(int k) { return 4 * (k & 3); }
 __device__ __forceinline__ int a_slot(int row, int c) { return row * 4 + (c ^ a_mask(row)); }
 __device__ __forceinline__ int b_slot(int k, int c) { return k * 32 + (c ^ b_mask(k)); }
-typedef short s16x4 __attribute__((ext_vector_type(4)));
 template <int S>
 struct StageIdx {
   static constexpr int value = S;
 };
 }  // namespace gemmp
-
-// Wait until at most N of this wave's vector-memory ops (including HBM->LDS copies) are
-// outstanding and all of its LDS ops are done, then meet the other waves. The copies are
-// issued through inline asm (g2lds16), so the compiler neither tracks nor waits for them;
-// these explicit waits are the only synchronisation, and the empty asm statements keep
-// LDS reads from being moved across the barrier.
-template <int N>
-__device__ __forceinline__ void wait_and_barrier() {
-  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-  else if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)" ::: "memory");
-  else if constexpr (N == 16) asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)" ::: "memory");
-  else if constexpr (N == 24) asm volatile("s_waitcnt vmcnt(24) lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
-// 16 bytes per lane HBM -> LDS: lane l's data lands at LDS byte lds_base + 16*l
-// (lds_base must be wave-uniform; it goes through M0).
-__device__ __forceinline__ void g2lds16(const void* gptr, const void* lds_base) {
-  const uint32_t m0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_base;
-  asm volatile(
-      "s_mov_b32 m0, %1\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %0, off"
-      :
-      : "v"(gptr), "s"(m0)
-      : "memory", "m0");
-}
-
-// 16 bytes per lane HBM -> LDS with a wave-uniform 64-bit base (SGPRs) and a per-lane
-// 32-bit byte offset: lane l's data lands at LDS byte m0 + 16*l.
-__device__ __forceinline__ void g2lds16_s(uint32_t voff, const void* sbase, uint32_t m0) {
-  asm volatile(
-      "s_mov_b32 m0, %2\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %0, %1"
-      :
-      : "v"(voff), "s"(sbase), "s"(m0)
-      : "memory", "m0");
-}
 
 template <typename Tag, int kBias>
 __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(

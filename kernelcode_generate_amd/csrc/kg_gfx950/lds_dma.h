@@ -1,0 +1,82 @@
+// HBM -> LDS copies with global_load_lds_dwordx4 and the explicit waits they need.
+//
+// The copies are issued through inline asm so that the compiler neither tracks nor waits
+// for them (its own tracking of global_load_lds inserts vmcnt(0) before every LDS read).
+// The waits below are therefore the only synchronisation: a wave waits for its own copies
+// with s_waitcnt vmcnt, then meets the other waves at s_barrier; the empty asm statement
+// after the barrier keeps LDS reads from being moved across it.
+#pragma once
+
+#include <utility>
+
+#include "common.h"
+
+namespace kg_gfx950 {
+
+// Wait until at most N of this wave's vector-memory ops (copies included) are outstanding
+// and all of its LDS ops are done, then meet the other waves of the workgroup.
+template <int N>
+__device__ __forceinline__ void wait_and_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(N) : "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// 16 bytes per lane: lane l's data lands at LDS byte lds_base + 16*l (lds_base must be
+// wave-uniform; it goes through M0). gptr is a per-lane 64-bit address.
+__device__ __forceinline__ void g2lds16(const void* gptr, const void* lds_base) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_base;
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, off"
+      :
+      : "v"(gptr), "s"(m0)
+      : "memory", "m0");
+}
+
+// Same with the LDS byte address given directly.
+__device__ __forceinline__ void g2lds16_m(const void* gptr, uint32_t m0) {
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, off"
+      :
+      : "v"(gptr), "s"(m0)
+      : "memory", "m0");
+}
+
+// 16 bytes per lane with a wave-uniform 64-bit base (SGPRs) and a per-lane 32-bit byte
+// offset: lane l's data lands at LDS byte m0 + 16*l. (No immediate offset is used: the
+// instruction's offset field would also move the LDS address.)
+__device__ __forceinline__ void g2lds16_s(uint32_t voff, const void* sbase, uint32_t m0) {
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %1"
+      :
+      : "v"(voff), "s"(sbase), "s"(m0)
+      : "memory", "m0");
+}
+
+// LDS byte address of a shared-memory object (what M0 and ds_* addresses take).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+template <int N>
+struct Int {
+  static constexpr int value = N;
+};
+// f(Int<0>{}), ..., f(Int<N-1>{}): for indices that must be compile-time constants.
+template <typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(Int<Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+}  // namespace kg_gfx950
