@@ -1,10 +1,11 @@
 // Flash-attention forward on gfx950 MFMA: 16-bit Q/K/V/O [B,H,S,D], D in {64, 128},
 // fp32 online softmax, optional scale and causal mask.
 //
-// Work split: one workgroup = 128 query rows of one (b,h), 4 waves x 32 queries; key/value
-// tiles of 64 keys are copied HBM -> LDS (two buffers each for K and V) and shared by the
-// four waves. Workgroup ids are dealt to the 8 XCDs round-robin; they are remapped so that
-// each XCD runs the query blocks of the same (b,h) together and its L2 serves their K/V.
+// Work split: a workgroup holds query rows of one (b,h), 32 per wave (Cfg<D>: 8 waves for
+// D=128, 4 for D=64; two waves per SIMD either way). Key/value tiles of 64 keys are copied
+// HBM -> LDS (two buffers each for K and V) and shared by the workgroup's waves. Workgroup
+// ids are dealt to the 8 XCDs round-robin; they are remapped so that each XCD runs the query
+// blocks of the same (b,h) together and its L2 serves their K/V.
 //
 // Per wave and key tile the kernel computes S^T = K Q^T with v_mfma_f32_32x32x16 (operand A
 // = 32 keys x 16 d from LDS, operand B = Q^T kept in registers for the whole kernel). In
@@ -29,8 +30,8 @@
 //            reads slotted between them;
 //   block 2: the PV(j) MFMAs, with the last quarter of softmax(j), the V(j) fragment reads
 //            and the max of S(j+1) slotted between them.
-// Copies of K(j+2) and V(j+1) are issued at the start of iteration j into the buffers that
-// iteration j-1 finished with; one wait + barrier ends the iteration.
+// The copies of K(j+2) and V(j+1) (into the buffers iteration j-1 finished with) are
+// slotted between the block-1 MFMAs of iteration j; one wait + barrier ends the iteration.
 //
 // LDS chunk swizzles (16-byte chunks, 64 banks of 4 bytes; ds_read_b128 serves 16 lanes per
 // cycle, 64-bit reads 32): K chunk c of key row r sits at slot c ^ k_mask(r) and V chunk c
@@ -44,9 +45,17 @@ namespace kg_gfx950 {
 
 namespace fa {
 
-constexpr int kBM = 128;  // queries per workgroup
-constexpr int kBC = 64;   // keys per tile
-constexpr int kThreads = 256;
+constexpr int kBC = 64;  // keys per tile
+// Waves per workgroup (32 queries each): D=128 uses one 8-wave workgroup per CU (K/V tiles
+// shared by 256 queries halve the HBM/L2 -> LDS copy traffic per query), D=64 two 4-wave
+// workgroups per CU. Either way two waves share each SIMD.
+template <int D>
+struct Cfg {
+  static constexpr int kWaves = D == 128 ? 8 : 4;
+  static constexpr int kBM = 32 * kWaves;  // queries per workgroup
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kPerCU = 8 / kWaves;
+};
 // Running-max slack (log2 units): P <= 2^8 between rescales.
 constexpr float kRescaleSlack = 8.0f;
 
@@ -69,8 +78,9 @@ __host__ __device__ constexpr int v_mask(int key) {
 // wave-uniform base by whole KiB, which needs the masks of their rows to repeat.
 template <int D>
 constexpr bool copy_masks_repeat() {
-  constexpr int RB = 2 * D, PW = kBC * RB / 1024 / 4, RPP = 1024 / RB, DCH = D / 8;
-  for (int w = 0; w < 4; ++w)
+  constexpr int kWaves = Cfg<D>::kWaves;
+  constexpr int RB = 2 * D, PW = kBC * RB / 1024 / kWaves, RPP = 1024 / RB, DCH = D / 8;
+  for (int w = 0; w < kWaves; ++w)
     for (int lane = 0; lane < 64; ++lane)
       for (int p = 0; p < PW; ++p) {
         const int row = (w * PW + p) * RPP + lane / DCH;
@@ -96,13 +106,15 @@ __device__ __forceinline__ float max3f(float a, float b, float c) {
 }  // namespace fa
 
 template <typename Tag, int D, bool kCausal, bool kMasked>
-__global__ __launch_bounds__(fa::kThreads, 2) void fa_fwd_mfma_kernel(const uint16_t* __restrict__ Q,
+__global__ __launch_bounds__(fa::Cfg<D>::kThreads, fa::Cfg<D>::kPerCU) void fa_fwd_mfma_kernel(const uint16_t* __restrict__ Q,
                                                                       const uint16_t* __restrict__ K,
                                                                       const uint16_t* __restrict__ V,
                                                                       uint16_t* __restrict__ O, int bh_count, int s_q,
                                                                       int s_kv, float scale_log2) {
   using namespace fa;
   using H = Half16<Tag>;
+  constexpr int kWaves = Cfg<D>::kWaves;
+  constexpr int kBM = Cfg<D>::kBM;
   constexpr int RB = 2 * D;          // bytes per K/V row
   constexpr int TB = kBC * RB;       // bytes per K or V tile
   constexpr int DCH = D / 8;         // 16-byte chunks per row
@@ -110,7 +122,8 @@ __global__ __launch_bounds__(fa::kThreads, 2) void fa_fwd_mfma_kernel(const uint
   constexpr int NDB = D / 32;        // 32-row d blocks of O^T
   constexpr int NS = 2 * NKK;        // S^T MFMAs per tile
   constexpr int NP = 4 * NDB;        // PV MFMAs per tile
-  constexpr int PW = TB / 1024 / 4;  // copy instructions per wave, tile and operand
+  constexpr int PW = TB / 1024 / kWaves;  // copy instructions per wave, tile and operand
+  static_assert(PW >= 1 && 2 * PW <= NS, "copy slots");
   constexpr int RPP = 1024 / RB;     // rows per copy instruction
 
   __shared__ __attribute__((aligned(1024))) u32x4 lds[4 * TB / 16];  // K0 K1 V0 V1
@@ -155,28 +168,28 @@ __global__ __launch_bounds__(fa::kThreads, 2) void fa_fwd_mfma_kernel(const uint
   }
   const uint32_t v_goff = (uint32_t)(c_row0 * RB + 16 * (c_slot ^ v_mask<D>(c_row0)));
 
-  auto copy_tile = [&](const char* src, int t, uint32_t lds_buf, auto is_v) {
-    constexpr bool kV = decltype(is_v)::value != 0;
+  // Copy instruction p (< PW) of tile t of K (kV false) or V into the LDS buffer at lds_buf.
+  auto copy_piece = [&](const char* src, int t, uint32_t lds_buf, bool kV, int p) {
     const int n0 = t * kBC;
-    const uint32_t mw = lds_buf + wave * PW * 1024;
+    const uint32_t m = lds_buf + (wave * PW + p) * 1024;
     if (kMasked && n0 + kBC > s_kv) {  // tail tile: rows past s_kv repeat the last key (masked in S)
-#pragma unroll
-      for (int p = 0; p < PW; ++p) {
-        const int row = c_row0 + p * RPP;
-        const int mask = kV ? v_mask<D>(row) : k_mask<D>(row);
-        g2lds16_m(src + (long long)min(n0 + row, s_kv - 1) * RB + 16 * (c_slot ^ mask), mw + p * 1024);
-      }
+      const int row = c_row0 + p * RPP;
+      const int mask = kV ? v_mask<D>(row) : k_mask<D>(row);
+      g2lds16_m(src + (long long)min(n0 + row, s_kv - 1) * RB + 16 * (c_slot ^ mask), m);
     } else {
       const char* base = src + (long long)n0 * RB;
-      static_for<PW>([&](auto pc) {
-        constexpr int p = decltype(pc)::value;
-        if constexpr (kV) g2lds16_s(v_goff, base + p * 1024, mw + p * 1024);
-        else g2lds16_s(k_goff[p & 1], base + (p & ~1) * 1024, mw + p * 1024);
-      });
+      if (kV) g2lds16_s(v_goff, base + p * 1024, m);
+      else g2lds16_s(k_goff[p & 1], base + (p & ~1) * 1024, m);
     }
   };
-  auto copy_k = [&](int t, int buf) { copy_tile(Kb, t, lds0 + buf * TB, Int<0>{}); };
-  auto copy_v = [&](int t, int buf) { copy_tile(Vb, t, lds0 + (2 + buf) * TB, Int<1>{}); };
+  auto copy_k = [&](int t, int buf) {
+#pragma unroll
+    for (int p = 0; p < PW; ++p) copy_piece(Kb, t, lds0 + buf * TB, false, p);
+  };
+  auto copy_v = [&](int t, int buf) {
+#pragma unroll
+    for (int p = 0; p < PW; ++p) copy_piece(Vb, t, lds0 + (2 + buf) * TB, true, p);
+  };
 
   // ---- fragment reads ----
   // K: MFMA step i (block kb = i&1, d step kk = i>>1) reads key key_perm(ql) + 32kb, chunk
@@ -285,8 +298,7 @@ __global__ __launch_bounds__(fa::kThreads, 2) void fa_fwd_mfma_kernel(const uint
   auto iteration = [&](int j, auto par_tag, auto next_tag, f32x16(&sc)[2], f32x16(&sn)[2]) {
     constexpr int par = decltype(par_tag)::value;
     constexpr bool kNext = decltype(next_tag)::value != 0;
-    if (j + 2 < ntiles) copy_k(j + 2, par);
-    if constexpr (kNext) copy_v(j + 1, par ^ 1);
+    const bool copy_k2 = j + 2 < ntiles;  // K(j+2) exists (only if kNext)
     rescale();
     if constexpr (!kNext) {
       u32x4 vf[NP];
@@ -309,6 +321,18 @@ __global__ __launch_bounds__(fa::kThreads, 2) void fa_fwd_mfma_kernel(const uint
 #pragma unroll
       for (int i = 0; i < NS; ++i) {
         s_mfma(sn, i, kf[i]);
+        // this wave's 2*PW copies of K(j+2) and V(j+1), spread over the steps: a burst of
+        // copies from all waves right after the barrier stalls their issue for hundreds of
+        // cycles (the HBM/L2 -> LDS path moves about 64-80 bytes per clock per CU)
+        constexpr int kGap = NS / (2 * PW);
+        if (i % kGap == kGap - 1) {
+          const int c = i / kGap;
+          if (c < PW) {
+            if (copy_k2) copy_piece(Kb, j + 2, lds0 + par * TB, false, c);
+          } else {
+            copy_piece(Vb, j + 1, lds0 + (2 + (par ^ 1)) * TB, true, c - PW);
+          }
+        }
         if (i + 3 < NS) kf[i + 3] = read_k(par ^ 1, i + 3);
         if (i == NS - 2) vf[0] = read_v(par, 0);
         if (i == NS - 1) vf[1] = read_v(par, 1);
@@ -409,29 +433,29 @@ __global__ __launch_bounds__(fa::kThreads, 2) void fa_fwd_mfma_kernel(const uint
 
 inline bool fa_mfma_supported(const FaShape& s) {
   return (s.d == 64 || s.d == 128) && s.scale > 0.f && s.s_q >= 1 && s.s_kv >= 1 && (!s.causal || s.s_q == s.s_kv) &&
-         (long long)((s.s_q + fa::kBM - 1) / fa::kBM) * s.bh < (1ll << 31);
+         (long long)((s.s_q + fa::Cfg<64>::kBM - 1) / fa::Cfg<64>::kBM) * s.bh < (1ll << 31);
 }
 
 template <typename Tag, int D>
 hipError_t launch_fa_fwd_mfma_d(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, const FaShape& s,
                                 hipStream_t stream) {
-  const int nmb = (s.s_q + fa::kBM - 1) / fa::kBM;
+  const int nmb = (s.s_q + fa::Cfg<D>::kBM - 1) / fa::Cfg<D>::kBM;
   const dim3 grid(nmb * s.bh);
-  const bool masked = (s.s_q % fa::kBM) != 0 || (s.s_kv % fa::kBC) != 0;
+  const bool masked = (s.s_q % fa::Cfg<D>::kBM) != 0 || (s.s_kv % fa::kBC) != 0;
   const float scale_log2 = s.scale * 1.4426950408889634f;
   if (s.causal) {
     if (masked)
-      hipLaunchKernelGGL((fa_fwd_mfma_kernel<Tag, D, true, true>), grid, dim3(fa::kThreads), 0, stream, q, k, v, o, s.bh,
+      hipLaunchKernelGGL((fa_fwd_mfma_kernel<Tag, D, true, true>), grid, dim3(fa::Cfg<D>::kThreads), 0, stream, q, k, v, o, s.bh,
                          s.s_q, s.s_kv, scale_log2);
     else
-      hipLaunchKernelGGL((fa_fwd_mfma_kernel<Tag, D, true, false>), grid, dim3(fa::kThreads), 0, stream, q, k, v, o, s.bh,
+      hipLaunchKernelGGL((fa_fwd_mfma_kernel<Tag, D, true, false>), grid, dim3(fa::Cfg<D>::kThreads), 0, stream, q, k, v, o, s.bh,
                          s.s_q, s.s_kv, scale_log2);
   } else {
     if (masked)
-      hipLaunchKernelGGL((fa_fwd_mfma_kernel<Tag, D, false, true>), grid, dim3(fa::kThreads), 0, stream, q, k, v, o, s.bh,
+      hipLaunchKernelGGL((fa_fwd_mfma_kernel<Tag, D, false, true>), grid, dim3(fa::Cfg<D>::kThreads), 0, stream, q, k, v, o, s.bh,
                          s.s_q, s.s_kv, scale_log2);
     else
-      hipLaunchKernelGGL((fa_fwd_mfma_kernel<Tag, D, false, false>), grid, dim3(fa::kThreads), 0, stream, q, k, v, o, s.bh,
+      hipLaunchKernelGGL((fa_fwd_mfma_kernel<Tag, D, false, false>), grid, dim3(fa::Cfg<D>::kThreads), 0, stream, q, k, v, o, s.bh,
                          s.s_q, s.s_kv, scale_log2);
   }
   return hipGetLastError();

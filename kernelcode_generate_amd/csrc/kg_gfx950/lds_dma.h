@@ -7,8 +7,6 @@
 // after the barrier keeps LDS reads from being moved across it.
 #pragma once
 
-#include <utility>
-
 #include "common.h"
 
 namespace kg_gfx950 {
@@ -69,14 +67,4 @@ template <int N>
 struct Int {
   static constexpr int value = N;
 };
-// f(Int<0>{}), ..., f(Int<N-1>{}): for indices that must be compile-time constants.
-template <typename F, int... Is>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
-  (f(Int<Is>{}), ...);
-}
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
 }  // namespace kg_gfx950
