@@ -2,43 +2,48 @@
 // a 3x3 window, stride 1, dilation 1 and padding 1 on every side (so Ho = H, Wo = W),
 // W a multiple of 8 and at most 56; fp32 accumulation.
 //
-// GEMM view per image: Y^T[p][f] = sum_k X[p][k] W^T[k][f] with p = ho*W + wo and the
-// contraction index k ordered (tap = 3*kh + kw, channel): 18 chunks of 32 = 9 taps x
-// 2 channel halves. In that order 8 consecutive k of one pixel are 8 consecutive channels,
-// so with the input tile stored channel-last in LDS every MFMA operand-A fragment is a
-// single 16-byte read.
+// GEMM view per output row: Y^T[w][f] = sum_k X[w][k] W^T[k][f] with the contraction index k
+// ordered (tap = 3*kh + kw, channel): 36 steps of 16 = 9 taps x 4 channel groups. In that
+// order 8 consecutive k of one pixel are 8 consecutive channels, so with the input tile
+// stored channel-last in LDS an MFMA operand-A fragment (v_mfma_f32_32x32x16: 8 k of one
+// pixel per lane) is one 16-byte read, and so is an operand-B fragment from the reordered
+// weights.
 //
-// Persistent workgroups (one per CU, 4 waves). Each workgroup first rewrites the weights
-// into LDS in that k order: a thread loads the 8 channels x 9 taps of one filter (144
-// contiguous bytes) with 16-byte loads and regroups them per tap with v_perm_b32. It
-// then walks work items (image n, 4 output rows): the 6 input rows an item needs are
-// loaded as 8-channel x 8-column blocks (16-byte loads along W), transposed in registers
-// and written channel-last into a double-buffered LDS tile with one zero column on each
-// side and zero rows outside the image; the next item's rows are fetched while the
-// current one is computed. Wave w computes output row 4i+w for all 64 filters:
-// 4 pixel blocks x 4 filter blocks of v_mfma_f32_16x16x32 per k chunk, operands read
-// from LDS (XOR-swizzled 16-byte chunks). The result layout puts 4 consecutive output
-// columns of one filter in each lane: one 8-byte store.
+// One workgroup (4 waves) per 7 output rows of one image: the C3 shape (N=32, H=56) is 256
+// workgroups, one per CU. The weights (rewritten per tap into k order) and the 9 input
+// rows (8-channel x 8-column blocks loaded along W, transposed in registers and written
+// channel-last, with a zero column on each side and zero rows outside the image) are staged
+// into LDS one channel group of 16 at a time: while the MFMAs of group cg run, the loads of
+// group cg+1 are in flight, so only the first group's ~35 KB is exposed. Wave w owns filter
+// block w >> 1 and pixel block w & 1 (32 each) of all 7 rows: 7 accumulators, and per k step
+// one weight fragment shared by 7 input fragments (252 MFMAs per wave).
+//
+// LDS layout (64 banks of 4 bytes; ds_read_b128 serves 16 lanes per cycle): a pixel of the
+// input tile is 128 bytes (8 chunks of 8 channels); chunk c of column col sits at slot
+// c ^ ((col >> 1) & 7), so 16 consecutive pixels at one chunk hit 16 distinct 16-byte bank
+// groups. A weight fragment (filter f, 8 channels) is 16 bytes at slot h ^ ((f >> 3) & 1)
+// of the filter's 32-byte pair.
 #pragma once
 
 #include "conv2d.h"
+#include "lds_dma.h"
 
 namespace kg_gfx950 {
 
 namespace convk {
 
 constexpr int kThreads = 256;
-constexpr int kRows = 4;               // output rows per work item (one per wave)
-constexpr int kInRows = kRows + 2;     // input rows per item
-constexpr int kCols = 58;              // LDS tile columns: W <= 56 plus two zero columns
+constexpr int kRows = 7;            // output rows per workgroup
+constexpr int kInRows = kRows + 2;  // input rows per workgroup
+constexpr int kCols = 58;           // LDS tile columns: W <= 56 plus two zero columns
 constexpr int kC = 64;
 constexpr int kF = 64;
-constexpr int kKChunks = 18;           // 9 taps x 2 channel halves of 32
-constexpr int kXVecs = kInRows * kCols * 8;   // u32x4 per input tile (8 chunks of 8 channels)
-constexpr int kWVecs = kKChunks * kF * 4;     // u32x4 of reordered weights
+constexpr int kKSteps = 36;                      // 9 taps x 4 groups of 16 channels
+constexpr int kXBytes = kInRows * kCols * 128;   // channel-last input tile
+constexpr int kWBytes = kKSteps * kF * 32;       // weights: 16 channels x 2 bytes per (step, f)
 
-__device__ __forceinline__ int x_swz(int ww) { return (ww & 7) ^ ((ww >> 3) & 7); }
-__device__ __forceinline__ int w_swz(int f) { return (f >> 1) & 3; }
+__host__ __device__ constexpr int x_slot(int col, int c8) { return c8 ^ ((col >> 1) & 7); }
+__host__ __device__ constexpr int w_slot(int f, int h) { return h ^ ((f >> 3) & 1); }
 
 }  // namespace convk
 
@@ -48,188 +53,230 @@ __global__ __launch_bounds__(convk::kThreads, 1) void conv2d_3x3s1p1_mfma_kernel
     const void* __restrict__ bias, int N, int H, int W) {
   using namespace convk;
   using Hf = Half16<Tag>;
-  __shared__ u32x4 w_lds[kWVecs];
-  __shared__ u32x4 x_lds[2][kXVecs];
+  __shared__ __attribute__((aligned(1024))) u32x4 lds[(kXBytes + kWBytes) / 16];
+  u32x4* x_lds = lds;                  // [row][col][8 chunks]
+  u32x4* w_lds = lds + kXBytes / 16;   // [step][f][2 chunks]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int g = lane >> 4;
-  const int r16 = lane & 15;
-
-  // Zero both input tiles once: the border columns and any columns past W stay zero.
-  for (int i = tid; i < 2 * kXVecs; i += kThreads) (&x_lds[0][0])[i] = u32x4{0, 0, 0, 0};
-
-  // Reordered weights: w_lds[(kc*64 + f)*4 + (grp ^ w_swz(f))] holds channels
-  // 32*(kc&1) + 8*grp .. +7 of filter f at tap kc>>1.
-#pragma unroll
-  for (int rep = 0; rep < 2; ++rep) {
-    const int combo = tid + kThreads * rep;  // (filter, channel octet)
-    const int f = combo >> 3;
-    const int co = combo & 7;
-    const uint16_t* src = w + (long long)f * (kC * 9) + co * 72;
-    uint32_t v[36];
-#pragma unroll
-    for (int i = 0; i < 9; ++i) {
-      const u32x4 t = ld16(src + 8 * i);
-      v[4 * i] = t[0];
-      v[4 * i + 1] = t[1];
-      v[4 * i + 2] = t[2];
-      v[4 * i + 3] = t[3];
-    }
-#pragma unroll
-    for (int tap = 0; tap < 9; ++tap) {
-      u32x4 frag;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        // channels 2q and 2q+1 of the octet at this tap: elements (2q)*9+tap, (2q+1)*9+tap
-        const int e0 = (2 * q) * 9 + tap;
-        const int e1 = (2 * q + 1) * 9 + tap;
-        const uint32_t a = v[e0 >> 1];
-        const uint32_t b = v[e1 >> 1];
-        const uint32_t lo = (e0 & 1) ? (a >> 16) : (a & 0xffffu);
-        const uint32_t hi = (e1 & 1) ? (b >> 16) : (b & 0xffffu);
-        frag[q] = lo | (hi << 16);
-      }
-      const int kc = 2 * tap + (co >> 2);
-      const int grp = co & 3;
-      w_lds[(kc * kF + f) * 4 + (grp ^ w_swz(f))] = frag;
-    }
-  }
 
   const int row_blocks = (H + kRows - 1) / kRows;
-  const int items = N * row_blocks;
-  const int wblocks = W >> 3;                  // 8-column blocks per row
-  const int blocks = kInRows * 8 * wblocks;    // 8x8 staging blocks per item
-  constexpr int kMaxRounds = (kInRows * 8 * 7 + kThreads - 1) / kThreads;  // W <= 56
+  const int n = blockIdx.x / row_blocks;
+  const int r0 = (blockIdx.x - n * row_blocks) * kRows;  // first output row
 
-  u32x4 pre[kMaxRounds][8];
-
-  auto load_item = [&](int item) {
-    const int n = item / row_blocks;
-    const int ho0 = (item % row_blocks) * kRows;
+  // ---- staging, one channel group cg (16 channels) at a time ----
+  // Threads 0..127: weights of filter t/2, channel octet 2cg + (t&1) (144 contiguous bytes:
+  // 8 channels x 9 taps). Threads 128..: input blocks (tile row, octet 2cg + (b&1), 8-column
+  // block) of tile rows 0..8 (tile row r holds input row r0 - 1 + r).
+  const int wblocks = W >> 3;
+  const int in_blocks = kInRows * 2 * wblocks;  // <= 126 for W <= 56
+  u32x4 stage[9];
+  auto stage_load = [&](int cg) {
+    if (tid < 128) {
+      const int f = tid >> 1, co = 2 * cg + (tid & 1);
+      const uint16_t* src = w + (long long)f * (kC * 9) + co * 72;
 #pragma unroll
-    for (int rd = 0; rd < kMaxRounds; ++rd) {
-      const int b = tid + kThreads * rd;
+      for (int i = 0; i < 9; ++i) stage[i] = ld16(src + 8 * i);
+    } else {
+      const int b = tid - 128;
       const int wb = b % wblocks;
-      const int co = (b / wblocks) & 7;
-      const int r = b / (wblocks * 8);
-      const int h = ho0 - 1 + r;
-      const bool live = b < blocks && h >= 0 && h < H;
-      const uint16_t* src = x + (((long long)n * kC + 8 * co) * H + h) * W + 8 * wb;
+      const int co = 2 * cg + ((b / wblocks) & 1);
+      const int r = b / (2 * wblocks);
+      const int h = r0 - 1 + r;
+      if (b < in_blocks && h >= 0 && h < H) {
+        const uint16_t* src = x + (((long long)n * kC + 8 * co) * H + h) * W + 8 * wb;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) pre[rd][e] = live ? ld16(src + (long long)e * H * W) : u32x4{0, 0, 0, 0};
+        for (int e = 0; e < 8; ++e) stage[e] = ld16(src + (long long)e * H * W);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) stage[e] = u32x4{0, 0, 0, 0};
+      }
     }
   };
-  auto store_item = [&](int buf) {
+  // w_lds[(step*64 + f)*2 + w_slot(f, h)] holds channels 16*(step&3) + 8h .. +7 of filter f at
+  // tap step>>2; the input tile is channel-last (chunk c of column col at x_slot(col, c)).
+  auto stage_store = [&](int cg) {
+    if (tid < 128) {
+      const int f = tid >> 1, hsel = tid & 1;
 #pragma unroll
-    for (int rd = 0; rd < kMaxRounds; ++rd) {
-      const int b = tid + kThreads * rd;
-      if (b < blocks) {
+      for (int tap = 0; tap < 9; ++tap) {
+        u32x4 frag;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          // channels 2q and 2q+1 of the octet at this tap: elements (2q)*9+tap, (2q+1)*9+tap
+          const int e0 = (2 * q) * 9 + tap;
+          const int e1 = (2 * q + 1) * 9 + tap;
+          const uint32_t a = stage[e0 >> 3][(e0 >> 1) & 3];
+          const uint32_t b = stage[e1 >> 3][(e1 >> 1) & 3];
+          const uint32_t lo = (e0 & 1) ? (a >> 16) : (a & 0xffffu);
+          const uint32_t hi = (e1 & 1) ? (b >> 16) : (b & 0xffffu);
+          frag[q] = lo | (hi << 16);
+        }
+        w_lds[((4 * tap + cg) * kF + f) * 2 + w_slot(f, hsel)] = frag;
+      }
+    } else {
+      const int b = tid - 128;
+      if (b < in_blocks) {
         const int wb = b % wblocks;
-        const int co = (b / wblocks) & 7;
-        const int r = b / (wblocks * 8);
-        u32x4 t[8];
-        transpose8x8_b16(pre[rd], t);
+        const int co = 2 * cg + ((b / wblocks) & 1);
+        const int r = b / (2 * wblocks);
+        u32x4 cols[8];
+        transpose8x8_b16(stage, cols);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const int ww = 1 + 8 * wb + j;
-          x_lds[buf][(r * kCols + ww) * 8 + (co ^ x_swz(ww))] = t[j];
+          const int col = 1 + 8 * wb + j;
+          x_lds[(r * kCols + col) * 8 + x_slot(col, co)] = cols[j];
         }
       }
     }
   };
 
-  int item = blockIdx.x;
-  if (item < items) load_item(item);
-  __syncthreads();  // zero fill and weights complete before the first tile lands
-  if (item < items) store_item(0);
+  stage_load(0);
+  {  // zero columns (0 and W+1 .. kCols-1) of every tile row
+    const int zcols = kCols - W;
+    for (int i = tid; i < kInRows * zcols * 8; i += kThreads) {
+      const int c8 = i & 7;
+      const int zc = (i >> 3) % zcols;
+      const int r = (i >> 3) / zcols;
+      const int col = zc == 0 ? 0 : W + zc;
+      x_lds[(r * kCols + col) * 8 + x_slot(col, c8)] = u32x4{0, 0, 0, 0};
+    }
+  }
+  stage_store(0);
   __syncthreads();
 
-  int cur = 0;
-  for (; item < items; item += gridDim.x) {
-    const int next = item + gridDim.x;
-    if (next < items) load_item(next);
-
-    f32x4 acc[4][4];
+  // ---- compute: wave = (filter block fb, pixel block pb) over all 7 rows ----
+  const int fb = wave >> 1;
+  const int pb = wave & 1;
+  const int f = 32 * fb + (lane & 31);
+  const int hsel = lane >> 5;
+  const bool live = 32 * pb < W;  // wave-uniform
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)&lds[0];
+  // A operand: pixel w = 32pb + lane%32 (dead lanes past W read column W-1), channels
+  // 16cg + 8hsel .. +7 at tap (kh, kw): LDS byte ((r + kh)*58 + w + kw)*128 + 16*slot.
+  const int wpix = min(32 * pb + (lane & 31), W - 1);
+  uint32_t a_off[3][4];
 #pragma unroll
-    for (int pb = 0; pb < 4; ++pb)
+  for (int kw = 0; kw < 3; ++kw)
 #pragma unroll
-      for (int fb = 0; fb < 4; ++fb) acc[pb][fb] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    int wo_lane[4];
-#pragma unroll
-    for (int pb = 0; pb < 4; ++pb) wo_lane[pb] = min(16 * pb + r16, W - 1);  // dead lanes read a live column
-
-#pragma unroll 2
-    for (int kc = 0; kc < kKChunks; ++kc) {
-      const int tap = kc >> 1;
-      const int kh = tap / 3;
-      const int kw = tap - 3 * kh;
-      const int chunk = 4 * (kc & 1) + g;
-      u32x4 a[4], b[4];
-#pragma unroll
-      for (int pb = 0; pb < 4; ++pb) {
-        const int ww = wo_lane[pb] + kw;
-        a[pb] = x_lds[cur][((wave + kh) * kCols + ww) * 8 + (chunk ^ x_swz(ww))];
-      }
-#pragma unroll
-      for (int fb = 0; fb < 4; ++fb) {
-        const int f = 16 * fb + r16;
-        b[fb] = w_lds[(kc * kF + f) * 4 + (g ^ w_swz(f))];
-      }
-#pragma unroll
-      for (int pb = 0; pb < 4; ++pb)
-#pragma unroll
-        for (int fb = 0; fb < 4; ++fb) acc[pb][fb] = Hf::mfma16(a[pb], b[fb], acc[pb][fb]);
+    for (int cg = 0; cg < 4; ++cg) {
+      const int col = wpix + kw;
+      a_off[kw][cg] = lds0 + col * 128 + 16 * x_slot(col, 2 * cg + hsel);
     }
-
-    const int n = item / row_blocks;
-    const int ho = (item % row_blocks) * kRows + wave;
-    if (ho < H) {
+  const uint32_t b_off = lds0 + kXBytes + (f * 2 + w_slot(f, hsel)) * 16;
+  auto read_a = [&](int tap, int cg, int r) -> u32x4 {
+    const int kh = tap / 3, kw = tap - 3 * (tap / 3);
+    return *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(a_off[kw][cg] + (r + kh) * kCols * 128);
+  };
+  auto read_b = [&](int tap, int cg) -> u32x4 {
+    return *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(b_off + (4 * tap + cg) * kF * 32);
+  };
+  // R accumulators (output rows row0 .. row0+R-1), channel group cg: 9 taps x R MFMAs, one
+  // weight fragment shared by the R input fragments of a tap, fragments read a tap ahead.
+  auto compute_cg = [&](auto rows_tag, int row0, int cg, f32x16 (&acc)[decltype(rows_tag)::value]) {
+    constexpr int R = decltype(rows_tag)::value;
+    if (!live) return;
+    u32x4 a_cur[R], a_nxt[R], b_cur, b_nxt;
 #pragma unroll
-      for (int fb = 0; fb < 4; ++fb) {
-        const int f = 16 * fb + r16;
-        float bv = 0.f;
-        if constexpr (kBias == 1) bv = static_cast<const float*>(bias)[f];
-        if constexpr (kBias == 2) bv = Hf::to_float(static_cast<const uint16_t*>(bias)[f]);
-        uint16_t* yrow = y + (((long long)n * kF + f) * H + ho) * W;
+    for (int r = 0; r < R; ++r) a_cur[r] = read_a(0, cg, row0 + r);
+    b_cur = read_b(0, cg);
 #pragma unroll
-        for (int pb = 0; pb < 4; ++pb) {
-          const int wo = 16 * pb + 4 * g;
-          if (wo < W) {
-            const f32x4 v = acc[pb][fb];
-            u32x2 packed;
-            packed[0] = Hf::pack2(v[0] + bv, v[1] + bv);
-            packed[1] = Hf::pack2(v[2] + bv, v[3] + bv);
-            st8(yrow + wo, packed);
-          }
+    for (int tap = 0; tap < 9; ++tap) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        acc[r] = Hf::mfma32(a_cur[r], b_cur, acc[r]);
+        if (tap + 1 < 9) a_nxt[r] = read_a(tap + 1, cg, row0 + r);
+        if (r == 0 && tap + 1 < 9) b_nxt = read_b(tap + 1, cg);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) a_cur[r] = a_nxt[r];
+      b_cur = b_nxt;
+    }
+  };
+  // Output rows row0 .. row0+R-1 go out through LDS (bytes [0, 64*R*2W) of the input tile,
+  // laid out [f][row][w] like Y) so that the HBM writes are whole 16-byte chunks of each
+  // filter plane, consecutive per lane; scattered 8-byte stores from the MFMA layout write
+  // far below HBM speed. Lane holds filter f, pixels 32pb + 8j + 4*hsel + 0..3 of each row.
+  float bv = 0.f;
+  if constexpr (kBias == 1) bv = static_cast<const float*>(bias)[f];
+  if constexpr (kBias == 2) bv = Hf::to_float(static_cast<const uint16_t*>(bias)[f]);
+  char* out_lds = reinterpret_cast<char*>(x_lds);
+  auto stage_out = [&](auto rows_tag, const f32x16 (&acc)[decltype(rows_tag)::value]) {
+    constexpr int R = decltype(rows_tag)::value;
+    if (!live) return;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int wo = 32 * pb + 8 * j + 4 * hsel;
+        if (wo < W) {
+          u32x2 packed;
+          packed[0] = Hf::pack2(acc[r][4 * j] + bv, acc[r][4 * j + 1] + bv);
+          packed[1] = Hf::pack2(acc[r][4 * j + 2] + bv, acc[r][4 * j + 3] + bv);
+          *reinterpret_cast<u32x2*>(out_lds + ((f * R + r) * W + wo) * 2) = packed;
         }
       }
+  };
+  auto flush_out = [&](int R, int row0) {  // rows past H are not written
+    const int ho0 = r0 + row0;
+    const int rv = min(R, H - ho0);
+    if (rv <= 0) return;
+    const int per_f = rv * W / 8;  // 16-byte chunks per filter
+    for (int c = tid; c < kF * per_f; c += kThreads) {
+      const int f2 = c / per_f;
+      const int k = c - f2 * per_f;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(out_lds + f2 * R * W * 2 + 16 * k);
+      st16(y + (((long long)n * kF + f2) * H + ho0) * W + 8 * k, v);
     }
-    if (next < items) store_item(cur ^ 1);
+  };
+
+  constexpr int kRowsA = 4;  // output rows 0..3: tile rows 0..5
+  constexpr int kRowsB = kRows - kRowsA;
+  // ---- group A, staged by channel group: the loads of group cg+1 are in flight while the
+  // MFMAs of group cg run, and land in LDS regions group cg does not read ----
+  f32x16 acc_a[kRowsA];
+#pragma unroll
+  for (int r = 0; r < kRowsA; ++r)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc_a[r][i] = 0.f;
+#pragma unroll
+  for (int cg = 0; cg < 4; ++cg) {
+    if (cg + 1 < 4) stage_load(cg + 1);
+    compute_cg(Int<kRowsA>{}, 0, cg, acc_a);
+    if (cg + 1 < 4) stage_store(cg + 1);
     __syncthreads();
-    cur ^= 1;
   }
+  // ---- A's outputs into tile rows 0..3 (only group A read them), then out to HBM while
+  // group B (output rows 4..6, tile rows 4..8) computes ----
+  stage_out(Int<kRowsA>{}, acc_a);
+  __syncthreads();
+  flush_out(kRowsA, 0);
+  f32x16 acc_b[kRowsB];
+#pragma unroll
+  for (int r = 0; r < kRowsB; ++r)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc_b[r][i] = 0.f;
+#pragma unroll
+  for (int cg = 0; cg < 4; ++cg) compute_cg(Int<kRowsB>{}, kRowsA, cg, acc_b);
+  __syncthreads();  // every wave has read A's outputs back and finished group B
+  stage_out(Int<kRowsB>{}, acc_b);
+  __syncthreads();
+  flush_out(kRowsB, kRowsA);
 }
 
 inline bool conv_mfma_supported(const ConvShape& s) {
   return s.c == convk::kC && s.f == convk::kF && s.kh == 3 && s.kw == 3 && s.sh == 1 && s.sw == 1 && s.dh == 1 &&
          s.dw == 1 && s.pt == 1 && s.pl == 1 && s.ho == s.h && s.wo == s.w && s.w % 8 == 0 && s.w >= 8 &&
-         s.w <= convk::kCols - 2 && s.h >= 1 && s.n >= 1;
+         s.w <= convk::kCols - 2 && s.h >= 1 && s.n >= 1 &&
+         (long long)s.n * ((s.h + convk::kRows - 1) / convk::kRows) < (1ll << 31);
 }
 
 template <typename Tag>
 hipError_t launch_conv2d_mfma(const uint16_t* x, const uint16_t* w, uint16_t* y, const void* bias, int bias_kind,
                               const ConvShape& s, hipStream_t stream) {
-  int cus = 256;
-  int dev = 0;
-  if (hipGetDevice(&dev) == hipSuccess) {
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
-  }
-  const long long items = (long long)s.n * ((s.h + convk::kRows - 1) / convk::kRows);
-  const int grid = (int)(items < cus ? items : cus);
+  const int grid = s.n * ((s.h + convk::kRows - 1) / convk::kRows);
   if (bias_kind == 1)
     hipLaunchKernelGGL((conv2d_3x3s1p1_mfma_kernel<Tag, 1>), dim3(grid), dim3(convk::kThreads), 0, stream, x, w, y, bias,
                        s.n, s.h, s.w);
