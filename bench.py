@@ -133,7 +133,7 @@ def secondary(dev, steps: int, warmup: int, only=None):
     out = []
     keys = set(SECONDARY_KEYS if only is None else only)
 
-    def add(name, flop, call, peak, nsteps, byts=None):
+    def add(name, flop, call, peak, nsteps, byts=None, traffic_file=None):
         wall, ev = time_steps(call, nsteps, max(2, warmup // 2))
         tf = flop / (ev * 1e-3) / 1e12
         rec = {"workload": name, "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ev, 5),
@@ -142,6 +142,8 @@ def secondary(dev, steps: int, warmup: int, only=None):
             gbs = byts / (ev * 1e-3) / 1e9
             rec["hbm_gbs"] = round(gbs, 1)
             rec["hbm_frac"] = round(gbs / PEAK_HBM_GBS, 4)
+        if traffic_file is not None:
+            rec["traffic"] = read_traffic(REPO_ROOT / "profiles" / traffic_file)  # measured HBM bytes per launch
         log(f"[bench] {name}: {ev * 1e3:.1f} us  {tf:.1f} TFLOP/s  wall/step {wall * 1e3:.1f} us")
         out.append(rec)
 
@@ -187,7 +189,7 @@ def c3(dev, add, steps):
     conv_bytes = 2 * (32 * 64 * 56 * 56 * 2) + 64 * 64 * 9 * 2
     add("C3 fp16 conv2d N=32 C=64 H=W=56 F=64 3x3 s1 p1", 2 * 32 * 64 * 56 * 56 * 64 * 9,
         PreparedCall("kg_gfx950_conv2d_entry", (y, x, w, None, 1, 1, 1, 1, 1, 1, 1, 1)), PEAK_BF16_TFLOPS,
-        max(steps, 50), conv_bytes)
+        max(steps, 50), conv_bytes, "conv2d_fp16_c3_traffic.txt")
 
 
 def c4(dev, add, steps):
@@ -198,7 +200,7 @@ def c4(dev, add, steps):
     o = torch.empty_like(q)
     add("C4 bf16 flash-attn fwd B=4 H=32 S=2048 D=128 non-causal", 4 * 4 * 32 * 2048 * 2048 * 128,
         PreparedCall("kg_gfx950_flash_attention_entry", (o, q, k, v, 128, 64, 1.0 / math.sqrt(128.0), 0)),
-        PEAK_BF16_TFLOPS, steps)
+        PEAK_BF16_TFLOPS, steps, None, "flash_attn_bf16_c4_traffic.txt")
 
 
 def c5(dev, add, steps, d):
@@ -271,7 +273,7 @@ def main() -> int:
         "data": "synthetic: A,B ~ N(0,1)*0.02 (seeded torch generator on the device), resident in HBM",
         "config": {
             "workload": "bf16 matmul M=N=K=4096, row-major A[M,K] B[K,N], fp32 accumulate, bf16 out (BASELINE configs[1])",
-            "M": m, "N": n, "K": k, "kernel": "gemm_mfma_kernel 256x256x64, v_mfma_f32_16x16x32_bf16",
+            "M": m, "N": n, "K": k, "kernel": "gemm_pipe_kernel 256x256 tiles, 4-stage HBM->LDS ring, v_mfma_f32_32x32x16_bf16",
         },
         "roofline": {
             "bound": "mfma",
