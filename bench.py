@@ -273,7 +273,7 @@ def main() -> int:
         "data": "synthetic: A,B ~ N(0,1)*0.02 (seeded torch generator on the device), resident in HBM",
         "config": {
             "workload": "bf16 matmul M=N=K=4096, row-major A[M,K] B[K,N], fp32 accumulate, bf16 out (BASELINE configs[1])",
-            "M": m, "N": n, "K": k, "kernel": "gemm_pipe_kernel 256x256 tiles, 4-stage HBM->LDS ring, v_mfma_f32_32x32x16_bf16",
+            "M": m, "N": n, "K": k, "kernel": "gemm_pipe_kernel 256x256 tiles, 8 waves, 4-stage HBM->LDS ring, v_mfma_f32_32x32x16_bf16",
         },
         "roofline": {
             "bound": "mfma",

@@ -213,23 +213,26 @@ __global__ __launch_bounds__(gemm::kThreads, 1) void gemm_mfma_kernel(
 }
 
 // gemm_pipe_kernel: the aligned-shape path (M % 256 == 0, N % 256 == 0, K % 32 == 0).
-//   Same 256x256 tile and 2x2 waves of 128x128 with 32x32x16 MFMAs, but both operands are
-//   copied HBM -> LDS by global_load_lds_dwordx4 (no registers, no VALU work) through a
-//   4-stage ring of 32-deep K slices (4 x 32 KiB), so loads are issued three slices ahead
-//   of their use. lhs slices are [m][k] rows of 64 bytes; rhs slices stay [k][n] as in HBM
-//   and the MFMA operand (8 consecutive k of one n) is read with two ds_read_b64_tr_b16:
-//   within each 16-lane group, lane j addresses 4 consecutive n of k-row j/4 and lane i
-//   receives k-rows 0..3 of column i. Chunk swizzles: lhs p = c ^ ((row >> 2) & 3),
-//   rhs p = c ^ 4(k & 3) -- the fragment reads hit distinct banks of the 64-bank LDS.
-//   Fragments are double-buffered in registers: while the MFMAs of one 16-deep half of a
-//   slice run, the other half (or the next slice's first half) is being read, and the
-//   per-slice barrier sits between the two halves.
+//   256x256 tiles computed by 8 waves (2 x 4 waves of 128x64, two per SIMD) with 32x32x16
+//   MFMAs. Both operands are copied HBM -> LDS by global_load_lds_dwordx4 (no registers, no
+//   VALU work) through a 4-stage ring of 32-deep K slices (4 x 32 KiB), so loads are issued
+//   three slices ahead of their use; every wave issues 4 of a slice's 32 copies, slotted
+//   between its MFMAs, and while one wave of a SIMD waits on a copy's issue or an LDS read
+//   the other keeps the MFMA pipe busy. lhs slices are [m][k] rows of 64 bytes; rhs slices
+//   stay [k][n] as in HBM and the MFMA operand (8 consecutive k of one n) is read with two
+//   ds_read_b64_tr_b16: within each 16-lane group, lane j addresses 4 consecutive n of
+//   k-row j/4 and lane i receives k-rows 0..3 of column i. Chunk swizzles: lhs
+//   p = c ^ ((row >> 2) & 3), rhs p = c ^ 4(k & 3) -- the fragment reads hit distinct
+//   banks of the 64-bank LDS. Fragments are double-buffered in registers: while the MFMAs
+//   of one 16-deep half of a slice run, the other half (or the next slice's first half) is
+//   being read, and the per-slice barrier sits between the two halves.
 namespace gemmp {
 constexpr int kBM = 256;
 constexpr int kBN = 256;
 constexpr int kBK = 32;
 constexpr int kStages = 4;
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;  // 8 waves: 2 x 4 of 128 x 64, two per SIMD
+constexpr int kPieces = 4;     // copies per wave per slice: 2 lhs, 2 rhs
 constexpr int kAVecs = kBM * kBK / 8;  // 1024 u32x4 per lhs stage
 constexpr int kBVecs = kBK * kBN / 8;  // 1024 u32x4 per rhs stage
 // LDS has 64 banks of 4 bytes: ds_read_b128 serves 16 lanes per cycle, 64-bit reads 32.
@@ -256,8 +259,8 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1;
-  const int wn = wave & 1;
+  const int wm = wave >> 2;  // 128-row half of the tile
+  const int wn = wave & 3;   // 64-column quarter
 
   const int tiles_n = N / kBN;
   const int tiles_m = M / kBM;
@@ -272,35 +275,32 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
   const int n0 = (in_group / gm) * kBN;
 
   // ---- HBM -> LDS copies ----
-  // Copy piece p < 4: lhs rows (wave*4+p)*16 + lane/4; the swizzle mask of a row depends on
-  // row>>2 & 3 only, so all four pieces share one per-lane offset and differ by 16 rows.
-  // Copy piece 4+p: rhs k-rows (wave*4+p)*2 + lane/32; the mask depends on k & 3, so pieces
-  // 0/2 and 1/3 share offsets and differ by 4 k-rows.
-  const int a_row0 = wave * 64 + (lane >> 2);
+  // Piece p < 2: lhs rows (wave*2+p)*16 + lane/4 (a_mask depends on lane only, so one
+  // per-lane offset and 16 rows between pieces). Piece 2+p: rhs k-rows (wave*2+p)*2 +
+  // lane/32 (b_mask depends on p and lane).
+  const int a_row0 = wave * 32 + (lane >> 2);
   const uint32_t a_goff = (uint32_t)((a_row0 * lda + 8 * ((lane & 3) ^ a_mask(a_row0))) * 2);
   uint32_t b_goff[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int k = (wave * 4 + i) * 2 + (lane >> 5);
+    const int k = (wave * 2 + i) * 2 + (lane >> 5);
     b_goff[i] = (uint32_t)((k * ldb + 8 * ((lane & 31) ^ b_mask(k))) * 2);
   }
   const char* a_tile = reinterpret_cast<const char*>(A + (long long)m0 * lda);
   const char* b_tile = reinterpret_cast<const char*>(B + n0);
   const long long a_piece = 16 * lda * 2;
-  const long long b_piece = 4 * ldb * 2;
   const long long b_step = (long long)kBK * ldb * 2;
-  const uint32_t lds_a0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)&lds_a[0][0];
-  const uint32_t lds_b0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)&lds_b[0][0];
+  const uint32_t lds_a0 = lds_addr(&lds_a[0][0]);
+  const uint32_t lds_b0 = lds_addr(&lds_b[0][0]);
   constexpr uint32_t kStageBytes = kAVecs * 16;  // == kBVecs * 16
 
-  auto issue_piece = [&](int kt, int s, int piece) {  // piece 0..7: 4 lhs then 4 rhs
-    if (piece < 4) {
+  auto issue_piece = [&](int kt, int s, int piece) {  // piece 0..3: 2 lhs then 2 rhs
+    if (piece < 2) {
       g2lds16_s(a_goff, a_tile + (long long)kt * kBK * 2 + piece * a_piece,
-                lds_a0 + s * kStageBytes + (wave * 4 + piece) * 1024);
+                lds_a0 + s * kStageBytes + (wave * 2 + piece) * 1024);
     } else {
-      const int i = piece - 4;
-      g2lds16_s(b_goff[i & 1], b_tile + kt * b_step + (i >> 1) * b_piece,
-                lds_b0 + s * kStageBytes + (wave * 4 + i) * 1024);
+      const int i = piece - 2;
+      g2lds16_s(b_goff[i], b_tile + kt * b_step, lds_b0 + s * kStageBytes + (wave * 2 + i) * 1024);
     }
   };
 
@@ -313,20 +313,20 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
   const int j16 = lane & 15;
   const int b_nofs = 16 * (g & 1) + 4 * (j16 & 3);
   const int b_kofs = 8 * (g >> 1) + (j16 >> 2);
-  uint32_t a_rd[2], b_rd[4];
+  uint32_t a_rd[2], b_rd[2];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) a_rd[ks] = lds_a0 + a_slot(wm * 128 + frag_row, 2 * ks + frag_half) * 16;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int n = wn * 128 + j * 32 + b_nofs;
+  for (int j = 0; j < 2; ++j) {
+    const int n = wn * 64 + j * 32 + b_nofs;
     b_rd[j] = lds_b0 + b_slot(b_kofs, n >> 3) * 16 + (n & 7) * 2;
   }
 
   struct Frag {
     u32x4 a[4];
-    u32x4 b[4];
+    u32x4 b[2];
   };
-  // read #r (0..11) of a fragment set: 4 lhs b128 reads, then 8 rhs transposed reads
+  // read #r (0..7) of a fragment set: 4 lhs b128 reads, then 4 rhs transposed reads
   auto read_piece = [&](int s, int ks, Frag& f, int r) {
     if (r < 4) {
       f.a[r] = *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(a_rd[ks] + s * kStageBytes + r * 2048);
@@ -340,11 +340,11 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
     }
   };
 
-  f32x16 acc[4][4];
+  f32x16 acc[4][2];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
@@ -353,17 +353,17 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
   for (int st = 0; st < kStages; ++st)
     if (st < ktiles)
 #pragma unroll
-      for (int piece = 0; piece < 8; ++piece) issue_piece(st, st, piece);
+      for (int piece = 0; piece < kPieces; ++piece) issue_piece(st, st, piece);
   {
     const int younger = min(kStages - 1, ktiles - 1);
-    if (younger >= 3) wait_and_barrier<24>();
-    else if (younger == 2) wait_and_barrier<16>();
-    else if (younger == 1) wait_and_barrier<8>();
+    if (younger >= 3) wait_and_barrier<3 * kPieces>();
+    else if (younger == 2) wait_and_barrier<2 * kPieces>();
+    else if (younger == 1) wait_and_barrier<kPieces>();
     else wait_and_barrier<0>();
   }
   Frag f0, f1;
 #pragma unroll
-  for (int r = 0; r < 12; ++r) read_piece(0, 0, f0, r);
+  for (int r = 0; r < 8; ++r) read_piece(0, 0, f0, r);
 
   // One 32-deep slice in stage S: MFMAs of half 0 with the reads of half 1 slotted in
   // between, barrier, MFMAs of half 1 with the next slice's first reads and this stage's
@@ -372,41 +372,41 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
     constexpr int S = decltype(stage_tag)::value;
     constexpr bool kSteady = decltype(steady_tag)::value != 0;
 #pragma unroll
-    for (int idx = 0; idx < 16; ++idx) {
-      const int i = idx >> 2, j = idx & 3;
+    for (int idx = 0; idx < 8; ++idx) {
+      const int i = idx >> 1, j = idx & 1;
       acc[i][j] = H::mfma32(f0.b[j], f0.a[i], acc[i][j]);
-      if (idx < 12) read_piece(S, 1, f1, idx);
+      read_piece(S, 1, f1, idx);
       __builtin_amdgcn_sched_barrier(0);
     }
     const bool more = kSteady || kt + 1 < ktiles;
     const bool refill = kSteady || kt + kStages < ktiles;
     if (kSteady) {
-      wait_and_barrier<16>();
+      wait_and_barrier<2 * kPieces>();
     } else if (more) {
       const int younger = min(kStages - 2, ktiles - 2 - kt);
-      if (younger >= 2) wait_and_barrier<16>();
-      else if (younger == 1) wait_and_barrier<8>();
+      if (younger >= 2) wait_and_barrier<2 * kPieces>();
+      else if (younger == 1) wait_and_barrier<kPieces>();
       else wait_and_barrier<0>();
     }
     if (kSteady) {
 #pragma unroll
-      for (int idx = 0; idx < 16; ++idx) {
-        const int i = idx >> 2, j = idx & 3;
+      for (int idx = 0; idx < 8; ++idx) {
+        const int i = idx >> 1, j = idx & 1;
         acc[i][j] = H::mfma32(f1.b[j], f1.a[i], acc[i][j]);
-        if (idx < 12) read_piece((S + 1) % kStages, 0, f0, idx);
-        if (idx >= 4 && idx < 12) issue_piece(kt + kStages, S, idx - 4);
+        read_piece((S + 1) % kStages, 0, f0, idx);
+        if (idx & 1) issue_piece(kt + kStages, S, idx >> 1);
         __builtin_amdgcn_sched_barrier(0);
       }
     } else {
       if (refill)
 #pragma unroll
-        for (int piece = 0; piece < 8; ++piece) issue_piece(kt + kStages, S, piece);
+        for (int piece = 0; piece < kPieces; ++piece) issue_piece(kt + kStages, S, piece);
       if (more)
 #pragma unroll
-        for (int r = 0; r < 12; ++r) read_piece((S + 1) % kStages, 0, f0, r);
+        for (int r = 0; r < 8; ++r) read_piece((S + 1) % kStages, 0, f0, r);
 #pragma unroll
-      for (int idx = 0; idx < 16; ++idx) {
-        const int i = idx >> 2, j = idx & 3;
+      for (int idx = 0; idx < 8; ++idx) {
+        const int i = idx >> 1, j = idx & 1;
         acc[i][j] = H::mfma32(f1.b[j], f1.a[i], acc[i][j]);
       }
     }
@@ -430,10 +430,10 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
   for (int i = 0; i < 4; ++i) {
     const int m = m0 + wm * 128 + i * 32 + frag_row;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 2; ++j) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int n = n0 + wn * 128 + j * 32 + 8 * q + 4 * frag_half;
+        const int n = n0 + wn * 64 + j * 32 + 8 * q + 4 * frag_half;
         float v0 = acc[i][j][4 * q], v1 = acc[i][j][4 * q + 1], v2 = acc[i][j][4 * q + 2], v3 = acc[i][j][4 * q + 3];
         if constexpr (kBias == 1) {
           const float* bp = static_cast<const float*>(bias);
