@@ -114,10 +114,13 @@ def test_general_params_f32(device, oracle_mod, xs, ws, stride, dil, pad):
 @pytest.mark.parametrize(
     "xs,ws,bias",
     [
-        ((2, 64, 56, 56), (64, 64, 3, 3), False),  # C3 geometry, 2 images
-        ((1, 64, 12, 20), (64, 64, 3, 3), True),
-        ((3, 16, 9, 13), (32, 16, 3, 3), True),
-        ((1, 8, 7, 7), (5, 8, 3, 3), False),
+        ((2, 64, 56, 56), (64, 64, 3, 3), None),  # C3 geometry, 2 images (MFMA path)
+        ((1, 64, 12, 24), (64, 64, 3, 3), "f32"),  # MFMA: 7-row blocks with a 5-row tail, W <= 32
+        ((3, 64, 20, 40), (64, 64, 3, 3), "h16"),  # MFMA: 6-row tail, second pixel block partly live
+        ((1, 64, 1, 8), (64, 64, 3, 3), "f32"),  # MFMA: one row, one 8-column block
+        ((1, 64, 12, 20), (64, 64, 3, 3), "f32"),  # W % 8 != 0: direct kernel
+        ((3, 16, 9, 13), (32, 16, 3, 3), "f32"),
+        ((1, 8, 7, 7), (5, 8, 3, 3), None),
     ],
 )
 def test_16bit_3x3(device, oracle_mod, dtype_name, xs, ws, bias):
@@ -128,10 +131,14 @@ def test_16bit_3x3(device, oracle_mod, dtype_name, xs, ws, bias):
     xt, x = round_to(rng.standard_normal(xs), dt)
     bound = np.sqrt(6.0 / (ws[1] * 9))
     wt, w = round_to(rng.uniform(-bound, bound, size=ws), dt)
-    b = rng.normal(size=(ws[0],)).astype(np.float32) if bias else None
+    b = bt = None
+    if bias == "f32":
+        b = bt = rng.normal(size=(ws[0],)).astype(np.float32)
+    elif bias == "h16":  # bias in the output format
+        bt, b = round_to(rng.normal(size=(ws[0],)).astype(np.float32), dt)
     ref = oracle_mod.conv2d_demo(x, w, b, (1, 1), (1, 1), (1, 1, 1, 1), (16, 16, 1, 8, 16))
-    out = run(device, dt, xt, wt, b, (1, 1), (1, 1), (1, 1, 1, 1))
-    assert_h16_close(to_numpy(out), ref, what=f"{dtype_name} {xs}")
+    out = run(device, dt, xt, wt, bt, (1, 1), (1, 1), (1, 1, 1, 1))
+    assert_h16_close(to_numpy(out), ref, what=f"{dtype_name} {xs} bias={bias}")
 
 
 def test_c3_full_size_fp16(device, oracle_mod):

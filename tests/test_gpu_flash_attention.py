@@ -89,6 +89,11 @@ def test_extensions_f32(device, oracle_mod, scale, causal):
         ((1, 1, 300, 128), False),  # ragged S
         ((1, 1, 200, 64), True),  # ragged S, causal
         ((1, 2, 257, 48), False),  # demo-like D
+        ((1, 2, 700, 128), True),  # ragged causal over several 256-query blocks
+        ((2, 3, 130, 128), False),  # one partial query block, ragged key tail
+        ((1, 1, 64, 128), True),  # a single key tile
+        ((1, 2, 1, 128), False),  # one query, one key
+        ((1, 1, 1000, 64), True),  # D=64 ragged causal over several 128-query blocks
     ],
 )
 def test_16bit(device, oracle_mod, dtype_name, shape, causal):
