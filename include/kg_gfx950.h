@@ -113,6 +113,32 @@ const char* kg_gfx950_last_error(void);
 /* ABI revision of this library (bumped on any slot-contract change). */
 int kg_gfx950_abi_version(void);
 
+/* Operations and cost kinds of kg_gfx950_cost. */
+enum {
+  KG_OP_MATMUL = 1,
+  KG_OP_CONV2D = 2,
+  KG_OP_FLASH_ATTENTION = 3
+};
+enum {
+  KG_COST_MAC = 0,       /* multiply-accumulates of the operation (mask-kept pairs for causal attention) */
+  KG_COST_MFMA = 1,      /* wave-level MFMA instructions the chosen kernel issues (0 on SIMT paths) */
+  KG_COST_HBM_READ = 2,  /* compulsory bytes read: every input element once */
+  KG_COST_HBM_WRITE = 3, /* compulsory bytes written: every output element once */
+  KG_COST_KINDS = 4
+};
+
+/*
+ * Static cost of one call, without a GPU: replaces the reference's dsl_cost_run
+ * (kernel_gen/tools/dsl_run.py:656-730), which runs the npu_demo cost pipeline and
+ * returns one integer per cost kind (DMA1..DMA4, MAC, VECTOR1, VECTOR2). op is a
+ * KG_OP_* code; ordered_args/arg_count are exactly the slots the matching entry above
+ * takes (memory slots need shapes, strides and dtypes; their data pointers are not
+ * read). The entry's own validation and kernel choice run unchanged, so a call the
+ * entry would reject fails here with the same code and message. On success writes
+ * KG_COST_KINDS values to costs[] and returns 0.
+ */
+int kg_gfx950_cost(int op, const KgArgSlot* ordered_args, unsigned long long arg_count, long long* costs);
+
 #ifdef __cplusplus
 }
 #endif

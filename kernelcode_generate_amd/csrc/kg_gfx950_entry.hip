@@ -6,6 +6,7 @@
 // configured stream and, in the default synchronous mode, waits for it.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -50,6 +51,14 @@ int finish_launch(const char* what) {
   g_last_error[0] = '\0';
   return kOk;
 }
+
+// Cost queries (kg_gfx950_cost) run the entries' validation and dispatch with this set:
+// pointers are not dereferenced or checked, and each dispatch point records the chosen
+// kernel's per-launch cost instead of launching.
+struct CostOut {
+  long long v[KG_COST_KINDS];
+};
+thread_local CostOut* g_cost = nullptr;
 
 // A memory slot viewed with its element shape/strides.
 struct Mem {
@@ -118,7 +127,7 @@ int read_mem(const KgArgSlot* slots, int idx, int rank, bool allow_absent, const
     if (s.shape[i] == 0) empty = true;
     else last += (s.shape[i] - 1) * s.stride[i];
   }
-  if (empty) return kOk;
+  if (empty || g_cost != nullptr) return kOk;
   // The kernels dereference these pointers on the GPU: refuse host memory and views that
   // run past the end of their device allocation instead of faulting the device.
   hipPointerAttribute_t attr;
@@ -159,7 +168,17 @@ int read_float(const KgArgSlot* slots, int idx, const char* name, double* out) {
   return fail(kInvalid, "slot %d (%s): expected float slot, got kind %d", idx, name, s.kind);
 }
 
-bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+// (cost queries model device buffers, which are always 256-byte aligned)
+bool aligned16(const void* p) { return g_cost != nullptr || ((uintptr_t)p & 15u) == 0; }
+
+int record_cost(long long mac, long long mfma, long long read, long long write) {
+  g_cost->v[KG_COST_MAC] = mac;
+  g_cost->v[KG_COST_MFMA] = mfma;
+  g_cost->v[KG_COST_HBM_READ] = read;
+  g_cost->v[KG_COST_HBM_WRITE] = write;
+  return kOk;
+}
+long long esize(int dtype) { return dtype == KG_DTYPE_F32 ? 4 : 2; }
 
 int grid_1d(long long total, int threads) {
   long long blocks = (total + threads - 1) / threads;
@@ -247,16 +266,28 @@ int matmul_impl(const KgArgSlot* args, unsigned long long n) {
                 dtype_name(rhs.dtype), dtype_name(out.dtype));
   if (bias.present && bias.dtype != out.dtype && bias.dtype != KG_DTYPE_F32)
     return fail(kInvalid, "matmul: bias dtype %s must be f32 or match out", dtype_name(bias.dtype));
-  if (M == 0 || N == 0) return finish_launch("matmul(empty)");
   const int m = (int)M, nn = (int)N, k = (int)K;
+  const bool mfma_ok = out.dtype != KG_DTYPE_F32 && k > 0 && (k % 8 == 0) && (nn % 8 == 0) && lhs.stride[1] == 1 &&
+                       rhs.stride[1] == 1 && out.stride[1] == 1 && lhs.stride[0] % 8 == 0 && rhs.stride[0] % 8 == 0 &&
+                       out.stride[0] % 8 == 0 && aligned16(lhs.data) && aligned16(rhs.data) && aligned16(out.data) &&
+                       (!bias.present || bias.stride[0] == 1);
+  if (g_cost) {
+    long long mfma = 0;
+    if (mfma_ok && M > 0 && N > 0) {
+      const bool pipe = M % gemmp::kBM == 0 && N % gemmp::kBN == 0 && K % gemm::kBK == 0;
+      if (pipe)  // 8 waves x 16 MFMAs (32x32x16) per 32-deep slice of a 256x256 tile
+        mfma = (M / gemmp::kBM) * (N / gemmp::kBN) * (K / gemmp::kBK) * 128;
+      else  // 4 waves x 64 MFMAs per 64-deep slice of a 256x256 tile
+        mfma = ((M + gemm::kBM - 1) / gemm::kBM) * ((N + gemm::kBN - 1) / gemm::kBN) * ((K + gemm::kBK - 1) / gemm::kBK) * 256;
+    }
+    const long long es = esize(out.dtype);
+    return record_cost(M * N * K, mfma, (M * K + K * N) * es + (bias.present ? N * esize(bias.dtype) : 0), M * N * es);
+  }
+  if (M == 0 || N == 0) return finish_launch("matmul(empty)");
 
   if (out.dtype == KG_DTYPE_F32) {
     return launch_gemm_simt<float, float>(out, lhs, rhs, bias, m, nn, k);
   }
-  const bool mfma_ok = k > 0 && (k % 8 == 0) && (nn % 8 == 0) && lhs.stride[1] == 1 && rhs.stride[1] == 1 &&
-                       out.stride[1] == 1 && lhs.stride[0] % 8 == 0 && rhs.stride[0] % 8 == 0 &&
-                       out.stride[0] % 8 == 0 && aligned16(lhs.data) && aligned16(rhs.data) && aligned16(out.data) &&
-                       (!bias.present || bias.stride[0] == 1);
   if (out.dtype == KG_DTYPE_BF16) {
     if (mfma_ok) return launch_gemm_mfma<Bf16Tag>(out, lhs, rhs, bias, m, nn, k);
     if (bias.present && bias.dtype == KG_DTYPE_F32) return launch_gemm_simt<__bf16, float>(out, lhs, rhs, bias, m, nn, k);
@@ -334,6 +365,15 @@ int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
     return fail(kInvalid, "conv2d: out shape [%lld,%lld,%lld,%lld] != [%lld,%lld,%lld,%lld]", out.shape[0], out.shape[1],
                 out.shape[2], out.shape[3], x.shape[0], w.shape[0], ho, wo);
   if (bias.present && bias.shape[0] != w.shape[0]) return fail(kInvalid, "conv2d: bias extent != F");
+  if (g_cost) {
+    long long mfma = 0;
+    if (out.dtype != KG_DTYPE_F32 && conv_mfma_supported(s))  // live waves x 252 MFMAs per 7-row block
+      mfma = (long long)s.n * ((s.h + convk::kRows - 1) / convk::kRows) * (s.w > 32 ? 4 : 2) * 252;
+    const long long es = esize(out.dtype);
+    return record_cost(out.numel() * w.shape[1] * w.shape[2] * w.shape[3], mfma,
+                       (x.numel() + w.numel()) * es + (bias.present ? bias.shape[0] * esize(bias.dtype) : 0),
+                       out.numel() * es);
+  }
   if (out.numel() == 0) return finish_launch("conv2d(empty)");
 
   if (out.dtype == KG_DTYPE_F16 && conv_mfma_supported(s) && aligned16(x.data) && aligned16(w.data) && aligned16(out.data)) {
@@ -415,9 +455,29 @@ int flash_attention_impl(const KgArgSlot* args, unsigned long long n) {
   s.d = (int)q.shape[3];
   s.scale = (float)scale;
   s.causal = (int)causal;
-  if (out.numel() == 0) return finish_launch("flash_attention(empty)");
+  if (g_cost == nullptr && out.numel() == 0) return finish_launch("flash_attention(empty)");
   if (s.d > 512) return fail(kUnsupported, "flash_attention: head dim %d > 512", s.d);
   if (s.causal && s.s_kv != s.s_q) return fail(kUnsupported, "flash_attention: causal mask needs S_q == S_kv");
+  if (g_cost) {
+    const long long B_H = (long long)s.bh, D = s.d;
+    // products Q.K^T and P.V that the mask keeps: causal row i sees keys 0..i
+    const long long pairs = s.causal ? (long long)s.s_q * (s.s_q + 1) / 2 : (long long)s.s_q * s.s_kv;
+    long long mfma = 0;
+    if ((out.dtype == KG_DTYPE_BF16 || out.dtype == KG_DTYPE_F16) && fa_mfma_supported(s) && out.numel() > 0) {
+      // per workgroup: waves x key tiles x (D/8 MFMAs for S^T + D/8 for PV)
+      const int waves = s.d == 128 ? fa::Cfg<128>::kWaves : fa::Cfg<64>::kWaves;
+      const int bm = 32 * waves;
+      const int nmb = (s.s_q + bm - 1) / bm;
+      long long tiles = 0;
+      for (int mb = 0; mb < nmb; ++mb) {
+        const int n_end = s.causal ? std::min(s.s_kv, (mb + 1) * bm) : s.s_kv;
+        tiles += (n_end + fa::kBC - 1) / fa::kBC;
+      }
+      mfma = B_H * tiles * waves * (s.d / 4);
+    }
+    const long long es = esize(out.dtype);
+    return record_cost(2 * B_H * pairs * D, mfma, (q.numel() + k.numel() + v.numel()) * es, out.numel() * es);
+  }
 
   if ((out.dtype == KG_DTYPE_BF16 || out.dtype == KG_DTYPE_F16) && fa_mfma_supported(s) && aligned16(q.data) &&
       aligned16(k.data) && aligned16(v.data) && aligned16(out.data)) {
@@ -461,6 +521,25 @@ int kg_gfx950_set_launch_mode(int synchronous, void* stream) {
 }
 
 const char* kg_gfx950_last_error(void) { return g_last_error; }
+
+int kg_gfx950_cost(int op, const KgArgSlot* ordered_args, unsigned long long arg_count, long long* costs) {
+  if (costs == nullptr) return fail(kInvalid, "cost: output array is null");
+  CostOut out{};
+  g_cost = &out;
+  int rc;
+  switch (op) {
+    case KG_OP_MATMUL: rc = matmul_impl(ordered_args, arg_count); break;
+    case KG_OP_CONV2D: rc = conv2d_impl(ordered_args, arg_count); break;
+    case KG_OP_FLASH_ATTENTION: rc = flash_attention_impl(ordered_args, arg_count); break;
+    default: rc = fail(kInvalid, "cost: unknown op %d", op);
+  }
+  g_cost = nullptr;
+  if (rc == kOk) {
+    for (int i = 0; i < KG_COST_KINDS; ++i) costs[i] = out.v[i];
+    g_last_error[0] = '\0';
+  }
+  return rc;
+}
 
 int kg_gfx950_abi_version(void) { return 1; }
 

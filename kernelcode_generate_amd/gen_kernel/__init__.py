@@ -20,7 +20,7 @@ from __future__ import annotations
 
 import hashlib
 from dataclasses import dataclass, field
-from typing import Callable
+from typing import Callable, Sequence
 
 from ..core.error import ErrorKind, ErrorModule, KernelCodeError
 
@@ -120,6 +120,19 @@ def gen_kernel(pattern: KernelPattern) -> str:
         lines.append(f"  return {entry}(slots, {total}ULL);")
     lines += ["}", ""]
     return "\n".join(lines)
+
+
+def forward_args(pattern: KernelPattern, args: Sequence) -> tuple:
+    """The slot list the generated entry forwards to the library entry for ``args``: the
+    runtime args with the baked constants inserted at ``insert_at`` and the trailing
+    constants appended (the same order gen_kernel writes into kernel.hip)."""
+
+    args = tuple(args)
+    if len(args) != len(pattern.params):
+        raise _error(f"{pattern.function}: expected {len(pattern.params)} args, got {len(args)}")
+    baked = tuple(value for _, value in pattern.baked)
+    trailing = tuple(value for _, value in pattern.trailing)
+    return args[: pattern.insert_at] + baked + args[pattern.insert_at:] + trailing
 
 
 # ------------------------------------------------------------------------------------
@@ -239,5 +252,5 @@ register_pattern("flash_attention_inputs_dynamic_tile_dynamic_kernel",
 register_pattern("flash_attention_scaled_kernel", _fa_scaled("flash_attention_scaled_kernel", False))
 register_pattern("flash_attention_scaled_causal_kernel", _fa_scaled("flash_attention_scaled_causal_kernel", True))
 
-__all__ = ["BUNDLE_MARKER_PREFIX", "ENTRY_POINT", "KernelPattern", "gen_kernel", "known_patterns", "recognise",
-           "register_pattern"]
+__all__ = ["BUNDLE_MARKER_PREFIX", "ENTRY_POINT", "KernelPattern", "forward_args", "gen_kernel", "known_patterns",
+           "recognise", "register_pattern"]

@@ -43,7 +43,12 @@ CONTROL_SYMBOLS = (
     "kg_gfx950_set_launch_mode",
     "kg_gfx950_last_error",
     "kg_gfx950_abi_version",
+    "kg_gfx950_cost",
 )
+
+# kg_gfx950_cost: op codes (KG_OP_*) and the order of its output array (KG_COST_*).
+COST_OPS = {"matmul": 1, "conv2d": 2, "flash_attention": 3}
+COST_KINDS = ("MAC", "MFMA", "HBM_READ", "HBM_WRITE")
 
 
 class KgArgSlot(ctypes.Structure):
@@ -88,6 +93,13 @@ def load_library() -> ctypes.CDLL:
         raise NativeLibraryError(
             f"{path} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'`"
         )
+    # torch ships its own libamdhip64.so.7. Loaded first, it serves this library too (same
+    # soname); loaded after this library, it would be a second HIP runtime in the process,
+    # and device memory or kernels of one are not valid in the other.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(str(path))
     for name in ENTRY_POINTS:
         fn = getattr(lib, name)
@@ -99,8 +111,44 @@ def load_library() -> ctypes.CDLL:
     lib.kg_gfx950_last_error.restype = ctypes.c_char_p
     lib.kg_gfx950_abi_version.argtypes = []
     lib.kg_gfx950_abi_version.restype = ctypes.c_int
+    lib.kg_gfx950_cost.argtypes = [ctypes.c_int, ctypes.POINTER(KgArgSlot), ctypes.c_ulonglong,
+                                   ctypes.POINTER(ctypes.c_longlong)]
+    lib.kg_gfx950_cost.restype = ctypes.c_int
     _LIBRARY = lib
     return lib
+
+
+class TensorSpec:
+    """Shape, element strides and dtype of an operand, for cost queries without memory.
+
+    ``data_ptr()`` returns a non-zero placeholder: a present memory slot needs a non-NULL
+    pointer, and kg_gfx950_cost never dereferences it.
+    """
+
+    def __init__(self, shape: Sequence[int], dtype: str, strides: Sequence[int] | None = None) -> None:
+        self.shape = tuple(int(d) for d in shape)
+        self.dtype = str(dtype).replace("torch.", "")
+        if strides is None:
+            strides, step = [], 1
+            for d in reversed(self.shape):
+                strides.insert(0, step)
+                step *= max(d, 1)
+        self._strides = tuple(int(s) for s in strides)
+
+    @classmethod
+    def of(cls, value: Any) -> "TensorSpec":
+        """Spec of a torch tensor or numpy array (numpy byte strides become element strides)."""
+
+        if hasattr(value, "stride") and callable(value.stride):
+            return cls(value.shape, str(value.dtype), value.stride())
+        itemsize = int(value.itemsize)
+        return cls(value.shape, value.dtype.name, [s // itemsize for s in value.strides])
+
+    def stride(self) -> tuple[int, ...]:
+        return self._strides
+
+    def data_ptr(self) -> int:
+        return 256
 
 
 def dtype_code_of(value: Any) -> int:
@@ -160,6 +208,24 @@ def call_entry(entry_point: str, args: Sequence[Any], *, check: bool = True) -> 
         detail = lib.kg_gfx950_last_error().decode("utf-8", "replace")
         raise NativeLibraryError(f"{entry_point} returned {status}: {detail}", status)
     return status
+
+
+def cost(family: str, args: Sequence[Any]) -> dict[str, int]:
+    """Per-call cost of ``family``'s entry on ``args`` (its full slot list; memory args may
+    be TensorSpec), computed by kg_gfx950_cost without touching a GPU."""
+
+    lib = load_library()
+    op = COST_OPS.get(family)
+    if op is None:
+        raise NativeLibraryError(f"no cost model for {family!r}", -1)
+    array, keepalive = marshal_slots(args)
+    values = (ctypes.c_longlong * len(COST_KINDS))()
+    status = int(lib.kg_gfx950_cost(op, array, ctypes.c_ulonglong(len(args)), values))
+    del keepalive
+    if status != 0:
+        detail = lib.kg_gfx950_last_error().decode("utf-8", "replace")
+        raise NativeLibraryError(f"kg_gfx950_cost({family}) returned {status}: {detail}", status)
+    return {kind: int(values[i]) for i, kind in enumerate(COST_KINDS)}
 
 
 def last_error() -> str:

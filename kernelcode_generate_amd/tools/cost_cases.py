@@ -1,0 +1,79 @@
+"""Run each cost-model case once on the GPU and print the modelled costs, so a hardware
+counter run can be laid beside the model:
+
+    rocprofv3 --pmc SQ_INSTS_MFMA -d <dir> -- python3 -m kernelcode_generate_amd.tools.cost_cases
+
+Every case makes exactly one library kernel dispatch, in the order printed, and nothing
+else dispatches a kernel (inputs are generated on the host and copied), so dispatch i of the
+counter run is case i. Cases cover every kernel choice the model distinguishes:
+the pipelined and the masked MFMA GEMM, the SIMT GEMM, the MFMA conv with four and with two
+live waves and a ragged last row block, and the MFMA attention kernels for D=128 and D=64,
+causal and not, with ragged query and key tails.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import sys
+
+from .. import native
+
+# (name, family, dtype, shapes, scalars): shapes are (out, in0, in1[, in2]) in the slot
+# order of the family's entry; bias is always absent.
+CASES = (
+    ("gemm_bf16_4096", "matmul", "bfloat16", ((4096, 4096), (4096, 4096), (4096, 4096)), ()),
+    ("gemm_f16_512x768x256", "matmul", "float16", ((512, 768), (512, 256), (256, 768)), ()),
+    ("gemm_bf16_masked_1000x1000x520", "matmul", "bfloat16", ((1000, 1000), (1000, 520), (520, 1000)), ()),
+    ("gemm_f32_256", "matmul", "float32", ((256, 256), (256, 256), (256, 256)), ()),
+    ("conv_f16_c3", "conv2d", "float16", ((32, 64, 56, 56), (32, 64, 56, 56), (64, 64, 3, 3)), (1, 1, 1, 1, 1, 1, 1, 1)),
+    ("conv_bf16_3x64x20x40", "conv2d", "bfloat16", ((3, 64, 20, 40), (3, 64, 20, 40), (64, 64, 3, 3)),
+     (1, 1, 1, 1, 1, 1, 1, 1)),
+    ("conv_f16_2x64x12x24", "conv2d", "float16", ((2, 64, 12, 24), (2, 64, 12, 24), (64, 64, 3, 3)),
+     (1, 1, 1, 1, 1, 1, 1, 1)),
+    ("fa_bf16_c4", "flash_attention", "bfloat16", ((4, 32, 2048, 128),) * 4, (128, 64, 0.088388, 0)),
+    ("fa_bf16_causal_1x4x4096x128", "flash_attention", "bfloat16", ((1, 4, 4096, 128),) * 4, (128, 64, 0.088388, 1)),
+    ("fa_f16_causal_1x2x1000x64", "flash_attention", "float16", ((1, 2, 1000, 64),) * 4, (128, 64, 0.125, 1)),
+    ("fa_bf16_2x3x130x128", "flash_attention", "bfloat16", ((2, 3, 130, 128),) * 4, (128, 64, 0.088388, 0)),
+)
+
+
+def _slots(family: str, operands: list, scalars: tuple) -> list:
+    if family == "flash_attention":
+        return [*operands, *scalars]
+    return [*operands, None, *scalars]
+
+
+def modelled(case) -> dict[str, int]:
+    name, family, dtype, shapes, scalars = case
+    return native.cost(family, _slots(family, [native.TensorSpec(s, dtype) for s in shapes], scalars))
+
+
+def run(case, device: str = "cuda") -> None:
+    import torch
+
+    name, family, dtype, shapes, scalars = case
+    dt = getattr(torch, dtype)
+    gen = torch.Generator().manual_seed(7)  # host-side values: the only device work is the copy
+    tensors = [torch.randn(s, generator=gen, dtype=torch.float32).to(dt).to(device) for s in shapes]
+    torch.cuda.synchronize()
+    entry = {"matmul": "kg_gfx950_matmul_entry", "conv2d": "kg_gfx950_conv2d_entry",
+             "flash_attention": "kg_gfx950_flash_attention_entry"}[family]
+    native.call_entry(entry, _slots(family, tensors, scalars))
+
+
+def main(argv: list[str] | None = None) -> int:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--model-only", action="store_true", help="print the modelled costs without a GPU")
+    opts = parser.parse_args(argv)
+    for case in CASES:
+        line = {"case": case[0], **modelled(case)}
+        if not opts.model_only:
+            run(case)
+            line["ran"] = True
+        print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

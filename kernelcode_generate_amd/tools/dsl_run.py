@@ -8,6 +8,13 @@ Memory arguments may be ROCm torch tensors (used in place) or host numpy arrays 
 CPU tensors, which are staged to the device and copied back after the call -- what the
 reference's cuda_sm89 entry does per call (source_bundle.py:647-707). ``None`` is
 allowed for the bias slot only; ints and floats are passed as INT / FLOAT slots.
+
+``dsl_cost_run(func_obj, real_args, pipeline, cost_kind)`` (kernel_gen/tools/dsl_run.py:
+656-730) returns one integer cost of the same call without running it: the reference
+lowers to an npu_demo cost function whose kinds are DMA1..DMA4, MAC, VECTOR1, VECTOR2;
+here the library's kg_gfx950_cost runs the entry's validation and kernel choice and
+reports MAC, MFMA (wave-level matrix instructions of the chosen kernel), HBM_READ and
+HBM_WRITE (compulsory bytes).
 """
 
 from __future__ import annotations
@@ -22,11 +29,15 @@ from typing import Any, Callable
 from ..core.config import get_dump_dir, get_target
 from ..core.error import ErrorKind, ErrorModule, KernelCodeError
 from ..execute_engine import CompiledKernel, ExecuteResult, ExecutionEngine
-from ..gen_kernel import KernelPattern, gen_kernel, recognise
+from ..gen_kernel import KernelPattern, forward_args, gen_kernel, recognise
 from ..pipeline import PassManager, get_pipeline
 from ..pipeline.gfx950_lowering import LoweredKernel
 
 ARITY_ERROR = "DslRunArityMismatch: real_args count must match the kernel's positional parameters"
+VALID_DSL_COST_KINDS = ("MAC", "MFMA", "HBM_READ", "HBM_WRITE")
+DSL_COST_KIND_ERROR = "DslCostRunInvalidCostKind: cost_kind must be one of [MAC, MFMA, HBM_READ, HBM_WRITE]"
+DSL_COST_TARGET_ERROR = "DslCostRunInvalidTarget: dsl_cost_run only supports target 'gfx950'"
+DSL_COST_OUTPUT_ERROR = "DslCostRunInvalidOutput: cost query was rejected by the gfx950 library"
 _COMPILED: dict[str, CompiledKernel] = {}
 
 
@@ -91,10 +102,7 @@ def _resolve_pipeline(pipeline: str | PassManager) -> PassManager:
     raise _error("pipeline must be a registered name or a PassManager")
 
 
-def dsl_run(func_obj: Callable, real_args: tuple | list, pipeline: str | PassManager) -> DslRunResult:
-    target = get_target()
-    if target != "gfx950":
-        raise _error(f"DslRunInvalidTarget: core config target must be 'gfx950' for this backend, got {target!r}")
+def _check_arity(func_obj: Callable, real_args: tuple | list) -> tuple:
     if not isinstance(real_args, (tuple, list)):
         raise _error("real_args must be a tuple or list")
     args = tuple(real_args)
@@ -102,12 +110,29 @@ def dsl_run(func_obj: Callable, real_args: tuple | list, pipeline: str | PassMan
               if p.kind in (inspect.Parameter.POSITIONAL_ONLY, inspect.Parameter.POSITIONAL_OR_KEYWORD)]
     if len(args) != len(params):
         raise _error(ARITY_ERROR)
-    pm = _resolve_pipeline(pipeline)
-    memory = [a for a in args if a is not None and not isinstance(a, (Integral, Real))]
+    return args
+
+
+def _is_scalar(arg: Any) -> bool:
+    return arg is None or isinstance(arg, (Integral, Real))
+
+
+def _recognise(func_obj: Callable, args: tuple) -> KernelPattern:
+    memory = [a for a in args if not _is_scalar(a)]
     dtype = _dtype_name(memory[0]) if memory else "float32"
     pattern = recognise(func_obj, dtype)
     if len(pattern.params) != len(args):
         raise _error(f"{pattern.function}: expected {len(pattern.params)} args, got {len(args)}")
+    return pattern
+
+
+def dsl_run(func_obj: Callable, real_args: tuple | list, pipeline: str | PassManager) -> DslRunResult:
+    target = get_target()
+    if target != "gfx950":
+        raise _error(f"DslRunInvalidTarget: core config target must be 'gfx950' for this backend, got {target!r}")
+    args = _check_arity(func_obj, real_args)
+    pm = _resolve_pipeline(pipeline)
+    pattern = _recognise(func_obj, args)
     lowered = pm.run(pattern)
     source = gen_kernel(lowered.pattern)
     dump = get_dump_dir()
@@ -122,7 +147,7 @@ def dsl_run(func_obj: Callable, real_args: tuple | list, pipeline: str | PassMan
     staged = []
     writebacks = []
     for a in args:
-        if a is None or isinstance(a, (Integral, Real)):
+        if _is_scalar(a):
             staged.append(a)
             continue
         dev, back = _stage(a)
@@ -134,3 +159,29 @@ def dsl_run(func_obj: Callable, real_args: tuple | list, pipeline: str | PassMan
         back()
     return DslRunResult(pattern=pattern, module=lowered, source=source, compiled_kernel=compiled,
                         execute_result=result, runtime_args=tuple(staged))
+
+
+def dsl_cost_run(func_obj: Callable, real_args: tuple | list, pipeline: str | PassManager, cost_kind: str) -> int:
+    """One integer cost of ``func_obj(*real_args)`` on gfx950, computed without a GPU.
+
+    Contract of kernel_gen/tools/dsl_run.py:656-730: ``cost_kind`` is required and checked
+    first, then the target, the pipeline and the arity; the result is an int. Memory
+    arguments contribute only shape, strides and dtype (torch tensors on any device, numpy
+    arrays or native.TensorSpec), so full-size shapes cost nothing to query.
+    """
+
+    from .. import native
+
+    if cost_kind not in VALID_DSL_COST_KINDS:
+        raise _error(DSL_COST_KIND_ERROR)
+    if get_target() != "gfx950":
+        raise _error(DSL_COST_TARGET_ERROR)
+    pm = _resolve_pipeline(pipeline)
+    args = _check_arity(func_obj, real_args)
+    pattern = pm.run(_recognise(func_obj, args)).pattern
+    slots = forward_args(pattern, [a if _is_scalar(a) else native.TensorSpec.of(a) for a in args])
+    try:
+        costs = native.cost(pattern.family, slots)
+    except native.NativeLibraryError as exc:
+        raise _error(f"{DSL_COST_OUTPUT_ERROR}: {exc}") from exc
+    return costs[cost_kind]
