@@ -65,74 +65,83 @@ __global__ __launch_bounds__(convk::kThreads, 1) void conv2d_3x3s1p1_mfma_kernel
   const int n = blockIdx.x / row_blocks;
   const int r0 = (blockIdx.x - n * row_blocks) * kRows;  // first output row
 
-  // ---- staging, one channel group cg (16 channels) at a time ----
-  // Threads 0..127: weights of filter t/2, channel octet 2cg + (t&1) (144 contiguous bytes:
-  // 8 channels x 9 taps). Threads 128..: input blocks (tile row, octet 2cg + (b&1), 8-column
-  // block) of tile rows 0..8 (tile row r holds input row r0 - 1 + r).
+  // ---- staging roles, fixed per thread (every channel group cg uses the same ones) ----
+  // Waves 0-1 (threads 0..127): weights of filter t/2, channel octet 2cg + (t&1) (144
+  // contiguous bytes: 8 channels x 9 taps), rewritten per tap into k order. Waves 2-3:
+  // input block b = t - 128 = (tile row, octet 2cg + parity, 8-column block) of tile rows
+  // 0..8 (tile row r holds input row r0 - 1 + r): 8 rows of 16 bytes along W, transposed to
+  // channel-last. Roles, sources and LDS destinations are computed once here.
+  const bool w_role = wave < 2;  // wave-uniform
+  const int wf = tid >> 1, wh = tid & 1;
+  const uint16_t* w_src = w + (long long)wf * (kC * 9) + wh * 72;
+  const int w_dst = wf * 2 + w_slot(wf, wh);
   const int wblocks = W >> 3;
   const int in_blocks = kInRows * 2 * wblocks;  // <= 126 for W <= 56
-  u32x4 stage[9];
-  auto stage_load = [&](int cg) {
-    if (tid < 128) {
-      const int f = tid >> 1, co = 2 * cg + (tid & 1);
-      const uint16_t* src = w + (long long)f * (kC * 9) + co * 72;
+  const int xb = w_role ? 0 : tid - 128;
+  const int xb_col = xb % wblocks;
+  const int xb_par = (xb / wblocks) & 1;
+  const int xb_row = xb / (2 * wblocks);
+  const int x_h = r0 - 1 + xb_row;
+  const bool x_store = !w_role && xb < in_blocks;
+  const bool x_load = x_store && x_h >= 0 && x_h < H;
+  const long long hw = (long long)H * W;
+  const uint16_t* x_src = x + ((long long)n * kC + 8 * xb_par) * hw + (long long)(x_load ? x_h : 0) * W + 8 * xb_col;
+  const int x_dst = (xb_row * kCols + 1 + 8 * xb_col) * 8;  // column 1 + 8*xb_col, chunk 0
+
+  // Loads of channel group cg into the register set. Every path writes all nine entries:
+  // with paths that write different entries the compiler merges the stores through a
+  // selected pointer and moves the set to scratch memory.
+  auto stage_load = [&](u32x4 (&stage)[9], int cg) {
+    if (w_role) {
 #pragma unroll
-      for (int i = 0; i < 9; ++i) stage[i] = ld16(src + 8 * i);
+      for (int i = 0; i < 9; ++i) stage[i] = ld16(w_src + cg * 144 + 8 * i);
     } else {
-      const int b = tid - 128;
-      const int wb = b % wblocks;
-      const int co = 2 * cg + ((b / wblocks) & 1);
-      const int r = b / (2 * wblocks);
-      const int h = r0 - 1 + r;
-      if (b < in_blocks && h >= 0 && h < H) {
-        const uint16_t* src = x + (((long long)n * kC + 8 * co) * H + h) * W + 8 * wb;
+      if (x_load) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) stage[e] = ld16(src + (long long)e * H * W);
+        for (int e = 0; e < 8; ++e) stage[e] = ld16(x_src + cg * 16 * hw + e * hw);
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) stage[e] = u32x4{0, 0, 0, 0};
       }
+      stage[8] = u32x4{0, 0, 0, 0};
     }
   };
   // w_lds[(step*64 + f)*2 + w_slot(f, h)] holds channels 16*(step&3) + 8h .. +7 of filter f at
-  // tap step>>2; the input tile is channel-last (chunk c of column col at x_slot(col, c)).
-  auto stage_store = [&](int cg) {
-    if (tid < 128) {
-      const int f = tid >> 1, hsel = tid & 1;
+  // tap step>>2: tap u of the weight role's octet.
+  auto store_w = [&](const u32x4 (&stage)[9], int cg, int u) {
+    u32x4 frag;
 #pragma unroll
-      for (int tap = 0; tap < 9; ++tap) {
-        u32x4 frag;
+    for (int q = 0; q < 4; ++q) {
+      // channels 2q and 2q+1 of the octet at tap u: elements (2q)*9+u and (2q+1)*9+u
+      const int e0 = (2 * q) * 9 + u;
+      const int e1 = (2 * q + 1) * 9 + u;
+      const uint32_t a = stage[e0 >> 3][(e0 >> 1) & 3];
+      const uint32_t b = stage[e1 >> 3][(e1 >> 1) & 3];
+      const uint32_t lo = (e0 & 1) ? (a >> 16) : (a & 0xffffu);
+      const uint32_t hi = (e1 & 1) ? (b >> 16) : (b & 0xffffu);
+      frag[q] = lo | (hi << 16);
+    }
+    w_lds[(4 * u + cg) * kF * 2 + w_dst] = frag;
+  };
+  // The input tile is channel-last: chunk c of column col at x_slot(col, c). Column
+  // 1 + 8*xb_col + j has mask ((1 + 8*xb_col + j) >> 1) & 7 = (4*xb_col + ((j + 1) >> 1)) & 7.
+  auto store_x = [&](const u32x4 (&cols)[8], int cg, int j) {
+    const int mask = (4 * xb_col + ((j + 1) >> 1)) & 7;
+    x_lds[x_dst + 8 * j + ((2 * cg + xb_par) ^ mask)] = cols[j];
+  };
+  auto stage_store = [&](const u32x4 (&stage)[9], int cg) {
+    if (w_role) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          // channels 2q and 2q+1 of the octet at this tap: elements (2q)*9+tap, (2q+1)*9+tap
-          const int e0 = (2 * q) * 9 + tap;
-          const int e1 = (2 * q + 1) * 9 + tap;
-          const uint32_t a = stage[e0 >> 3][(e0 >> 1) & 3];
-          const uint32_t b = stage[e1 >> 3][(e1 >> 1) & 3];
-          const uint32_t lo = (e0 & 1) ? (a >> 16) : (a & 0xffffu);
-          const uint32_t hi = (e1 & 1) ? (b >> 16) : (b & 0xffffu);
-          frag[q] = lo | (hi << 16);
-        }
-        w_lds[((4 * tap + cg) * kF + f) * 2 + w_slot(f, hsel)] = frag;
-      }
-    } else {
-      const int b = tid - 128;
-      if (b < in_blocks) {
-        const int wb = b % wblocks;
-        const int co = 2 * cg + ((b / wblocks) & 1);
-        const int r = b / (2 * wblocks);
-        u32x4 cols[8];
-        transpose8x8_b16(stage, cols);
+      for (int u = 0; u < 9; ++u) store_w(stage, cg, u);
+    } else if (x_store) {
+      u32x4 xcols[8];
+      transpose8x8_b16(stage, xcols);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int col = 1 + 8 * wb + j;
-          x_lds[(r * kCols + col) * 8 + x_slot(col, co)] = cols[j];
-        }
-      }
+      for (int j = 0; j < 8; ++j) store_x(xcols, cg, j);
     }
   };
-
-  stage_load(0);
+  u32x4 set0[9];
+  stage_load(set0, 0);
   {  // zero columns (0 and W+1 .. kCols-1) of every tile row
     const int zcols = kCols - W;
     for (int i = tid; i < kInRows * zcols * 8; i += kThreads) {
@@ -143,7 +152,7 @@ __global__ __launch_bounds__(convk::kThreads, 1) void conv2d_3x3s1p1_mfma_kernel
       x_lds[(r * kCols + col) * 8 + x_slot(col, c8)] = u32x4{0, 0, 0, 0};
     }
   }
-  stage_store(0);
+  stage_store(set0, 0);
   __syncthreads();
 
   // ---- compute: wave = (filter block fb, pixel block pb) over all 7 rows ----
@@ -195,17 +204,21 @@ __global__ __launch_bounds__(convk::kThreads, 1) void conv2d_3x3s1p1_mfma_kernel
       b_cur = b_nxt;
     }
   };
-  // Output rows row0 .. row0+R-1 go out through LDS (bytes [0, 64*R*2W) of the input tile,
-  // laid out [f][row][w] like Y) so that the HBM writes are whole 16-byte chunks of each
+  // Output rows row0 .. row0+R-1 go out through LDS (laid out [f][row][w] like Y, filter
+  // planes `stride` bytes apart) so that the HBM writes are whole 16-byte chunks of each
   // filter plane, consecutive per lane; scattered 8-byte stores from the MFMA layout write
   // far below HBM speed. Lane holds filter f, pixels 32pb + 8j + 4*hsel + 0..3 of each row.
+  // stride = R*W*2 rounded so that stride/16 is odd: the 8-byte writes of 32 consecutive
+  // filters then spread over all 16-byte bank groups (two lanes per group).
   float bv = 0.f;
   if constexpr (kBias == 1) bv = static_cast<const float*>(bias)[f];
   if constexpr (kBias == 2) bv = Hf::to_float(static_cast<const uint16_t*>(bias)[f]);
   char* out_lds = reinterpret_cast<char*>(x_lds);
+  auto out_stride = [&](int R) { return R * W * 2 + (((R * W / 8) & 1) ? 0 : 16); };
   auto stage_out = [&](auto rows_tag, const f32x16 (&acc)[decltype(rows_tag)::value]) {
     constexpr int R = decltype(rows_tag)::value;
     if (!live) return;
+    const int stride = out_stride(R);
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -215,20 +228,24 @@ __global__ __launch_bounds__(convk::kThreads, 1) void conv2d_3x3s1p1_mfma_kernel
           u32x2 packed;
           packed[0] = Hf::pack2(acc[r][4 * j] + bv, acc[r][4 * j + 1] + bv);
           packed[1] = Hf::pack2(acc[r][4 * j + 2] + bv, acc[r][4 * j + 3] + bv);
-          *reinterpret_cast<u32x2*>(out_lds + ((f * R + r) * W + wo) * 2) = packed;
+          *reinterpret_cast<u32x2*>(out_lds + f * stride + (r * W + wo) * 2) = packed;
         }
       }
   };
-  auto flush_out = [&](int R, int row0) {  // rows past H are not written
+  // Wave v writes filters 16v .. 16v+15, two per pass (lane / 32), 16 bytes per lane: a
+  // filter's rv rows are rv*W/8 <= 28 consecutive chunks of Y. Rows past H are not written.
+  auto flush_out = [&](int R, int row0) {
     const int ho0 = r0 + row0;
     const int rv = min(R, H - ho0);
-    if (rv <= 0) return;
-    const int per_f = rv * W / 8;  // 16-byte chunks per filter
-    for (int c = tid; c < kF * per_f; c += kThreads) {
-      const int f2 = c / per_f;
-      const int k = c - f2 * per_f;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(out_lds + f2 * R * W * 2 + 16 * k);
-      st16(y + (((long long)n * kF + f2) * H + ho0) * W + 8 * k, v);
+    const int per_f = rv * W / 8;
+    const int k = lane & 31;
+    if (rv <= 0 || k >= per_f) return;
+    const int stride = out_stride(R);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int f2 = wave * 16 + 2 * i + (lane >> 5);
+      const u32x4 v = *reinterpret_cast<const u32x4*>(out_lds + f2 * stride + 16 * k);
+      st16(y + ((long long)n * kF + f2) * hw + (long long)ho0 * W + 8 * k, v);
     }
   };
 
@@ -243,13 +260,14 @@ __global__ __launch_bounds__(convk::kThreads, 1) void conv2d_3x3s1p1_mfma_kernel
     for (int i = 0; i < 16; ++i) acc_a[r][i] = 0.f;
 #pragma unroll
   for (int cg = 0; cg < 4; ++cg) {
-    if (cg + 1 < 4) stage_load(cg + 1);
+    if (cg + 1 < 4) stage_load(set0, cg + 1);
     compute_cg(Int<kRowsA>{}, 0, cg, acc_a);
-    if (cg + 1 < 4) stage_store(cg + 1);
+    if (cg + 1 < 4) stage_store(set0, cg + 1);
     __syncthreads();
   }
-  // ---- A's outputs into tile rows 0..3 (only group A read them), then out to HBM while
-  // group B (output rows 4..6, tile rows 4..8) computes ----
+  // ---- A's outputs into tile rows 0..3 (only group A read them; 64 planes of
+  // out_stride(4) <= 29696 bytes = 4 tile rows for W <= 56), then out to HBM while group B
+  // (output rows 4..6, tile rows 4..8) computes ----
   stage_out(Int<kRowsA>{}, acc_a);
   __syncthreads();
   flush_out(kRowsA, 0);
