@@ -9,14 +9,16 @@
 // pixel per lane) is one 16-byte read, and so is an operand-B fragment from the reordered
 // weights.
 //
-// One workgroup (4 waves) per 7 output rows of one image: the C3 shape (N=32, H=56) is 256
-// workgroups, one per CU. The weights (rewritten per tap into k order) and the 9 input
-// rows (8-channel x 8-column blocks loaded along W, transposed in registers and written
-// channel-last, with a zero column on each side and zero rows outside the image) are staged
-// into LDS one channel group of 16 at a time: while the MFMAs of group cg run, the loads of
-// group cg+1 are in flight, so only the first group's ~35 KB is exposed. Wave w owns filter
-// block w >> 1 and pixel block w & 1 (32 each) of all 7 rows: 7 accumulators, and per k step
-// one weight fragment shared by 7 input fragments (252 MFMAs per wave).
+// One workgroup per 7 output rows of one image: the C3 shape (N=32, H=56) is 256
+// workgroups, one per CU, of 8 waves in two roles, one of each per SIMD. Compute waves 0-3:
+// wave w owns filter block w >> 1 and pixel block w & 1 (32 each) of all 7 rows: 7
+// accumulators, and per k step one weight fragment shared by 7 input fragments (252 MFMAs
+// per wave). Staging waves 4-7 put the weights (rewritten per tap into k order) and the 9
+// input rows (8-channel x 8-column blocks loaded along W, transposed in registers and
+// written channel-last, with a zero column on each side and zero rows outside the image)
+// into LDS one channel group of 16 at a time while the compute waves run the previous
+// group, and write finished output rows to HBM while the compute waves run the next rows,
+// so staging and MFMA work overlap instead of alternating.
 //
 // LDS layout (64 banks of 4 bytes; ds_read_b128 serves 16 lanes per cycle): a pixel of the
 // input tile is 128 bytes (8 chunks of 8 channels); chunk c of column col sits at slot
@@ -32,7 +34,8 @@ namespace kg_gfx950 {
 
 namespace convk {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;       // waves 0-3 compute, waves 4-7 stage
+constexpr int kStageThreads = 256;
 constexpr int kRows = 7;            // output rows per workgroup
 constexpr int kInRows = kRows + 2;  // input rows per workgroup
 constexpr int kCols = 58;           // LDS tile columns: W <= 56 plus two zero columns
@@ -65,24 +68,29 @@ __global__ __launch_bounds__(convk::kThreads, 1) void conv2d_3x3s1p1_mfma_kernel
   const int n = blockIdx.x / row_blocks;
   const int r0 = (blockIdx.x - n * row_blocks) * kRows;  // first output row
 
-  // ---- staging roles, fixed per thread (every channel group cg uses the same ones) ----
-  // Waves 0-1 (threads 0..127): weights of filter t/2, channel octet 2cg + (t&1) (144
-  // contiguous bytes: 8 channels x 9 taps), rewritten per tap into k order. Waves 2-3:
-  // input block b = t - 128 = (tile row, octet 2cg + parity, 8-column block) of tile rows
-  // 0..8 (tile row r holds input row r0 - 1 + r): 8 rows of 16 bytes along W, transposed to
-  // channel-last. Roles, sources and LDS destinations are computed once here.
-  const bool w_role = wave < 2;  // wave-uniform
-  const int wf = tid >> 1, wh = tid & 1;
+  // ---- roles: waves 0-3 run the MFMAs, waves 4-7 (staging thread st = t - 256) load,
+  // reorder and store the next channel group and write finished outputs to HBM, so a step
+  // costs max(compute, staging) instead of their sum. Each SIMD holds one wave of each. ----
+  const bool stager = wave >= 4;  // wave-uniform
+  const int st = tid - kStageThreads;
+  // Staging, fixed per thread (every channel group cg uses the same roles): st 0..127:
+  // weights of filter st/2, channel octet 2cg + (st&1) (144 contiguous bytes: 8 channels x
+  // 9 taps), rewritten per tap into k order. st 128..255: input block b = st - 128 = (tile
+  // row, octet 2cg + parity, 8-column block) of tile rows 0..8 (tile row r holds input row
+  // r0 - 1 + r): 8 rows of 16 bytes along W, transposed to channel-last. Sources and LDS
+  // destinations are computed once here.
+  const bool w_role = stager && st < 128;  // wave-uniform
+  const int wf = (st >> 1) & 63, wh = st & 1;
   const uint16_t* w_src = w + (long long)wf * (kC * 9) + wh * 72;
   const int w_dst = wf * 2 + w_slot(wf, wh);
   const int wblocks = W >> 3;
   const int in_blocks = kInRows * 2 * wblocks;  // <= 126 for W <= 56
-  const int xb = w_role ? 0 : tid - 128;
+  const int xb = (stager && !w_role) ? st - 128 : 0;
   const int xb_col = xb % wblocks;
   const int xb_par = (xb / wblocks) & 1;
   const int xb_row = xb / (2 * wblocks);
   const int x_h = r0 - 1 + xb_row;
-  const bool x_store = !w_role && xb < in_blocks;
+  const bool x_store = stager && !w_role && xb < in_blocks;
   const bool x_load = x_store && x_h >= 0 && x_h < H;
   const long long hw = (long long)H * W;
   const uint16_t* x_src = x + ((long long)n * kC + 8 * xb_par) * hw + (long long)(x_load ? x_h : 0) * W + 8 * xb_col;
@@ -141,26 +149,29 @@ __global__ __launch_bounds__(convk::kThreads, 1) void conv2d_3x3s1p1_mfma_kernel
     }
   };
   u32x4 set0[9];
-  stage_load(set0, 0);
-  {  // zero columns (0 and W+1 .. kCols-1) of every tile row
+  if (stager) {
+    stage_load(set0, 0);
+    // zero columns (0 and W+1 .. kCols-1) of every tile row
     const int zcols = kCols - W;
-    for (int i = tid; i < kInRows * zcols * 8; i += kThreads) {
+    for (int i = st; i < kInRows * zcols * 8; i += kStageThreads) {
       const int c8 = i & 7;
       const int zc = (i >> 3) % zcols;
       const int r = (i >> 3) / zcols;
       const int col = zc == 0 ? 0 : W + zc;
       x_lds[(r * kCols + col) * 8 + x_slot(col, c8)] = u32x4{0, 0, 0, 0};
     }
+    stage_store(set0, 0);
+    stage_load(set0, 1);
   }
-  stage_store(set0, 0);
   __syncthreads();
 
-  // ---- compute: wave = (filter block fb, pixel block pb) over all 7 rows ----
-  const int fb = wave >> 1;
+  // ---- compute: wave = (filter block fb, pixel block pb) over all 7 rows (staging waves
+  // get the indices of wave - 4, unused) ----
+  const int fb = (wave >> 1) & 1;
   const int pb = wave & 1;
   const int f = 32 * fb + (lane & 31);
   const int hsel = lane >> 5;
-  const bool live = 32 * pb < W;  // wave-uniform
+  const bool live = !stager && 32 * pb < W;  // wave-uniform
   const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)&lds[0];
   // A operand: pixel w = 32pb + lane%32 (dead lanes past W read column W-1), channels
   // 16cg + 8hsel .. +7 at tap (kh, kw): LDS byte ((r + kh)*58 + w + kw)*128 + 16*slot.
@@ -232,8 +243,9 @@ __global__ __launch_bounds__(convk::kThreads, 1) void conv2d_3x3s1p1_mfma_kernel
         }
       }
   };
-  // Wave v writes filters 16v .. 16v+15, two per pass (lane / 32), 16 bytes per lane: a
-  // filter's rv rows are rv*W/8 <= 28 consecutive chunks of Y. Rows past H are not written.
+  // Staging wave v (4..7) writes filters 16(v-4) .. +15, two per pass (lane / 32), 16 bytes
+  // per lane: a filter's rv rows are rv*W/8 <= 28 consecutive chunks of Y. Rows past H are
+  // not written.
   auto flush_out = [&](int R, int row0) {
     const int ho0 = r0 + row0;
     const int rv = min(R, H - ho0);
@@ -243,7 +255,7 @@ __global__ __launch_bounds__(convk::kThreads, 1) void conv2d_3x3s1p1_mfma_kernel
     const int stride = out_stride(R);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int f2 = wave * 16 + 2 * i + (lane >> 5);
+      const int f2 = (wave - 4) * 16 + 2 * i + (lane >> 5);
       const u32x4 v = *reinterpret_cast<const u32x4*>(out_lds + f2 * stride + 16 * k);
       st16(y + ((long long)n * kF + f2) * hw + (long long)ho0 * W + 8 * k, v);
     }
@@ -251,8 +263,9 @@ __global__ __launch_bounds__(convk::kThreads, 1) void conv2d_3x3s1p1_mfma_kernel
 
   constexpr int kRowsA = 4;  // output rows 0..3: tile rows 0..5
   constexpr int kRowsB = kRows - kRowsA;
-  // ---- group A, staged by channel group: the loads of group cg+1 are in flight while the
-  // MFMAs of group cg run, and land in LDS regions group cg does not read ----
+  // ---- group A, one channel group per step: the compute waves run group cg while the
+  // staging waves store group cg+1 (loaded during the previous step) into LDS regions
+  // group cg does not read and issue the loads of group cg+2 ----
   f32x16 acc_a[kRowsA];
 #pragma unroll
   for (int r = 0; r < kRowsA; ++r)
@@ -260,28 +273,34 @@ __global__ __launch_bounds__(convk::kThreads, 1) void conv2d_3x3s1p1_mfma_kernel
     for (int i = 0; i < 16; ++i) acc_a[r][i] = 0.f;
 #pragma unroll
   for (int cg = 0; cg < 4; ++cg) {
-    if (cg + 1 < 4) stage_load(set0, cg + 1);
-    compute_cg(Int<kRowsA>{}, 0, cg, acc_a);
-    if (cg + 1 < 4) stage_store(set0, cg + 1);
+    if (!stager) {
+      compute_cg(Int<kRowsA>{}, 0, cg, acc_a);
+    } else if (cg + 1 < 4) {
+      stage_store(set0, cg + 1);
+      if (cg + 2 < 4) stage_load(set0, cg + 2);
+    }
     __syncthreads();
   }
   // ---- A's outputs into tile rows 0..3 (only group A read them; 64 planes of
-  // out_stride(4) <= 29696 bytes = 4 tile rows for W <= 56), then out to HBM while group B
-  // (output rows 4..6, tile rows 4..8) computes ----
+  // out_stride(4) <= 29696 bytes = 4 tile rows for W <= 56); the staging waves write them
+  // to HBM while the compute waves run group B (output rows 4..6, tile rows 4..8) ----
   stage_out(Int<kRowsA>{}, acc_a);
   __syncthreads();
-  flush_out(kRowsA, 0);
   f32x16 acc_b[kRowsB];
+  if (!stager) {
 #pragma unroll
-  for (int r = 0; r < kRowsB; ++r)
+    for (int r = 0; r < kRowsB; ++r)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc_b[r][i] = 0.f;
+      for (int i = 0; i < 16; ++i) acc_b[r][i] = 0.f;
 #pragma unroll
-  for (int cg = 0; cg < 4; ++cg) compute_cg(Int<kRowsB>{}, kRowsA, cg, acc_b);
-  __syncthreads();  // every wave has read A's outputs back and finished group B
+    for (int cg = 0; cg < 4; ++cg) compute_cg(Int<kRowsB>{}, kRowsA, cg, acc_b);
+  } else {
+    flush_out(kRowsA, 0);
+  }
+  __syncthreads();  // A's outputs are read back and group B is done
   stage_out(Int<kRowsB>{}, acc_b);
   __syncthreads();
-  flush_out(kRowsB, kRowsA);
+  if (stager) flush_out(kRowsB, kRowsA);
 }
 
 inline bool conv_mfma_supported(const ConvShape& s) {
