@@ -5,8 +5,10 @@
 Headline workload: bf16 matmul C = A @ B, M = N = K = 4096,
 row-major, fp32 accumulation, bf16 output, A and B ~ N(0,1)*0.02 (synthetic, resident in
 HBM before timing). One step = one launch of the matmul entry through the C ABI on
-torch's current stream; W untimed warm-up steps, then exactly K timed steps bracketed by
-torch.cuda.synchronize(). value = algorithmic FLOP (2*M*N*K) per step / step time.
+torch's current stream; W untimed warm-up steps (default 500, about 60 ms: MI355X raises
+its clock over the first tens of milliseconds of sustained load, so fewer would time the
+ramp), then exactly K timed steps (default 200) bracketed by torch.cuda.synchronize().
+value = algorithmic FLOP (2*M*N*K) per step / step time.
 
 The JSON line also carries
   roofline: the GEMM kernel against dense bf16 MFMA peak, from HIP events on the launch
@@ -16,7 +18,9 @@ The JSON line also carries
             compiled without optimisation like the reference (g++ -shared -fPIC, no -O)
             and run on 2 host threads (npu_demo block_num = 2) over a bounded sample of
             the same workload (the first 384 output rows);
-  secondary: the other BASELINE configs (C1, C2', C3, C4, C5 D=128/64) timed the same way.
+  secondary: the other BASELINE configs (C1, C2', C3, C4, C5 D=128/64), each after 0.15 s
+            of untimed launches, over >= 200 (C1, C2'), 1000 (C3), 100 (C4) or 25 (C5)
+            back-to-back launches.
 """
 
 from __future__ import annotations
@@ -62,14 +66,25 @@ class PreparedCall:
             raise RuntimeError(f"{self.entry} returned {rc}: {self.lib.kg_gfx950_last_error().decode()}")
 
 
-def time_steps(call: PreparedCall, steps: int, warmup: int):
-    """Return (wall ms per step, event ms per step) over exactly `steps` launches."""
+def time_steps(call: PreparedCall, steps: int, warmup: int, min_warmup_s: float = 0.0):
+    """Return (wall ms per step, event ms per step, warmup launches) over exactly `steps`
+    launches, after `warmup` untimed launches and, if min_warmup_s > 0, more untimed
+    launches until that much time has passed. MI355X raises its clock over the first tens
+    of milliseconds of sustained load (C4: 299 us per launch over the first 20 launches,
+    251 us after 150), so a short warm-up times the clock ramp, not the kernel."""
 
     import torch
 
     for _ in range(warmup):
         call()
     torch.cuda.synchronize()
+    if min_warmup_s > 0:
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < min_warmup_s:
+            for _ in range(16):
+                call()
+            torch.cuda.synchronize()
+            warmup += 16
     stream = torch.cuda.current_stream()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
@@ -80,7 +95,7 @@ def time_steps(call: PreparedCall, steps: int, warmup: int):
     e1.record(stream)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    return (t1 - t0) * 1e3 / steps, e0.elapsed_time(e1) / steps
+    return (t1 - t0) * 1e3 / steps, e0.elapsed_time(e1) / steps, warmup
 
 
 def read_traffic(path: Path):
@@ -127,6 +142,9 @@ def cpu_baseline_matmul(rows: int = 384):
 SECONDARY_KEYS = ("c1", "c2s", "c3", "c4", "c5d128", "c5d64")
 
 
+SECONDARY_WARMUP_S = 0.15  # untimed back-to-back launches per secondary workload, seconds
+
+
 def secondary(dev, steps: int, warmup: int, only=None):
     import torch
 
@@ -134,10 +152,10 @@ def secondary(dev, steps: int, warmup: int, only=None):
     keys = set(SECONDARY_KEYS if only is None else only)
 
     def add(name, flop, call, peak, nsteps, byts=None, traffic_file=None):
-        wall, ev = time_steps(call, nsteps, max(2, warmup // 2))
+        wall, ev, nwarm = time_steps(call, nsteps, min(warmup, 10), SECONDARY_WARMUP_S)
         tf = flop / (ev * 1e-3) / 1e12
         rec = {"workload": name, "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ev, 5),
-               "frac_of_peak": round(tf / peak, 4), "peak": peak}
+               "frac_of_peak": round(tf / peak, 4), "peak": peak, "steps": nsteps, "warmup_launches": nwarm}
         if byts is not None:
             gbs = byts / (ev * 1e-3) / 1e9
             rec["hbm_gbs"] = round(gbs, 1)
@@ -169,13 +187,14 @@ def c1(dev, add, steps):
     a = torch.rand(256, 256, generator=g, device=dev) * 2 - 1
     b = torch.rand(256, 256, generator=g, device=dev) * 2 - 1
     c = torch.empty(256, 256, device=dev)
-    add("C1 fp32 matmul 256^3", 2 * 256**3, PreparedCall("kg_gfx950_matmul_entry", (c, a, b, None)), PEAK_FP32_TFLOPS, steps)
+    add("C1 fp32 matmul 256^3", 2 * 256**3, PreparedCall("kg_gfx950_matmul_entry", (c, a, b, None)), PEAK_FP32_TFLOPS,
+        max(steps, 200))
 
 
 def c2s(dev, add, steps):
     a, b, c = gemm_workload(dev, 8192, 1024, 4096, 20261203)
     add("C2' bf16 matmul M=8192 N=1024 K=4096", 2 * 8192 * 1024 * 4096,
-        PreparedCall("kg_gfx950_matmul_entry", (c, a, b, None)), PEAK_BF16_TFLOPS, steps)
+        PreparedCall("kg_gfx950_matmul_entry", (c, a, b, None)), PEAK_BF16_TFLOPS, max(steps, 200))
 
 
 def c3(dev, add, steps):
@@ -189,7 +208,7 @@ def c3(dev, add, steps):
     conv_bytes = 2 * (32 * 64 * 56 * 56 * 2) + 64 * 64 * 9 * 2
     add("C3 fp16 conv2d N=32 C=64 H=W=56 F=64 3x3 s1 p1", 2 * 32 * 64 * 56 * 56 * 64 * 9,
         PreparedCall("kg_gfx950_conv2d_entry", (y, x, w, None, 1, 1, 1, 1, 1, 1, 1, 1)), PEAK_BF16_TFLOPS,
-        max(steps, 50), conv_bytes, "conv2d_fp16_c3_traffic.txt")
+        max(steps, 1000), conv_bytes, "conv2d_fp16_c3_traffic.txt")
 
 
 def c4(dev, add, steps):
@@ -200,7 +219,7 @@ def c4(dev, add, steps):
     o = torch.empty_like(q)
     add("C4 bf16 flash-attn fwd B=4 H=32 S=2048 D=128 non-causal", 4 * 4 * 32 * 2048 * 2048 * 128,
         PreparedCall("kg_gfx950_flash_attention_entry", (o, q, k, v, 128, 64, 1.0 / math.sqrt(128.0), 0)),
-        PEAK_BF16_TFLOPS, steps, None, "flash_attn_bf16_c4_traffic.txt")
+        PEAK_BF16_TFLOPS, max(steps, 100), None, "flash_attn_bf16_c4_traffic.txt")
 
 
 def c5(dev, add, steps, d):
@@ -212,14 +231,15 @@ def c5(dev, add, steps, d):
     o = torch.empty_like(q)
     add(f"C5 bf16 flash-attn fwd B=1 H=32 S=16384 D={d} causal", 4 * 32 * 16384 * 16384 * d // 2,
         PreparedCall("kg_gfx950_flash_attention_entry", (o, q, k, v, 128, 64, 1.0 / math.sqrt(d), 1)),
-        PEAK_BF16_TFLOPS, max(3, steps // 4))
+        PEAK_BF16_TFLOPS, max(20, steps // 4))
 
 
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200, help="timed launches of the headline GEMM")
+    ap.add_argument("--warmup", type=int, default=500,
+                    help="untimed launches before them (500 x ~115 us: the clock has settled)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--only", nargs="+", choices=SECONDARY_KEYS,
@@ -252,7 +272,7 @@ def main() -> int:
     a, b, c = gemm_workload(dev, m, n, k, 20261202)
     call = PreparedCall("kg_gfx950_matmul_entry", (c, a, b, None))
     torch.cuda.synchronize()
-    wall_ms, ev_ms = time_steps(call, args.steps, args.warmup)
+    wall_ms, ev_ms, _ = time_steps(call, args.steps, args.warmup)
     flop = 2.0 * m * n * k
     value = flop / (wall_ms * 1e-3) / 1e12
     achieved = flop / (ev_ms * 1e-3) / 1e12
