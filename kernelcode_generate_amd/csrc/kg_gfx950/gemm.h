@@ -212,13 +212,14 @@ __global__ __launch_bounds__(gemm::kThreads, 1) void gemm_mfma_kernel(
   }
 }
 
-// gemm_pipe_kernel: the aligned-shape path (M % 256 == 0, N % 256 == 0, K % 32 == 0).
-//   256x256 tiles computed by 8 waves (2 x 4 waves of 128x64, two per SIMD) with 32x32x16
-//   MFMAs. Both operands are copied HBM -> LDS by global_load_lds_dwordx4 (no registers, no
-//   VALU work) through a 4-stage ring of 32-deep K slices (4 x 32 KiB), so loads are issued
-//   three slices ahead of their use; every wave issues 4 of a slice's 32 copies, slotted
-//   between its MFMAs, and while one wave of a SIMD waits on a copy's issue or an LDS read
-//   the other keeps the MFMA pipe busy. lhs slices are [m][k] rows of 64 bytes; rhs slices
+// gemm_pipe_kernel: the aligned-shape path (M % kTM == 0, N % 256 == 0, K % 32 == 0).
+//   kTM x 256 tiles (kTM = 256, or 128 when 256-row tiles would leave CUs idle) computed by
+//   8 waves (2 x 4 waves of kTM/2 x 64, two per SIMD) with 32x32x16 MFMAs. Both operands
+//   are copied HBM -> LDS by global_load_lds_dwordx4 (no registers, no VALU work) through a
+//   4-stage ring of 32-deep K slices (4 x (kTM/16 + 16) KiB), so loads are issued three
+//   slices ahead of their use; every wave issues kTM/128 + 2 of a slice's copies (1 KiB
+//   each), slotted between its MFMAs, and while one wave of a SIMD waits on a copy's issue
+//   or an LDS read the other keeps the MFMA pipe busy. lhs slices are [m][k] rows of 64 bytes; rhs slices
 //   stay [k][n] as in HBM and the MFMA operand (8 consecutive k of one n) is read with two
 //   ds_read_b64_tr_b16: within each 16-lane group, lane j addresses 4 consecutive n of
 //   k-row j/4 and lane i receives k-rows 0..3 of column i. Chunk swizzles: lhs
@@ -227,13 +228,11 @@ __global__ __launch_bounds__(gemm::kThreads, 1) void gemm_mfma_kernel(
 //   of one 16-deep half of a slice run, the other half (or the next slice's first half) is
 //   being read, and the per-slice barrier sits between the two halves.
 namespace gemmp {
-constexpr int kBM = 256;
+constexpr int kBM = 256;  // largest tile height (kTM)
 constexpr int kBN = 256;
 constexpr int kBK = 32;
 constexpr int kStages = 4;
-constexpr int kThreads = 512;  // 8 waves: 2 x 4 of 128 x 64, two per SIMD
-constexpr int kPieces = 4;     // copies per wave per slice: 2 lhs, 2 rhs
-constexpr int kAVecs = kBM * kBK / 8;  // 1024 u32x4 per lhs stage
+constexpr int kThreads = 512;  // 8 waves: 2 x 4 of kTM/2 x 64, two per SIMD
 constexpr int kBVecs = kBK * kBN / 8;  // 1024 u32x4 per rhs stage
 // LDS has 64 banks of 4 bytes: ds_read_b128 serves 16 lanes per cycle, 64-bit reads 32.
 // The swizzles are XOR masks, so the same mask maps an LDS slot back to its HBM chunk.
@@ -247,23 +246,31 @@ struct StageIdx {
 };
 }  // namespace gemmp
 
-template <typename Tag, int kBias>
+template <typename Tag, int kBias, int kTM>
 __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, uint16_t* __restrict__ C,
     const void* __restrict__ bias, int M, int N, int K, long long lda, long long ldb, long long ldc) {
   using namespace gemmp;
   using H = Half16<Tag>;
+  static_assert(kTM == 256 || kTM == 128, "tile height");
+  constexpr int MI = kTM / 64;              // 32-row fragments per wave
+  constexpr int AP = kTM / 128;             // lhs copies per wave per slice
+  constexpr int kPieces = AP + 2;           // copies per wave per slice: AP lhs, 2 rhs
+  constexpr int NR = MI + 4;                // fragment reads per half slice: MI lhs, 4 rhs
+  constexpr int NM = 2 * MI;                // MFMAs per half slice
+  constexpr int NSTEP = NM > NR ? NM : NR;  // interleave steps per half slice
+  constexpr int kAVecs = kTM * kBK / 8;     // u32x4 per lhs stage
   __shared__ u32x4 lds_a[kStages][kAVecs];
   __shared__ u32x4 lds_b[kStages][kBVecs];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 2;  // 128-row half of the tile
+  const int wm = wave >> 2;  // kTM/2-row half of the tile
   const int wn = wave & 3;   // 64-column quarter
 
   const int tiles_n = N / kBN;
-  const int tiles_m = M / kBM;
+  const int tiles_m = M / kTM;
   const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
   constexpr int kGroupM = 4;
   const int group_size = kGroupM * tiles_n;
@@ -271,14 +278,14 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
   const int first_m = group * kGroupM;
   const int gm = min(tiles_m - first_m, kGroupM);
   const int in_group = logical - group * group_size;
-  const int m0 = (first_m + in_group % gm) * kBM;
+  const int m0 = (first_m + in_group % gm) * kTM;
   const int n0 = (in_group / gm) * kBN;
 
   // ---- HBM -> LDS copies ----
-  // Piece p < 2: lhs rows (wave*2+p)*16 + lane/4 (a_mask depends on lane only, so one
-  // per-lane offset and 16 rows between pieces). Piece 2+p: rhs k-rows (wave*2+p)*2 +
+  // Piece p < AP: lhs rows (wave*AP+p)*16 + lane/4 (a_mask depends on lane only, so one
+  // per-lane offset and 16 rows between pieces). Piece AP+p: rhs k-rows (wave*2+p)*2 +
   // lane/32 (b_mask depends on p and lane).
-  const int a_row0 = wave * 32 + (lane >> 2);
+  const int a_row0 = wave * AP * 16 + (lane >> 2);
   const uint32_t a_goff = (uint32_t)((a_row0 * lda + 8 * ((lane & 3) ^ a_mask(a_row0))) * 2);
   uint32_t b_goff[2];
 #pragma unroll
@@ -292,15 +299,16 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
   const long long b_step = (long long)kBK * ldb * 2;
   const uint32_t lds_a0 = lds_addr(&lds_a[0][0]);
   const uint32_t lds_b0 = lds_addr(&lds_b[0][0]);
-  constexpr uint32_t kStageBytes = kAVecs * 16;  // == kBVecs * 16
+  constexpr uint32_t kAStage = kAVecs * 16;
+  constexpr uint32_t kBStage = kBVecs * 16;
 
-  auto issue_piece = [&](int kt, int s, int piece) {  // piece 0..3: 2 lhs then 2 rhs
-    if (piece < 2) {
+  auto issue_piece = [&](int kt, int s, int piece) {  // piece 0..kPieces-1: AP lhs then 2 rhs
+    if (piece < AP) {
       g2lds16_s(a_goff, a_tile + (long long)kt * kBK * 2 + piece * a_piece,
-                lds_a0 + s * kStageBytes + (wave * 2 + piece) * 1024);
+                lds_a0 + s * kAStage + (wave * AP + piece) * 1024);
     } else {
-      const int i = piece - 2;
-      g2lds16_s(b_goff[i], b_tile + kt * b_step, lds_b0 + s * kStageBytes + (wave * 2 + i) * 1024);
+      const int i = piece - AP;
+      g2lds16_s(b_goff[i], b_tile + kt * b_step, lds_b0 + s * kBStage + (wave * 2 + i) * 1024);
     }
   };
 
@@ -315,7 +323,7 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
   const int b_kofs = 8 * (g >> 1) + (j16 >> 2);
   uint32_t a_rd[2], b_rd[2];
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) a_rd[ks] = lds_a0 + a_slot(wm * 128 + frag_row, 2 * ks + frag_half) * 16;
+  for (int ks = 0; ks < 2; ++ks) a_rd[ks] = lds_a0 + a_slot(wm * (kTM / 2) + frag_row, 2 * ks + frag_half) * 16;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int n = wn * 64 + j * 32 + b_nofs;
@@ -323,26 +331,26 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
   }
 
   struct Frag {
-    u32x4 a[4];
+    u32x4 a[MI];
     u32x4 b[2];
   };
-  // read #r (0..7) of a fragment set: 4 lhs b128 reads, then 4 rhs transposed reads
+  // read #r (0..NR-1) of a fragment set: MI lhs b128 reads, then 4 rhs transposed reads
   auto read_piece = [&](int s, int ks, Frag& f, int r) {
-    if (r < 4) {
-      f.a[r] = *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(a_rd[ks] + s * kStageBytes + r * 2048);
+    if (r < MI) {
+      f.a[r] = *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(a_rd[ks] + s * kAStage + r * 2048);
     } else {
-      const int j = (r - 4) >> 1, t = (r - 4) & 1;
+      const int j = (r - MI) >> 1, t = (r - MI) & 1;
       const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) s16x4*)(uintptr_t)(b_rd[j] + s * kStageBytes + t * 2048 + ks * 8192));
+          (__attribute__((address_space(3))) s16x4*)(uintptr_t)(b_rd[j] + s * kBStage + t * 2048 + ks * 8192));
       const u32x2 w = __builtin_bit_cast(u32x2, v);
       f.b[j][2 * t] = w[0];
       f.b[j][2 * t + 1] = w[1];
     }
   };
 
-  f32x16 acc[4][2];
+  f32x16 acc[MI][2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -363,7 +371,7 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
   }
   Frag f0, f1;
 #pragma unroll
-  for (int r = 0; r < 8; ++r) read_piece(0, 0, f0, r);
+  for (int r = 0; r < NR; ++r) read_piece(0, 0, f0, r);
 
   // One 32-deep slice in stage S: MFMAs of half 0 with the reads of half 1 slotted in
   // between, barrier, MFMAs of half 1 with the next slice's first reads and this stage's
@@ -372,10 +380,10 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
     constexpr int S = decltype(stage_tag)::value;
     constexpr bool kSteady = decltype(steady_tag)::value != 0;
 #pragma unroll
-    for (int idx = 0; idx < 8; ++idx) {
+    for (int idx = 0; idx < NSTEP; ++idx) {
       const int i = idx >> 1, j = idx & 1;
-      acc[i][j] = H::mfma32(f0.b[j], f0.a[i], acc[i][j]);
-      read_piece(S, 1, f1, idx);
+      if (idx < NM) acc[i][j] = H::mfma32(f0.b[j], f0.a[i], acc[i][j]);
+      if (idx < NR) read_piece(S, 1, f1, idx);
       __builtin_amdgcn_sched_barrier(0);
     }
     const bool more = kSteady || kt + 1 < ktiles;
@@ -390,11 +398,11 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
     }
     if (kSteady) {
 #pragma unroll
-      for (int idx = 0; idx < 8; ++idx) {
+      for (int idx = 0; idx < NSTEP; ++idx) {
         const int i = idx >> 1, j = idx & 1;
-        acc[i][j] = H::mfma32(f1.b[j], f1.a[i], acc[i][j]);
-        read_piece((S + 1) % kStages, 0, f0, idx);
-        if (idx & 1) issue_piece(kt + kStages, S, idx >> 1);
+        if (idx < NM) acc[i][j] = H::mfma32(f1.b[j], f1.a[i], acc[i][j]);
+        if (idx < NR) read_piece((S + 1) % kStages, 0, f0, idx);
+        if ((idx & 1) && (idx >> 1) < kPieces) issue_piece(kt + kStages, S, idx >> 1);
         __builtin_amdgcn_sched_barrier(0);
       }
     } else {
@@ -403,9 +411,9 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
         for (int piece = 0; piece < kPieces; ++piece) issue_piece(kt + kStages, S, piece);
       if (more)
 #pragma unroll
-        for (int r = 0; r < 8; ++r) read_piece((S + 1) % kStages, 0, f0, r);
+        for (int r = 0; r < NR; ++r) read_piece((S + 1) % kStages, 0, f0, r);
 #pragma unroll
-      for (int idx = 0; idx < 8; ++idx) {
+      for (int idx = 0; idx < NM; ++idx) {
         const int i = idx >> 1, j = idx & 1;
         acc[i][j] = H::mfma32(f1.b[j], f1.a[i], acc[i][j]);
       }
@@ -427,8 +435,8 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
   }
 
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int m = m0 + wm * 128 + i * 32 + frag_row;
+  for (int i = 0; i < MI; ++i) {
+    const int m = m0 + wm * (kTM / 2) + i * 32 + frag_row;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
 #pragma unroll

@@ -202,6 +202,13 @@ int launch_gemm_simt(const Mem& out, const Mem& lhs, const Mem& rhs, const Mem& 
   return finish_launch("matmul(simt)");
 }
 
+// MI355X has 256 CUs: the pipelined GEMM takes 128-row tiles when 256-row tiles would not
+// give every CU one (M % 256 == 0 on this path, so both divide M).
+constexpr long long kNumCUs = 256;
+long long pipe_tile_m(long long M, long long N) {
+  return (M / gemmp::kBM) * (N / gemmp::kBN) < kNumCUs ? 128 : 256;
+}
+
 template <typename Tag>
 int launch_gemm_mfma(const Mem& out, const Mem& lhs, const Mem& rhs, const Mem& bias, int M, int N, int K) {
   const bool masked = (M % gemm::kBM) || (N % gemm::kBN) || (K % gemm::kBK);
@@ -216,12 +223,21 @@ int launch_gemm_mfma(const Mem& out, const Mem& lhs, const Mem& rhs, const Mem& 
   hipLaunchKernelGGL((gemm_mfma_kernel<Tag, MASKED, BIAS>), dim3(tiles), dim3(gemm::kThreads), 0, g_stream, A, \
                      B, C, bp, M, N, K, lda, ldb, ldc)
   if (!masked && K % gemmp::kBK == 0) {
-#define KG_GEMM_PIPE(BIAS)                                                                                     \
-  hipLaunchKernelGGL((gemm_pipe_kernel<Tag, BIAS>), dim3(tiles), dim3(gemmp::kThreads), 0, g_stream, A, B, C, bp, M, N, \
-                     K, lda, ldb, ldc)
-    if (bias_kind == 0) KG_GEMM_PIPE(0);
-    else if (bias_kind == 1) KG_GEMM_PIPE(1);
-    else KG_GEMM_PIPE(2);
+    // 128-row tiles when 256-row ones would leave CUs idle (C2': 8192x1024 is 128 tiles)
+    const bool half = pipe_tile_m(M, N) == 128;
+    const int grid = (int)((M / pipe_tile_m(M, N)) * (N / gemmp::kBN));
+#define KG_GEMM_PIPE(BIAS, TM)                                                                                  \
+  hipLaunchKernelGGL((gemm_pipe_kernel<Tag, BIAS, TM>), dim3(grid), dim3(gemmp::kThreads), 0, g_stream, A, B, C, bp, M, \
+                     N, K, lda, ldb, ldc)
+    if (half) {
+      if (bias_kind == 0) KG_GEMM_PIPE(0, 128);
+      else if (bias_kind == 1) KG_GEMM_PIPE(1, 128);
+      else KG_GEMM_PIPE(2, 128);
+    } else {
+      if (bias_kind == 0) KG_GEMM_PIPE(0, 256);
+      else if (bias_kind == 1) KG_GEMM_PIPE(1, 256);
+      else KG_GEMM_PIPE(2, 256);
+    }
 #undef KG_GEMM_PIPE
     return finish_launch("matmul(mfma-pipe)");
   }
@@ -275,8 +291,8 @@ int matmul_impl(const KgArgSlot* args, unsigned long long n) {
     long long mfma = 0;
     if (mfma_ok && M > 0 && N > 0) {
       const bool pipe = M % gemmp::kBM == 0 && N % gemmp::kBN == 0 && K % gemm::kBK == 0;
-      if (pipe)  // 8 waves x 16 MFMAs (32x32x16) per 32-deep slice of a 256x256 tile
-        mfma = (M / gemmp::kBM) * (N / gemmp::kBN) * (K / gemmp::kBK) * 128;
+      if (pipe)  // 8 waves x tm/16 MFMAs (32x32x16) per 32-deep slice of a tm x 256 tile
+        mfma = (M / pipe_tile_m(M, N)) * (N / gemmp::kBN) * (K / gemmp::kBK) * (pipe_tile_m(M, N) / 2);
       else  // 4 waves x 64 MFMAs per 64-deep slice of a 256x256 tile
         mfma = ((M + gemm::kBM - 1) / gemm::kBM) * ((N + gemm::kBN - 1) / gemm::kBN) * ((K + gemm::kBK - 1) / gemm::kBK) * 256;
     }

@@ -6,7 +6,7 @@ counter run can be laid beside the model:
 Every case makes exactly one library kernel dispatch, in the order printed, and nothing
 else dispatches a kernel (inputs are generated on the host and copied), so dispatch i of the
 counter run is case i. Cases cover every kernel choice the model distinguishes:
-the pipelined and the masked MFMA GEMM, the SIMT GEMM, the MFMA conv with four and with two
+the pipelined MFMA GEMM with 256- and 128-row tiles, the masked MFMA GEMM, the SIMT GEMM, the MFMA conv with four and with two
 live waves and a ragged last row block, and the MFMA attention kernels for D=128 and D=64,
 causal and not, with ragged query and key tails.
 """
@@ -23,6 +23,7 @@ from .. import native
 # order of the family's entry; bias is always absent.
 CASES = (
     ("gemm_bf16_4096", "matmul", "bfloat16", ((4096, 4096), (4096, 4096), (4096, 4096)), ()),
+    ("gemm_bf16_c2s_8192x1024x4096", "matmul", "bfloat16", ((8192, 1024), (8192, 4096), (4096, 1024)), ()),
     ("gemm_f16_512x768x256", "matmul", "float16", ((512, 768), (512, 256), (256, 768)), ()),
     ("gemm_bf16_masked_1000x1000x520", "matmul", "bfloat16", ((1000, 1000), (1000, 520), (520, 1000)), ()),
     ("gemm_f32_256", "matmul", "float32", ((256, 256), (256, 256), (256, 256)), ()),

@@ -108,6 +108,27 @@ def test_16bit_shapes(device, oracle_mod, dtype_name, shape, bias_kind):
     assert_h16_close(to_numpy(out), ref, what=f"{dtype_name} {shape} bias={bias_kind}")
 
 
+@pytest.mark.parametrize("bias_kind", ["f32", "same"])
+def test_pipe_256_row_tiles_with_bias(device, oracle_mod, bias_kind):
+    """4096 x 4096 outputs are 256 tiles of 256 x 256 (one per CU): the 256-row pipelined
+    path; smaller aligned shapes above take its 128-row tiles."""
+
+    import torch
+
+    m, k, n = 4096, 64, 4096
+    rng = np.random.default_rng(91)
+    lt, lhs = round_to(rng.normal(size=(m, k)) * 0.5, torch.bfloat16)
+    rt, rhs = round_to(rng.normal(size=(k, n)) * 0.5, torch.bfloat16)
+    if bias_kind == "f32":
+        bias = rng.normal(size=(n,)).astype(np.float32)
+        bt = bias
+    else:
+        bt, bias = round_to(rng.normal(size=(n,)), torch.bfloat16)
+    ref = oracle_mod.matmul_demo(lhs, rhs, bias, (64, 64, 64))
+    out = run(device, torch.bfloat16, lt, rt, bt)
+    assert_h16_close(to_numpy(out), ref, what=f"4096x64x4096 bias={bias_kind}")
+
+
 @pytest.mark.parametrize(
     "cfg",
     [
