@@ -17,7 +17,8 @@ The JSON line also carries
   cpu_baseline: the oracle's restatement of the reference's npu_demo matmul loop nest,
             compiled without optimisation like the reference (g++ -shared -fPIC, no -O)
             and run on 2 host threads (npu_demo block_num = 2) over a bounded sample of
-            the same workload (the first 384 output rows);
+            the same workload (the first 384 output rows), plus the same sample built with
+            -O2 (optimized_value) and the host CPU model;
   secondary: the other BASELINE configs (C1, C2', C3, C4, C5 D=128/64), each after 0.15 s
             of untimed launches, over >= 200 (C1, C2'), 1000 (C3), 100 (C4) or 25 (C5)
             back-to-back launches.
@@ -128,15 +129,32 @@ def cpu_baseline_matmul(rows: int = 384):
     oracle.matmul_demo(a, b, None, (48, 80, 56), threads=2, m_range=(0, rows), optimized=False)
     dt = time.perf_counter() - t0
     flop = 2.0 * rows * 4096 * 4096
+    # the same sample through the same loop nest built with optimisation
+    t0 = time.perf_counter()
+    oracle.matmul_demo(a, b, None, (48, 80, 56), threads=2, m_range=(0, rows), optimized=True)
+    dt_opt = time.perf_counter() - t0
     return {
         "value": flop / dt / 1e12,
         "unit": "TFLOP/s",
         "cores": 2,
         "kind": "port",
         "sample": f"output rows 0-{rows - 1} of the 4096^3 matmul ({flop / 1e9:.1f} GFLOP) through the restated "
-                  f"npu_demo tile loop (tiles 48x80x56, fp32, -O0, 2 threads): {dt:.2f} s",
+                  f"npu_demo tile loop (tiles 48x80x56, fp32, -O0 like the reference's build, 2 threads): {dt:.2f} s",
+        "optimized_value": flop / dt_opt / 1e12,
+        "optimized_sample": f"the same rows built with -O2: {dt_opt:.2f} s",
         "host_cpus": os.cpu_count(),
+        "cpu_model": cpu_model(),
     }
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 SECONDARY_KEYS = ("c1", "c2s", "c3", "c4", "c5d128", "c5d64")
