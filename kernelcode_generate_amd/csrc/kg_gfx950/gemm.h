@@ -466,15 +466,20 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
 }
 
 // Generic path: any element type, any shape/strides (element strides), optional bias.
-// Each 256-thread block computes a 64x64 tile; each thread a 4x4 micro tile.
-template <typename TA, typename TB, typename TC, typename TBias>
+// Each 256-thread block computes a T x T tile (T = 64, 32 or 16: the host picks the largest
+// that still gives every CU a block); each thread a T/16 x T/16 micro tile. K advances in
+// 32-deep slices; the next slice is loaded into registers while the FMAs of the current
+// one run, so the loop pays one global-load latency in total rather than one per slice.
+template <typename TA, typename TB, typename TC, typename TBias, int T>
 __global__ __launch_bounds__(256) void gemm_simt_kernel(const TA* __restrict__ A, const TB* __restrict__ B,
                                                         TC* __restrict__ C, const TBias* __restrict__ bias,
                                                         int M, int N, int K, long long sam, long long sak,
                                                         long long sbk, long long sbn, long long scm,
                                                         long long scn, long long sbias) {
-  constexpr int T = 64;
-  constexpr int TK = 16;
+  static_assert(T == 64 || T == 32 || T == 16, "tile");
+  constexpr int MT = T / 16;  // micro tile
+  constexpr int TK = 32;
+  constexpr int kPer = T * TK / 256;  // elements of each operand per thread and slice
   __shared__ float As[TK][T + 1];
   __shared__ float Bs[TK][T + 1];
   const int tid = threadIdx.x;
@@ -482,49 +487,56 @@ __global__ __launch_bounds__(256) void gemm_simt_kernel(const TA* __restrict__ A
   const int ty = tid >> 4;
   const int m0 = blockIdx.y * T;
   const int n0 = blockIdx.x * T;
-  float acc[4][4];
+  float acc[MT][MT];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MT; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+    for (int j = 0; j < MT; ++j) acc[i][j] = 0.f;
 
-  for (int k0 = 0; k0 < K; k0 += TK) {
-    for (int e = tid; e < T * TK; e += 256) {
-      const int r = e / TK;
-      const int kk = e % TK;
-      const int m = m0 + r;
-      const int k = k0 + kk;
-      As[kk][r] = (m < M && k < K) ? Elem<TA>::load(A + m * sam + k * sak) : 0.f;
+  // element q of this thread: A row (tid + 256q) / TK, k (tid + 256q) % TK (consecutive
+  // threads walk k); B k-row (tid + 256q) / T, column (tid + 256q) % T (they walk n)
+  float ra[kPer], rb[kPer];
+  auto load_slice = [&](int k0) {
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      const int e = tid + 256 * q;
+      const int m = m0 + e / TK, ka = k0 + e % TK;
+      ra[q] = (m < M && ka < K) ? Elem<TA>::load(A + m * sam + ka * sak) : 0.f;
+      const int kb = k0 + e / T, n = n0 + e % T;
+      rb[q] = (kb < K && n < N) ? Elem<TB>::load(B + kb * sbk + n * sbn) : 0.f;
     }
-    for (int e = tid; e < T * TK; e += 256) {
-      const int kk = e / T;
-      const int c = e % T;
-      const int k = k0 + kk;
-      const int n = n0 + c;
-      Bs[kk][c] = (k < K && n < N) ? Elem<TB>::load(B + k * sbk + n * sbn) : 0.f;
+  };
+  load_slice(0);
+  for (int k0 = 0; k0 < K; k0 += TK) {
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      const int e = tid + 256 * q;
+      As[e % TK][e / TK] = ra[q];
+      Bs[e / T][e % T] = rb[q];
     }
     __syncthreads();
+    if (k0 + TK < K) load_slice(k0 + TK);
 #pragma unroll
     for (int kk = 0; kk < TK; ++kk) {
-      float a[4], b[4];
+      float a[MT], b[MT];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = As[kk][ty * 4 + i];
+      for (int i = 0; i < MT; ++i) a[i] = As[kk][ty * MT + i];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = Bs[kk][tx * 4 + j];
+      for (int j = 0; j < MT; ++j) b[j] = Bs[kk][tx * MT + j];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < MT; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(a[i], b[j], acc[i][j]);
+        for (int j = 0; j < MT; ++j) acc[i][j] = __builtin_fmaf(a[i], b[j], acc[i][j]);
     }
     __syncthreads();
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int m = m0 + ty * 4 + i;
+  for (int i = 0; i < MT; ++i) {
+    const int m = m0 + ty * MT + i;
     if (m >= M) continue;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int n = n0 + tx * 4 + j;
+    for (int j = 0; j < MT; ++j) {
+      const int n = n0 + tx * MT + j;
       if (n >= N) continue;
       float v = acc[i][j];
       if (bias != nullptr) v += Elem<TBias>::load(bias + n * sbias);

@@ -193,12 +193,20 @@ int grid_1d(long long total, int threads) {
 
 template <typename TA, typename TBias>
 int launch_gemm_simt(const Mem& out, const Mem& lhs, const Mem& rhs, const Mem& bias, int M, int N, int K) {
-  dim3 grid((N + 63) / 64, (M + 63) / 64);
   const long long sbias = bias.present ? bias.stride[0] : 0;
-  hipLaunchKernelGGL((gemm_simt_kernel<TA, TA, TA, TBias>), grid, dim3(256), 0, g_stream,
-                     static_cast<const TA*>(lhs.data), static_cast<const TA*>(rhs.data), static_cast<TA*>(out.data),
-                     static_cast<const TBias*>(bias.present ? bias.data : nullptr), M, N, K, lhs.stride[0],
-                     lhs.stride[1], rhs.stride[0], rhs.stride[1], out.stride[0], out.stride[1], sbias);
+  auto blocks = [&](int t) { return (long long)((N + t - 1) / t) * ((M + t - 1) / t); };
+  // the largest tile that still gives every CU a block (256-thread blocks of T x T outputs)
+  const int t = blocks(64) >= 256 ? 64 : blocks(32) >= 256 ? 32 : 16;
+#define KG_GEMM_SIMT(T)                                                                                          \
+  hipLaunchKernelGGL((gemm_simt_kernel<TA, TA, TA, TBias, T>), dim3((N + T - 1) / T, (M + T - 1) / T), dim3(256), 0, \
+                     g_stream, static_cast<const TA*>(lhs.data), static_cast<const TA*>(rhs.data),                   \
+                     static_cast<TA*>(out.data), static_cast<const TBias*>(bias.present ? bias.data : nullptr), M, N, \
+                     K, lhs.stride[0], lhs.stride[1], rhs.stride[0], rhs.stride[1], out.stride[0], out.stride[1],   \
+                     sbias)
+  if (t == 64) KG_GEMM_SIMT(64);
+  else if (t == 32) KG_GEMM_SIMT(32);
+  else KG_GEMM_SIMT(16);
+#undef KG_GEMM_SIMT
   return finish_launch("matmul(simt)");
 }
 
