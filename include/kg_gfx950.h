@@ -69,10 +69,13 @@ typedef struct KgArgSlot {
  * kernel/matmul/inputs_static_tile_dynamic.py:64-120,
  * kernel/matmul/inputs_dynamic_tile_dynamic.py:57-113.
  * Slot order (test/cuda/test_cuda_sm89_kernel_demos_runtime.py:520):
- *   (out[M,N], lhs[M,K], rhs[K,N], bias[N] | absent [, tile_m, tile_n, tile_k])
- * 4 or 7 slots. dtypes: all f32, all bf16 or all f16 (bias may be f32 with bf16/f16
+ *   (out[M,N], lhs[M,K], rhs[K,N], bias[N] | absent [, tile_m, tile_n, tile_k [, memory_stage]])
+ * 4, 7 or 8 slots. dtypes: all f32, all bf16 or all f16 (bias may be f32 with bf16/f16
  * operands). Absent bias = memory slot with data == NULL (runtime_args.py:497-516).
- * Result: out = lhs @ rhs (+ bias[None, :]), fp32 accumulation.
+ * Result: out = lhs @ rhs (+ bias[None, :]), fp32 accumulation. Slot 7 is an additive
+ * extension: INT memory_stage in {2, 3, 4}, the LDS ring depth of the pipelined 16-bit
+ * kernel (the gfx950 reading of the reference's multi-buffer memory_stage,
+ * kernel_gen/passes/memory/multi_buffer.py; default 4); other kernels ignore it.
  */
 int kg_gfx950_matmul_entry(const KgArgSlot* ordered_args, unsigned long long arg_count);
 
@@ -132,8 +135,8 @@ enum {
  * (kernel_gen/tools/dsl_run.py:656-730), which runs the npu_demo cost pipeline and
  * returns one integer per cost kind (DMA1..DMA4, MAC, VECTOR1, VECTOR2). op is a
  * KG_OP_* code; ordered_args/arg_count are exactly the slots the matching entry above
- * takes (memory slots need shapes, strides and dtypes; their data pointers are not
- * read). The entry's own validation and kernel choice run unchanged, so a call the
+ * takes (memory slots need shapes, strides and dtypes; a non-NULL data pointer marks a
+ * present operand and is never dereferenced). The entry's own validation and kernel choice run unchanged, so a call the
  * entry would reject fails here with the same code and message. On success writes
  * KG_COST_KINDS values to costs[] and returns 0.
  */

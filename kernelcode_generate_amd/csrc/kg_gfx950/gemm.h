@@ -216,8 +216,8 @@ __global__ __launch_bounds__(gemm::kThreads, 1) void gemm_mfma_kernel(
 //   kTM x 256 tiles (kTM = 256, or 128 when 256-row tiles would leave CUs idle) computed by
 //   8 waves (2 x 4 waves of kTM/2 x 64, two per SIMD) with 32x32x16 MFMAs. Both operands
 //   are copied HBM -> LDS by global_load_lds_dwordx4 (no registers, no VALU work) through a
-//   4-stage ring of 32-deep K slices (4 x (kTM/16 + 16) KiB), so loads are issued three
-//   slices ahead of their use; every wave issues kTM/128 + 2 of a slice's copies (1 KiB
+//   kStages-deep ring of 32-deep K slices (kStages x (kTM/16 + 16) KiB; 4 by default, 2 or
+//   3 on request), so loads are issued kStages - 1 slices ahead of their use; every wave issues kTM/128 + 2 of a slice's copies (1 KiB
 //   each), slotted between its MFMAs, and while one wave of a SIMD waits on a copy's issue
 //   or an LDS read the other keeps the MFMA pipe busy. lhs slices are [m][k] rows of 64 bytes; rhs slices
 //   stay [k][n] as in HBM and the MFMA operand (8 consecutive k of one n) is read with two
@@ -231,7 +231,7 @@ namespace gemmp {
 constexpr int kBM = 256;  // largest tile height (kTM)
 constexpr int kBN = 256;
 constexpr int kBK = 32;
-constexpr int kStages = 4;
+constexpr int kDefaultStages = 4;  // LDS ring depth unless the caller asks for 2 or 3
 constexpr int kThreads = 512;  // 8 waves: 2 x 4 of kTM/2 x 64, two per SIMD
 constexpr int kBVecs = kBK * kBN / 8;  // 1024 u32x4 per rhs stage
 // LDS has 64 banks of 4 bytes: ds_read_b128 serves 16 lanes per cycle, 64-bit reads 32.
@@ -246,13 +246,14 @@ struct StageIdx {
 };
 }  // namespace gemmp
 
-template <typename Tag, int kBias, int kTM>
+template <typename Tag, int kBias, int kTM, int kStages>
 __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, uint16_t* __restrict__ C,
     const void* __restrict__ bias, int M, int N, int K, long long lda, long long ldb, long long ldc) {
   using namespace gemmp;
   using H = Half16<Tag>;
   static_assert(kTM == 256 || kTM == 128, "tile height");
+  static_assert(kStages >= 2 && kStages <= 4, "ring depth");
   constexpr int MI = kTM / 64;              // 32-row fragments per wave
   constexpr int AP = kTM / 128;             // lhs copies per wave per slice
   constexpr int kPieces = AP + 2;           // copies per wave per slice: AP lhs, 2 rhs
@@ -389,7 +390,7 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
     const bool more = kSteady || kt + 1 < ktiles;
     const bool refill = kSteady || kt + kStages < ktiles;
     if (kSteady) {
-      wait_and_barrier<2 * kPieces>();
+      wait_and_barrier<(kStages - 2) * kPieces>();  // slices kt+2 .. kt+kStages-1 may be in flight
     } else if (more) {
       const int younger = min(kStages - 2, ktiles - 2 - kt);
       if (younger >= 2) wait_and_barrier<2 * kPieces>();
@@ -424,14 +425,16 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
   for (; kt + 2 * kStages <= ktiles; kt += kStages) {  // every slice refills its stage
     slice(kt, StageIdx<0>{}, StageIdx<1>{});
     slice(kt + 1, StageIdx<1>{}, StageIdx<1>{});
-    slice(kt + 2, StageIdx<2>{}, StageIdx<1>{});
-    slice(kt + 3, StageIdx<3>{}, StageIdx<1>{});
+    if constexpr (kStages > 2) slice(kt + 2, StageIdx<2 % kStages>{}, StageIdx<1>{});
+    if constexpr (kStages > 3) slice(kt + 3, StageIdx<3 % kStages>{}, StageIdx<1>{});
   }
   for (; kt < ktiles; kt += kStages) {
     slice(kt, StageIdx<0>{}, StageIdx<0>{});
     if (kt + 1 < ktiles) slice(kt + 1, StageIdx<1>{}, StageIdx<0>{});
-    if (kt + 2 < ktiles) slice(kt + 2, StageIdx<2>{}, StageIdx<0>{});
-    if (kt + 3 < ktiles) slice(kt + 3, StageIdx<3>{}, StageIdx<0>{});
+    if constexpr (kStages > 2)
+      if (kt + 2 < ktiles) slice(kt + 2, StageIdx<2 % kStages>{}, StageIdx<0>{});
+    if constexpr (kStages > 3)
+      if (kt + 3 < ktiles) slice(kt + 3, StageIdx<3 % kStages>{}, StageIdx<0>{});
   }
 
 #pragma unroll

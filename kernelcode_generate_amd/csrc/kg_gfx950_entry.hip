@@ -218,7 +218,8 @@ long long pipe_tile_m(long long M, long long N) {
 }
 
 template <typename Tag>
-int launch_gemm_mfma(const Mem& out, const Mem& lhs, const Mem& rhs, const Mem& bias, int M, int N, int K) {
+int launch_gemm_mfma(const Mem& out, const Mem& lhs, const Mem& rhs, const Mem& bias, int M, int N, int K,
+                     int stages) {
   const bool masked = (M % gemm::kBM) || (N % gemm::kBN) || (K % gemm::kBK);
   const int tiles = ((M + gemm::kBM - 1) / gemm::kBM) * ((N + gemm::kBN - 1) / gemm::kBN);
   const uint16_t* A = static_cast<const uint16_t*>(lhs.data);
@@ -234,18 +235,24 @@ int launch_gemm_mfma(const Mem& out, const Mem& lhs, const Mem& rhs, const Mem& 
     // 128-row tiles when 256-row ones would leave CUs idle (C2': 8192x1024 is 128 tiles)
     const bool half = pipe_tile_m(M, N) == 128;
     const int grid = (int)((M / pipe_tile_m(M, N)) * (N / gemmp::kBN));
-#define KG_GEMM_PIPE(BIAS, TM)                                                                                  \
-  hipLaunchKernelGGL((gemm_pipe_kernel<Tag, BIAS, TM>), dim3(grid), dim3(gemmp::kThreads), 0, g_stream, A, B, C, bp, M, \
-                     N, K, lda, ldb, ldc)
+#define KG_GEMM_PIPE(BIAS, TM, ST)                                                                                  \
+  hipLaunchKernelGGL((gemm_pipe_kernel<Tag, BIAS, TM, ST>), dim3(grid), dim3(gemmp::kThreads), 0, g_stream, A, B, C, bp, \
+                     M, N, K, lda, ldb, ldc)
+#define KG_GEMM_PIPE_BIAS(TM, ST)               \
+  if (bias_kind == 0) KG_GEMM_PIPE(0, TM, ST);   \
+  else if (bias_kind == 1) KG_GEMM_PIPE(1, TM, ST); \
+  else KG_GEMM_PIPE(2, TM, ST)
+#define KG_GEMM_PIPE_DEPTH(TM)                   \
+  if (stages == 2) { KG_GEMM_PIPE_BIAS(TM, 2); }   \
+  else if (stages == 3) { KG_GEMM_PIPE_BIAS(TM, 3); } \
+  else { KG_GEMM_PIPE_BIAS(TM, 4); }
     if (half) {
-      if (bias_kind == 0) KG_GEMM_PIPE(0, 128);
-      else if (bias_kind == 1) KG_GEMM_PIPE(1, 128);
-      else KG_GEMM_PIPE(2, 128);
+      KG_GEMM_PIPE_DEPTH(128)
     } else {
-      if (bias_kind == 0) KG_GEMM_PIPE(0, 256);
-      else if (bias_kind == 1) KG_GEMM_PIPE(1, 256);
-      else KG_GEMM_PIPE(2, 256);
+      KG_GEMM_PIPE_DEPTH(256)
     }
+#undef KG_GEMM_PIPE_DEPTH
+#undef KG_GEMM_PIPE_BIAS
 #undef KG_GEMM_PIPE
     return finish_launch("matmul(mfma-pipe)");
   }
@@ -264,20 +271,25 @@ int launch_gemm_mfma(const Mem& out, const Mem& lhs, const Mem& rhs, const Mem& 
 
 int matmul_impl(const KgArgSlot* args, unsigned long long n) {
   if (args == nullptr) return fail(kInvalid, "ordered_args is null");
-  if (n != 4 && n != 7) return fail(kInvalid, "matmul expects 4 or 7 slots, got %llu", n);
+  if (n != 4 && n != 7 && n != 8) return fail(kInvalid, "matmul expects 4, 7 or 8 slots, got %llu", n);
   Mem out, lhs, rhs, bias;
   int rc;
   if ((rc = read_mem(args, 0, 2, false, "out", &out))) return rc;
   if ((rc = read_mem(args, 1, 2, false, "lhs", &lhs))) return rc;
   if ((rc = read_mem(args, 2, 2, false, "rhs", &rhs))) return rc;
   if ((rc = read_mem(args, 3, 1, true, "bias", &bias))) return rc;
-  if (n == 7) {
+  if (n >= 7) {
     long long t;
     const char* names[3] = {"tile_m", "tile_n", "tile_k"};
     for (int i = 0; i < 3; ++i) {
       if ((rc = read_int(args, 4 + i, names[i], &t))) return rc;
       if (t <= 0) return fail(kInvalid, "%s must be positive, got %lld", names[i], t);
     }
+  }
+  long long stages = gemmp::kDefaultStages;  // LDS ring depth of the pipelined MFMA kernel
+  if (n == 8) {
+    if ((rc = read_int(args, 7, "memory_stage", &stages))) return rc;
+    if (stages < 2 || stages > 4) return fail(kInvalid, "matmul: memory_stage must be 2, 3 or 4, got %lld", stages);
   }
   const long long M = lhs.shape[0], K = lhs.shape[1], N = rhs.shape[1];
   if (rhs.shape[0] != K) return fail(kInvalid, "matmul: lhs K=%lld != rhs K=%lld", K, rhs.shape[0]);
@@ -313,11 +325,11 @@ int matmul_impl(const KgArgSlot* args, unsigned long long n) {
     return launch_gemm_simt<float, float>(out, lhs, rhs, bias, m, nn, k);
   }
   if (out.dtype == KG_DTYPE_BF16) {
-    if (mfma_ok) return launch_gemm_mfma<Bf16Tag>(out, lhs, rhs, bias, m, nn, k);
+    if (mfma_ok) return launch_gemm_mfma<Bf16Tag>(out, lhs, rhs, bias, m, nn, k, (int)stages);
     if (bias.present && bias.dtype == KG_DTYPE_F32) return launch_gemm_simt<__bf16, float>(out, lhs, rhs, bias, m, nn, k);
     return launch_gemm_simt<__bf16, __bf16>(out, lhs, rhs, bias, m, nn, k);
   }
-  if (mfma_ok) return launch_gemm_mfma<F16Tag>(out, lhs, rhs, bias, m, nn, k);
+  if (mfma_ok) return launch_gemm_mfma<F16Tag>(out, lhs, rhs, bias, m, nn, k, (int)stages);
   if (bias.present && bias.dtype == KG_DTYPE_F32) return launch_gemm_simt<_Float16, float>(out, lhs, rhs, bias, m, nn, k);
   return launch_gemm_simt<_Float16, _Float16>(out, lhs, rhs, bias, m, nn, k);
 }

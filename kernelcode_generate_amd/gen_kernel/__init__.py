@@ -27,7 +27,7 @@ from ..core.error import ErrorKind, ErrorModule, KernelCodeError
 BUNDLE_MARKER_PREFIX = "// __KG_BUNDLE_FILE__:"
 ENTRY_POINT = "kg_execute_entry"
 LIBRARY_ENTRY = {
-    "matmul": ("kg_gfx950_matmul_entry", (4, 7)),
+    "matmul": ("kg_gfx950_matmul_entry", (4, 7, 8)),
     "conv2d": ("kg_gfx950_conv2d_entry", (12, 17)),
     "flash_attention": ("kg_gfx950_flash_attention_entry", (4, 6, 8)),
 }

@@ -9,6 +9,15 @@ steps that run here act on the recognised ``KernelPattern``: option checks, the 
 fusion rule of KernelAggregatePass(matmul_acc=True) (sequential-k accumulation, which the
 GPU kernels honour by accumulating every k in fp32), the static-tile legality check, and
 attaching the gfx950 hardware description (CUs, wave width, LDS bytes).
+
+``memory_stage`` (option, 2-4) is the gfx950 reading of MultiBufferAnalysisPass's
+``memory_stage`` (kernel_gen/passes/memory/multi_buffer.py, npu-demo-lowering uses 2): the
+depth of the ring the staged operands cycle through. For matmul kernels it becomes the
+LDS ring depth of the pipelined MFMA GEMM, passed as a trailing INT slot; without the
+option the library uses 4. Like the reference pass on IR it cannot ring, it leaves conv2d
+and attention alone (their K/V and channel-group buffers are fixed double buffers). The
+software pipelining LoopSoftPipelinePass builds in IR (prologue, steady loop, epilogue) is
+what every gfx950 kernel does already, so that pass has no knob here.
 """
 
 from __future__ import annotations
@@ -96,6 +105,18 @@ def _kernel_aggregate(state: LoweredKernel) -> LoweredKernel:
     return state
 
 
+def _multi_buffer(stage: int) -> Callable[[LoweredKernel], LoweredKernel]:
+    def run(state: LoweredKernel) -> LoweredKernel:
+        p = state.pattern
+        if p.family != "matmul":
+            return state
+        if len(p.params) + len(p.baked) != 7:
+            raise _error(f"{p.function}: memory_stage needs the tile slots (7 forwarded slots)")
+        return replace(state, pattern=replace(p, trailing=p.trailing + (("memory_stage", stage),)))
+
+    return run
+
+
 def _attach_arch_information(state: LoweredKernel) -> LoweredKernel:
     keys = ("block_num", "thread_num", "subthread_num", "sm_memory_size")
     return replace(state, hardware={k: get_target_hardware("gfx950", k) for k in keys})
@@ -104,13 +125,23 @@ def _attach_arch_information(state: LoweredKernel) -> LoweredKernel:
 @register_pipeline("gfx950-lowering")
 def build_gfx950_lowering_pipeline(options: dict | None = None) -> PassManager:
     opts = {} if options is None else dict(options)
-    unknown = sorted(set(opts) - {"target"})
+    unknown = sorted(set(opts) - {"target", "memory_stage"})
     if unknown:
-        raise _error(f"gfx950-lowering only accepts target option; got {', '.join(unknown)}")
+        raise _error(f"gfx950-lowering accepts target and memory_stage options; got {', '.join(unknown)}")
     if opts.get("target", "gfx950") != "gfx950":
         raise _error("gfx950-lowering target must be gfx950")
+    stage = None
+    if "memory_stage" in opts:
+        try:
+            stage = int(opts["memory_stage"])
+        except (TypeError, ValueError):
+            stage = None
+        if stage not in (2, 3, 4):
+            raise _error(f"gfx950-lowering memory_stage must be 2, 3 or 4, got {opts['memory_stage']!r}")
     pm = PassManager(name="gfx950-lowering")
     pm.add_pass("tile-analysis", _check_static_tiles)
     pm.add_pass("kernel-aggregate{matmul-acc=true}", _kernel_aggregate)
+    if stage is not None:
+        pm.add_pass(f"multi-buffer{{memory-stage={stage}}}", _multi_buffer(stage))
     pm.add_pass("attach-arch-information{target=gfx950}", _attach_arch_information)
     return pm

@@ -238,3 +238,35 @@ def test_dsl_run_contract_checks():
             dsl_run(matmul_inputs_static_tile_static_kernel, (1, 2, 3, None), "no-such-pipeline")
     finally:
         restore_config(snap)
+
+
+def test_memory_stage_option_drives_matmul_ring_depth():
+    """memory_stage (MultiBufferAnalysisPass's option, kernel_gen/passes/memory/multi_buffer.py)
+    reaches the matmul entry as a trailing INT slot; conv2d and attention are left alone."""
+
+    pm = get_pipeline("gfx950-lowering", {"memory_stage": "3"})
+    for fn in (matmul_inputs_static_tile_static_kernel, matmul_inputs_static_tile_dynamic_kernel):
+        lowered = pm.run(recognise(fn, "bfloat16"))
+        assert "multi-buffer{memory-stage=3}" in lowered.applied
+        assert lowered.pattern.trailing[-1] == ("memory_stage", 3)
+        src = gen_kernel(lowered.pattern)
+        assert "slots[7].int_value = 3LL;" in src and "kg_gfx950_matmul_entry(slots, 8ULL)" in src
+    fa = pm.run(recognise(flash_attention_scaled_causal_kernel, "bfloat16")).pattern
+    assert ("memory_stage", 3) not in fa.trailing
+    conv = pm.run(recognise(conv2d_inputs_static_tile_static_kernel)).pattern
+    assert ("memory_stage", 3) not in conv.trailing
+    for bad in ("1", "5", "two"):
+        with pytest.raises(KernelCodeError):
+            build_gfx950_lowering_pipeline({"memory_stage": bad})
+
+
+def test_memory_stage_slot_validated_without_gpu():
+    lib = native.load_library()
+    from kernelcode_generate_amd.native import TensorSpec as T
+
+    base = [T((256, 256), "bfloat16"), T((256, 64), "bfloat16"), T((64, 256), "bfloat16"), None, 64, 64, 64]
+    assert native.cost("matmul", base + [2])["MAC"] == 256 * 256 * 64
+    for bad in (1, 5):
+        with pytest.raises(native.NativeLibraryError, match="memory_stage"):
+            native.cost("matmul", base + [bad])
+    assert lib is not None

@@ -166,3 +166,23 @@ def test_stream_execution(device):
     stream.synchronize()
     assert r.ok
     assert torch.equal(out, out2)
+
+
+def test_memory_stage_pipeline_option(device):
+    """gfx950-lowering{memory_stage=2}: the generated entry forwards the ring depth to the
+    library, and the result is the default pipeline's, bit for bit."""
+
+    import torch
+
+    from kernelcode_generate_amd.pipeline import get_pipeline
+
+    set_target("gfx950")
+    a = torch.randn(512, 256, device="cuda").to(torch.bfloat16)
+    b = torch.randn(256, 512, device="cuda").to(torch.bfloat16)
+    out = torch.empty(512, 512, device="cuda", dtype=torch.bfloat16)
+    out2 = torch.zeros_like(out)
+    dsl_run(matmul_inputs_static_tile_dynamic_kernel, (out, a, b, None, 64, 64, 64), "gfx950-lowering")
+    staged = dsl_run(matmul_inputs_static_tile_dynamic_kernel, (out2, a, b, None, 64, 64, 64),
+                     get_pipeline("gfx950-lowering", {"memory_stage": "2"}))
+    assert "slots[7].int_value = 2LL;" in staged.source
+    assert torch.equal(out, out2)

@@ -179,3 +179,28 @@ def test_rejects_mismatched_shapes(device):
     lib = native.load_library()
     assert lib.kg_gfx950_matmul_entry(slots, 4) == -1
     assert "allocation" in native.last_error()
+
+
+@pytest.mark.parametrize("shape", [(512, 256, 768), (2048, 1024, 8192)], ids=["tile128", "tile256"])
+def test_memory_stage_depths_bit_identical(device, oracle_mod, shape):
+    """Slot 7 (memory_stage 2/3/4) changes only the LDS ring depth of the pipelined kernel,
+    not the order of any accumulation: every depth gives the default run's bits. Shapes
+    cover both tile heights and K lengths with steady slices and tails at every depth."""
+
+    import torch
+
+    m, k, n = shape
+    rng = np.random.default_rng(m + k + n)
+    lt, lhs = round_to(rng.standard_normal((m, k), dtype=np.float32) * 0.05, torch.bfloat16)
+    rt, rhs = round_to(rng.standard_normal((k, n), dtype=np.float32) * 0.05, torch.bfloat16)
+    default = run(device, torch.bfloat16, lt, rt)
+    a, b = lt.to(device), rt.to(device)
+    for stages in (2, 3, 4):
+        out = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=device)
+        print(f"[matmul] {shape} memory_stage={stages}", flush=True)
+        native.call_entry("kg_gfx950_matmul_entry", (out, a, b, None, 64, 64, 64, stages))
+        assert torch.equal(out, default), f"memory_stage={stages}"
+    ref = oracle_mod.matmul_demo(lhs[:64], rhs, None, (64, 64, 64))
+    assert_h16_close(to_numpy(default)[:64], ref, what=f"{shape} rows 0:64")
+    with pytest.raises(native.NativeLibraryError, match="memory_stage"):
+        native.call_entry("kg_gfx950_matmul_entry", (default, a, b, None, 64, 64, 64, 5))
