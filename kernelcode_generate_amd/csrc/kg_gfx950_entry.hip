@@ -70,6 +70,7 @@ struct Mem {
   bool present = false;
 
   bool contiguous() const {
+    if (numel() == 0) return true;  // no elements: any strides describe the same (empty) view
     long long expect = 1;
     for (int i = rank - 1; i >= 0; --i) {
       if (shape[i] != 1 && stride[i] != expect) return false;
@@ -104,10 +105,20 @@ int read_mem(const KgArgSlot* slots, int idx, int rank, bool allow_absent, const
   const KgArgSlot& s = slots[idx];
   if (s.kind != KG_ARG_MEMORY) return fail(kInvalid, "slot %d (%s): expected memory slot, got kind %d", idx, name, s.kind);
   if (s.data == nullptr) {
-    if (!allow_absent) return fail(kInvalid, "slot %d (%s): memory slot has no data", idx, name);
-    out->present = false;
-    out->dtype = s.dtype_code;
-    return kOk;
+    if (allow_absent) {
+      out->present = false;
+      out->dtype = s.dtype_code;
+      return kOk;
+    }
+    // an empty view may carry a null pointer (torch's zero-size tensors do); it is never
+    // dereferenced, so it is accepted like any other empty operand
+    bool empty_view = (int)s.rank == rank && s.shape != nullptr && s.stride != nullptr;
+    bool has_zero = false;
+    for (int i = 0; empty_view && i < rank; ++i) {
+      if (s.shape[i] < 0) empty_view = false;
+      if (s.shape[i] == 0) has_zero = true;
+    }
+    if (!empty_view || !has_zero) return fail(kInvalid, "slot %d (%s): memory slot has no data", idx, name);
   }
   if ((int)s.rank != rank) return fail(kInvalid, "slot %d (%s): expected rank %d, got %llu", idx, name, rank, s.rank);
   if (s.shape == nullptr || s.stride == nullptr) return fail(kInvalid, "slot %d (%s): missing shape/stride", idx, name);
@@ -491,6 +502,7 @@ int flash_attention_impl(const KgArgSlot* args, unsigned long long n) {
   s.d = (int)q.shape[3];
   s.scale = (float)scale;
   s.causal = (int)causal;
+  if (s.s_kv == 0 && out.numel() > 0) return fail(kInvalid, "flash_attention: no keys (S_kv == 0) for a non-empty output");
   if (g_cost == nullptr && out.numel() == 0) return finish_launch("flash_attention(empty)");
   if (s.d > 512) return fail(kUnsupported, "flash_attention: head dim %d > 512", s.d);
   if (s.causal && s.s_kv != s.s_q) return fail(kUnsupported, "flash_attention: causal mask needs S_q == S_kv");
