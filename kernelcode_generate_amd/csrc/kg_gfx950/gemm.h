@@ -1,19 +1,9 @@
 // GEMM kernels for the matmul demos: out[M,N] = lhs[M,K] @ rhs[K,N] (+ bias[N]),
 // row-major, fp32 accumulation.
 //
-// gemm_mfma_kernel: bf16/f16 operands on gfx950 MFMA (v_mfma_f32_32x32x16_{bf16,f16}; the
+// gemm_pipe_kernel: bf16/f16 operands on gfx950 MFMA (v_mfma_f32_32x32x16_{bf16,f16}; the
 //   32x32x16 form is the one that reaches full matrix-core rate on gfx950, the 16x16x32
-//   form issues at half of it). Macro tile 256x256x64, 256 threads = 4 waves in a 2x2
-//   layout, 128x128 per wave (4x4 MFMA blocks, 256 fp32 accumulators per lane). LDS
-//   double buffer, 2 x 64 KiB. lhs tiles are K-contiguous in HBM and land in LDS as [m][k]
-//   (aligned shapes: global_load_lds_dwordx4 straight into LDS, no registers); rhs tiles are
-//   N-contiguous, so each thread loads an 8(k) x 8(n) block with 16-byte loads and
-//   transposes it in registers (v_perm_b32) before writing [n][k] rows to LDS. Both LDS
-//   arrays use 128-byte rows whose 16-byte chunks are XOR-swizzled so that the MFMA
-//   fragment reads (ds_read_b128) and the tile writes are bank-conflict free.
-//   The MFMA is issued with the rhs fragment as operand A and the lhs fragment as
-//   operand B, which yields C^T blocks: every lane then owns 4 consecutive columns of
-//   one output row, stored as one 8-byte write.
+//   form issues at half of it), any M, N % 8 == 0, K % 8 == 0.
 //
 // gemm_simt_kernel: any dtype (f32/bf16/f16), any shape and stride; 64x64 LDS tiles,
 //   4x4 outputs per thread, fp32 FMA accumulation in k order.
@@ -24,196 +14,7 @@
 
 namespace kg_gfx950 {
 
-namespace gemm {
-
-constexpr int kBM = 256;
-constexpr int kBN = 256;
-constexpr int kBK = 64;
-constexpr int kThreads = 256;
-constexpr int kChunks = kBK / 8;          // 16-byte chunks per LDS row
-constexpr int kTileVecs = kBM * kChunks;  // u32x4 per operand tile (2048)
-
-__device__ __forceinline__ int swz_a(int row, int chunk) { return row * kChunks + (chunk ^ (row & 7)); }
-__device__ __forceinline__ int swz_b(int n, int chunk) {
-  return n * kChunks + (chunk ^ (n & 7) ^ ((n >> 3) & 7));
-}
-
-}  // namespace gemm
-
-// Requirements checked by the host: K % 8 == 0, N % 8 == 0, lda/ldb/ldc multiples of 8,
-// 16-byte aligned base pointers. kMasked handles M, N, K that are not tile multiples.
-template <typename Tag, bool kMasked, int kBias>  // kBias: 0 none, 1 fp32 bias, 2 16-bit bias
-__global__ __launch_bounds__(gemm::kThreads, 1) void gemm_mfma_kernel(
-    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, uint16_t* __restrict__ C,
-    const void* __restrict__ bias, int M, int N, int K, long long lda, long long ldb, long long ldc) {
-  using namespace gemm;
-  using H = Half16<Tag>;
-  __shared__ u32x4 lds[2][2][kTileVecs];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1;
-  const int wn = wave & 1;
-
-  // Workgroup -> output tile: XCD-local logical id, then groups of 4 tile-rows.
-  const int tiles_m = (M + kBM - 1) / kBM;
-  const int tiles_n = (N + kBN - 1) / kBN;
-  const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
-  constexpr int kGroupM = 4;
-  const int group_size = kGroupM * tiles_n;
-  const int group = logical / group_size;
-  const int first_m = group * kGroupM;
-  const int gm = min(tiles_m - first_m, kGroupM);
-  const int in_group = logical - group * group_size;
-  const int tm = first_m + in_group % gm;
-  const int tn = in_group / gm;
-  const int m0 = tm * kBM;
-  const int n0 = tn * kBN;
-
-  // lhs, masked path: 8 register loads per thread, row = i*32 + tid/8, chunk = tid%8.
-  const int a_row = tid >> 3;
-  const int a_chunk = tid & 7;
-  // lhs, aligned path: 8 direct HBM->LDS copies per wave; slab s = 8 rows x 8 chunks, lane l
-  // fetches the chunk that the swizzle places at LDS slot s*64 + l.
-  const int d_row = lane >> 3;
-  const int d_pc = lane & 7;
-  // rhs: one 8x8 block per thread: n-block nb = tid%32, k-block kb = tid/32.
-  const int b_nb = tid & 31;
-  const int b_kb = tid >> 5;
-
-  const uint16_t* a_ptr = A + (long long)(m0 + a_row) * lda + a_chunk * 8;
-  const uint16_t* b_ptr = B + (long long)(b_kb * 8) * ldb + n0 + b_nb * 8;
-
-  u32x4 a_pref[kMasked ? 8 : 1];
-  u32x4 b_pref[8];
-
-  auto load_tile = [&](int kt, int buf) {
-    const int k0 = kt * kBK;
-    if constexpr (kMasked) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int m = m0 + i * 32 + a_row;
-        const int k = k0 + a_chunk * 8;
-        a_pref[i] = (m < M && k < K) ? ld16(a_ptr + (long long)i * 32 * lda + k0) : u32x4{0, 0, 0, 0};
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int slab = wave * 8 + i;
-        const int row = slab * 8 + d_row;
-        const uint16_t* src = A + (long long)(m0 + row) * lda + k0 + 8 * (d_pc ^ (row & 7));
-        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)&lds[buf][0][slab * 64], 16, 0, 0);
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      if constexpr (kMasked) {
-        const int k = k0 + b_kb * 8 + r;
-        const int n = n0 + b_nb * 8;
-        b_pref[r] = (k < K && n < N) ? ld16(b_ptr + (long long)(k0 + r) * ldb) : u32x4{0, 0, 0, 0};
-      } else {
-        b_pref[r] = ld16(b_ptr + (long long)(k0 + r) * ldb);
-      }
-    }
-  };
-
-  auto store_tile = [&](int buf) {
-    if constexpr (kMasked) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int row = i * 32 + a_row;
-        lds[buf][0][swz_a(row, a_chunk)] = a_pref[i];
-      }
-    }
-    u32x4 bt[8];
-    transpose8x8_b16(b_pref, bt);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int n = b_nb * 8 + j;
-      lds[buf][1][swz_b(n, b_kb)] = bt[j];
-    }
-  };
-
-  // 32x32 blocks: acc[i][j] covers rows wm*128 + 32i .., cols wn*128 + 32j ..
-  f32x16 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
-
-  const int ktiles = (K + kBK - 1) / kBK;
-  load_tile(0, 0);
-  store_tile(0);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-
-  const int frag_row = lane & 31;
-  const int frag_half = lane >> 5;
-
-  for (int kt = 0; kt < ktiles; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < ktiles) load_tile(kt + 1, cur ^ 1);
-#pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      const int c = 2 * ks + frag_half;
-      u32x4 af[4];
-      u32x4 bf[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) af[i] = lds[cur][0][swz_a(wm * 128 + i * 32 + frag_row, c)];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bf[j] = lds[cur][1][swz_b(wn * 128 + j * 32 + frag_row, c)];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = H::mfma32(bf[j], af[i], acc[i][j]);
-    }
-    if (kt + 1 < ktiles) store_tile(cur ^ 1);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-  }
-
-  // Epilogue: the MFMA ran as C^T = B^T A^T, so lane l holds C[m][n..n+3] with
-  // m = row block + l%32 and n = col block + 8q + 4*(l/32), q = 0..3.
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int m = m0 + wm * 128 + i * 32 + frag_row;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int n = n0 + wn * 128 + j * 32 + 8 * q + 4 * frag_half;
-        float v0 = acc[i][j][4 * q], v1 = acc[i][j][4 * q + 1], v2 = acc[i][j][4 * q + 2], v3 = acc[i][j][4 * q + 3];
-        if constexpr (kBias == 1) {
-          const float* bp = static_cast<const float*>(bias);
-          if (!kMasked || n < N) {
-            v0 += bp[n];
-            v1 += bp[n + 1];
-            v2 += bp[n + 2];
-            v3 += bp[n + 3];
-          }
-        } else if constexpr (kBias == 2) {
-          const uint16_t* bp = static_cast<const uint16_t*>(bias);
-          if (!kMasked || n < N) {
-            v0 += H::to_float(bp[n]);
-            v1 += H::to_float(bp[n + 1]);
-            v2 += H::to_float(bp[n + 2]);
-            v3 += H::to_float(bp[n + 3]);
-          }
-        }
-        u32x2 packed;
-        packed[0] = H::pack2(v0, v1);
-        packed[1] = H::pack2(v2, v3);
-        if (!kMasked || (m < M && n < N)) st8(C + (long long)m * ldc + n, packed);
-      }
-    }
-  }
-}
-
-// gemm_pipe_kernel: the aligned-shape path (M % kTM == 0, N % 256 == 0, K % 32 == 0).
-//   kTM x 256 tiles (kTM = 256, or 128 when 256-row tiles would leave CUs idle) computed by
+// gemm_pipe_kernel: kTM x 256 tiles (kTM = 256, or 128 when 256-row tiles would leave CUs idle) computed by
 //   8 waves (2 x 4 waves of kTM/2 x 64, two per SIMD) with 32x32x16 MFMAs. Both operands
 //   are copied HBM -> LDS by global_load_lds_dwordx4 (no registers, no VALU work) through a
 //   kStages-deep ring of 32-deep K slices (kStages x (kTM/16 + 16) KiB; 4 by default, 2 or
@@ -227,6 +28,11 @@ __global__ __launch_bounds__(gemm::kThreads, 1) void gemm_mfma_kernel(
 //   banks of the 64-bank LDS. Fragments are double-buffered in registers: while the MFMAs
 //   of one 16-deep half of a slice run, the other half (or the next slice's first half) is
 //   being read, and the per-slice barrier sits between the two halves.
+//   kRagged (M % kTM, N % 256 or K % 32 non-zero): the copies go through buffer loads whose
+//   out-of-range lanes land zeros in LDS (edge rows, edge column chunks, k >= K), and the
+//   epilogue stores only the rows and columns inside the matrix; the loop is unchanged.
+//   Host requirements: K % 8 == 0, N % 8 == 0, row strides multiples of 8 and at most
+//   2^22 elements, 16-byte aligned base pointers.
 namespace gemmp {
 constexpr int kBM = 256;  // largest tile height (kTM)
 constexpr int kBN = 256;
@@ -246,7 +52,7 @@ struct StageIdx {
 };
 }  // namespace gemmp
 
-template <typename Tag, int kBias, int kTM, int kStages>
+template <typename Tag, int kBias, int kTM, int kStages, bool kRagged>
 __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, uint16_t* __restrict__ C,
     const void* __restrict__ bias, int M, int N, int K, long long lda, long long ldb, long long ldc) {
@@ -270,8 +76,8 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
   const int wm = wave >> 2;  // kTM/2-row half of the tile
   const int wn = wave & 3;   // 64-column quarter
 
-  const int tiles_n = N / kBN;
-  const int tiles_m = M / kTM;
+  const int tiles_n = kRagged ? (N + kBN - 1) / kBN : N / kBN;
+  const int tiles_m = kRagged ? (M + kTM - 1) / kTM : M / kTM;
   const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
   constexpr int kGroupM = 4;
   const int group_size = kGroupM * tiles_n;
@@ -302,14 +108,36 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
   const uint32_t lds_b0 = lds_addr(&lds_b[0][0]);
   constexpr uint32_t kAStage = kAVecs * 16;
   constexpr uint32_t kBStage = kBVecs * 16;
+  // Ragged shapes: a copy lane whose lhs row or rhs column chunk lies outside the matrix
+  // takes voff kBufOOB for every slice, and one whose k lies at or beyond K (slice kt has
+  // k = 32 kt + the lane's k offset) takes it for that slice: both land zeros in LDS, which
+  // add nothing to the accumulators, and the epilogue stores only rows < M, columns < N.
+  uint32_t a_voff[AP], b_voff[2];
+  int a_klim = K, b_klim[2] = {K, K};
+  if constexpr (kRagged) {
+#pragma unroll
+    for (int p = 0; p < AP; ++p) a_voff[p] = m0 + a_row0 + 16 * p < M ? a_goff : kBufOOB;
+    a_klim = K - 8 * ((lane & 3) ^ a_mask(a_row0));
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int k = (wave * 2 + i) * 2 + (lane >> 5);
+      b_voff[i] = n0 + 8 * ((lane & 31) ^ b_mask(k)) < N ? b_goff[i] : kBufOOB;
+      b_klim[i] = K - k;
+    }
+  }
 
   auto issue_piece = [&](int kt, int s, int piece) {  // piece 0..kPieces-1: AP lhs then 2 rhs
     if (piece < AP) {
-      g2lds16_s(a_goff, a_tile + (long long)kt * kBK * 2 + piece * a_piece,
-                lds_a0 + s * kAStage + (wave * AP + piece) * 1024);
+      const char* src = a_tile + (long long)kt * kBK * 2 + piece * a_piece;
+      const uint32_t dst = lds_a0 + s * kAStage + (wave * AP + piece) * 1024;
+      if constexpr (kRagged) buf2lds16_s(kt * kBK < a_klim ? a_voff[piece] : kBufOOB, src, dst);
+      else g2lds16_s(a_goff, src, dst);
     } else {
       const int i = piece - AP;
-      g2lds16_s(b_goff[i], b_tile + kt * b_step, lds_b0 + s * kBStage + (wave * 2 + i) * 1024);
+      const char* src = b_tile + kt * b_step;
+      const uint32_t dst = lds_b0 + s * kBStage + (wave * 2 + i) * 1024;
+      if constexpr (kRagged) buf2lds16_s(kt * kBK < b_klim[i] ? b_voff[i] : kBufOOB, src, dst);
+      else g2lds16_s(b_goff[i], src, dst);
     }
   };
 
@@ -357,7 +185,7 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  const int ktiles = K / kBK;
+  const int ktiles = kRagged ? (K + kBK - 1) / kBK : K / kBK;
 #pragma unroll
   for (int st = 0; st < kStages; ++st)
     if (st < ktiles)
@@ -445,6 +273,7 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int n = n0 + wn * 64 + j * 32 + 8 * q + 4 * frag_half;
+        if (kRagged && (m >= M || n >= N)) continue;  // N % 8 == 0: n < N covers n .. n+3
         float v0 = acc[i][j][4 * q], v1 = acc[i][j][4 * q + 1], v2 = acc[i][j][4 * q + 2], v3 = acc[i][j][4 * q + 3];
         if constexpr (kBias == 1) {
           const float* bp = static_cast<const float*>(bias);

@@ -58,6 +58,29 @@ __device__ __forceinline__ void g2lds16_s(uint32_t voff, const void* sbase, uint
       : "memory", "m0");
 }
 
+// Same copy through a raw buffer resource (base = sbase, range kBufRange bytes, stride 0):
+// a lane whose voff is kBufOOB lies outside the range, reads nothing and lands zeros in
+// LDS. This is how the edges of ragged tiles are zero-filled without a branch. Every valid
+// voff must stay below kBufRange. Word 3 is the gfx9-family raw-buffer configuration
+// (32-bit data format, no swizzle).
+constexpr uint32_t kBufRange = 0x80000000u;
+constexpr uint32_t kBufOOB = 0x80000000u;
+__device__ __forceinline__ void buf2lds16_s(uint32_t voff, const void* sbase, uint32_t m0) {
+  const uint64_t p = (uint64_t)(uintptr_t)sbase;
+  u32x4 rsrc;
+  rsrc[0] = (uint32_t)p;
+  rsrc[1] = (uint32_t)(p >> 32);  // stride field (bits 48-61 of the resource) stays 0
+  rsrc[2] = kBufRange;
+  rsrc[3] = 0x00020000u;
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %0, %1, 0 offen lds"
+      :
+      : "v"(voff), "s"(rsrc), "s"(m0)
+      : "memory", "m0");
+}
+
 // LDS byte address of a shared-memory object (what M0 and ds_* addresses take).
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;

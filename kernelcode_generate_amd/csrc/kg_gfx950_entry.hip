@@ -222,62 +222,53 @@ int launch_gemm_simt(const Mem& out, const Mem& lhs, const Mem& rhs, const Mem& 
 }
 
 // MI355X has 256 CUs: the pipelined GEMM takes 128-row tiles when 256-row tiles would not
-// give every CU one (M % 256 == 0 on this path, so both divide M).
+// give every CU one.
 constexpr long long kNumCUs = 256;
+long long cdiv(long long a, long long b) { return (a + b - 1) / b; }
 long long pipe_tile_m(long long M, long long N) {
-  return (M / gemmp::kBM) * (N / gemmp::kBN) < kNumCUs ? 128 : 256;
+  return cdiv(M, gemmp::kBM) * cdiv(N, gemmp::kBN) < kNumCUs ? 128 : 256;
 }
+// Shapes the pipelined kernel covers without its ragged-edge copies.
+bool pipe_aligned(long long M, long long N, long long K) {
+  return M % pipe_tile_m(M, N) == 0 && N % gemmp::kBN == 0 && K % gemmp::kBK == 0;
+}
+// Row strides up to 2^22 elements keep every copy lane's byte offset within a tile below
+// 2^31 (the buffer range of the ragged copies; 255 rows x 2^23 bytes + 64).
+constexpr long long kMaxPipeLd = 1LL << 22;
 
 template <typename Tag>
 int launch_gemm_mfma(const Mem& out, const Mem& lhs, const Mem& rhs, const Mem& bias, int M, int N, int K,
                      int stages) {
-  const bool masked = (M % gemm::kBM) || (N % gemm::kBN) || (K % gemm::kBK);
-  const int tiles = ((M + gemm::kBM - 1) / gemm::kBM) * ((N + gemm::kBN - 1) / gemm::kBN);
   const uint16_t* A = static_cast<const uint16_t*>(lhs.data);
   const uint16_t* B = static_cast<const uint16_t*>(rhs.data);
   uint16_t* C = static_cast<uint16_t*>(out.data);
   const void* bp = bias.present ? bias.data : nullptr;
   const int bias_kind = !bias.present ? 0 : (bias.dtype == KG_DTYPE_F32 ? 1 : 2);
   const long long lda = lhs.stride[0], ldb = rhs.stride[0], ldc = out.stride[0];
-#define KG_GEMM_LAUNCH(MASKED, BIAS)                                                                     \
-  hipLaunchKernelGGL((gemm_mfma_kernel<Tag, MASKED, BIAS>), dim3(tiles), dim3(gemm::kThreads), 0, g_stream, A, \
-                     B, C, bp, M, N, K, lda, ldb, ldc)
-  if (!masked && K % gemmp::kBK == 0) {
-    // 128-row tiles when 256-row ones would leave CUs idle (C2': 8192x1024 is 128 tiles)
-    const bool half = pipe_tile_m(M, N) == 128;
-    const int grid = (int)((M / pipe_tile_m(M, N)) * (N / gemmp::kBN));
-#define KG_GEMM_PIPE(BIAS, TM, ST)                                                                                  \
-  hipLaunchKernelGGL((gemm_pipe_kernel<Tag, BIAS, TM, ST>), dim3(grid), dim3(gemmp::kThreads), 0, g_stream, A, B, C, bp, \
-                     M, N, K, lda, ldb, ldc)
-#define KG_GEMM_PIPE_BIAS(TM, ST)               \
-  if (bias_kind == 0) KG_GEMM_PIPE(0, TM, ST);   \
-  else if (bias_kind == 1) KG_GEMM_PIPE(1, TM, ST); \
-  else KG_GEMM_PIPE(2, TM, ST)
-#define KG_GEMM_PIPE_DEPTH(TM)                   \
-  if (stages == 2) { KG_GEMM_PIPE_BIAS(TM, 2); }   \
-  else if (stages == 3) { KG_GEMM_PIPE_BIAS(TM, 3); } \
-  else { KG_GEMM_PIPE_BIAS(TM, 4); }
-    if (half) {
-      KG_GEMM_PIPE_DEPTH(128)
-    } else {
-      KG_GEMM_PIPE_DEPTH(256)
-    }
+  // 128-row tiles when 256-row ones would leave CUs idle (C2': 8192x1024 is 128 tiles)
+  const long long tm = pipe_tile_m(M, N);
+  const bool ragged = !pipe_aligned(M, N, K);
+  const int grid = (int)(cdiv(M, tm) * cdiv(N, gemmp::kBN));
+#define KG_GEMM_PIPE(BIAS, TM, ST, RAG)                                                                              \
+  hipLaunchKernelGGL((gemm_pipe_kernel<Tag, BIAS, TM, ST, RAG>), dim3(grid), dim3(gemmp::kThreads), 0, g_stream, A, B, \
+                     C, bp, M, N, K, lda, ldb, ldc)
+#define KG_GEMM_PIPE_BIAS(TM, ST, RAG)               \
+  if (bias_kind == 0) KG_GEMM_PIPE(0, TM, ST, RAG);   \
+  else if (bias_kind == 1) KG_GEMM_PIPE(1, TM, ST, RAG); \
+  else KG_GEMM_PIPE(2, TM, ST, RAG)
+#define KG_GEMM_PIPE_DEPTH(TM, RAG)                        \
+  if (stages == 2) { KG_GEMM_PIPE_BIAS(TM, 2, RAG); }      \
+  else if (stages == 3) { KG_GEMM_PIPE_BIAS(TM, 3, RAG); } \
+  else { KG_GEMM_PIPE_BIAS(TM, 4, RAG); }
+  if (tm == 128) {
+    if (ragged) { KG_GEMM_PIPE_DEPTH(128, true) } else { KG_GEMM_PIPE_DEPTH(128, false) }
+  } else {
+    if (ragged) { KG_GEMM_PIPE_DEPTH(256, true) } else { KG_GEMM_PIPE_DEPTH(256, false) }
+  }
 #undef KG_GEMM_PIPE_DEPTH
 #undef KG_GEMM_PIPE_BIAS
 #undef KG_GEMM_PIPE
-    return finish_launch("matmul(mfma-pipe)");
-  }
-  if (masked) {
-    if (bias_kind == 0) KG_GEMM_LAUNCH(true, 0);
-    else if (bias_kind == 1) KG_GEMM_LAUNCH(true, 1);
-    else KG_GEMM_LAUNCH(true, 2);
-  } else {
-    if (bias_kind == 0) KG_GEMM_LAUNCH(false, 0);
-    else if (bias_kind == 1) KG_GEMM_LAUNCH(false, 1);
-    else KG_GEMM_LAUNCH(false, 2);
-  }
-#undef KG_GEMM_LAUNCH
-  return finish_launch("matmul(mfma)");
+  return finish_launch(ragged ? "matmul(mfma-pipe-ragged)" : "matmul(mfma-pipe)");
 }
 
 int matmul_impl(const KgArgSlot* args, unsigned long long n) {
@@ -316,16 +307,16 @@ int matmul_impl(const KgArgSlot* args, unsigned long long n) {
   const int m = (int)M, nn = (int)N, k = (int)K;
   const bool mfma_ok = out.dtype != KG_DTYPE_F32 && k > 0 && (k % 8 == 0) && (nn % 8 == 0) && lhs.stride[1] == 1 &&
                        rhs.stride[1] == 1 && out.stride[1] == 1 && lhs.stride[0] % 8 == 0 && rhs.stride[0] % 8 == 0 &&
-                       out.stride[0] % 8 == 0 && aligned16(lhs.data) && aligned16(rhs.data) && aligned16(out.data) &&
+                       out.stride[0] % 8 == 0 && lhs.stride[0] <= kMaxPipeLd && rhs.stride[0] <= kMaxPipeLd &&
+                       aligned16(lhs.data) && aligned16(rhs.data) && aligned16(out.data) &&
                        (!bias.present || bias.stride[0] == 1);
   if (g_cost) {
     long long mfma = 0;
     if (mfma_ok && M > 0 && N > 0) {
-      const bool pipe = M % gemmp::kBM == 0 && N % gemmp::kBN == 0 && K % gemm::kBK == 0;
-      if (pipe)  // 8 waves x tm/16 MFMAs (32x32x16) per 32-deep slice of a tm x 256 tile
-        mfma = (M / pipe_tile_m(M, N)) * (N / gemmp::kBN) * (K / gemmp::kBK) * (pipe_tile_m(M, N) / 2);
-      else  // 4 waves x 64 MFMAs per 64-deep slice of a 256x256 tile
-        mfma = ((M + gemm::kBM - 1) / gemm::kBM) * ((N + gemm::kBN - 1) / gemm::kBN) * ((K + gemm::kBK - 1) / gemm::kBK) * 256;
+      // 8 waves x tm/16 MFMAs (32x32x16) per 32-deep slice of a tm x 256 tile; ragged edges
+      // are covered by whole tiles and slices
+      const long long tm = pipe_tile_m(M, N);
+      mfma = cdiv(M, tm) * cdiv(N, gemmp::kBN) * cdiv(K, gemmp::kBK) * (tm / 2);
     }
     const long long es = esize(out.dtype);
     return record_cost(M * N * K, mfma, (M * K + K * N) * es + (bias.present ? N * esize(bias.dtype) : 0), M * N * es);

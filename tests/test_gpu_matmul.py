@@ -130,6 +130,39 @@ def test_pipe_256_row_tiles_with_bias(device, oracle_mod, bias_kind):
 
 
 @pytest.mark.parametrize(
+    "shape,rows",
+    [
+        ((1000, 520, 1000), None),  # 128-row tiles, every edge ragged, 8-deep last K slice
+        ((4224, 40, 4104), None),  # 256-row tiles, half a last tile row, 8 columns over, K = 40
+        ((520, 4096, 776), None),  # 128-row tiles, long K
+        ((4000, 4000, 4000), [(0, 32), (3968, 4000)]),  # 256-row tiles, ragged M and N
+    ],
+    ids=["1000x520x1000", "4224x40x4104", "520x4096x776", "4000^3"],
+)
+def test_ragged_edges_store_only_inside(device, oracle_mod, shape, rows):
+    """Shapes that are not tile multiples take the pipelined kernel's ragged mode: edge copies
+    land zeros and the epilogue masks its stores. The output is a window of a NaN-filled
+    buffer with 3 extra rows and 8 extra columns, which must stay NaN."""
+
+    import torch
+
+    m, k, n = shape
+    rng = np.random.default_rng(m + 3 * k + 7 * n)
+    lt, lhs = round_to(rng.standard_normal((m, k), dtype=np.float32) * 0.1, torch.bfloat16)
+    rt, rhs = round_to(rng.standard_normal((k, n), dtype=np.float32) * 0.1, torch.bfloat16)
+    bias = rng.standard_normal(n).astype(np.float32)
+    big = torch.full((m + 3, n + 8), float("nan"), dtype=torch.bfloat16, device=device)
+    out = big[:m, :n]
+    print(f"[matmul] ragged M={m} K={k} N={n} ldc={n + 8}", flush=True)
+    native.matmul(out, lt.to(device), rt.to(device), torch.from_numpy(bias).to(device))
+    got = to_numpy(big)
+    assert np.isnan(got[m:]).all() and np.isnan(got[:, n:]).all(), "store outside the output window"
+    for r0, r1 in rows or [(0, m)]:
+        ref = oracle_mod.matmul_demo(lhs[r0:r1], rhs, bias, (64, 64, 64))
+        assert_h16_close(got[r0:r1, :n], ref, what=f"{shape} rows {r0}:{r1}")
+
+
+@pytest.mark.parametrize(
     "cfg",
     [
         ("C2", 4096, 4096, 4096, 20261202, [(0, 96), (2016, 2112), (4000, 4096)]),
