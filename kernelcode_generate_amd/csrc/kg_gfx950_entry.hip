@@ -17,6 +17,7 @@
 #include "kg_gfx950/conv2d.h"
 #include "kg_gfx950/flash_attn.h"
 #include "kg_gfx950/gemm.h"
+#include "kg_gfx950/gemm_f32.h"
 #include "kg_gfx950/conv2d_mfma.h"
 #include "kg_gfx950/flash_attn_mfma.h"
 
@@ -271,6 +272,33 @@ int launch_gemm_mfma(const Mem& out, const Mem& lhs, const Mem& rhs, const Mem& 
   return finish_launch(ragged ? "matmul(mfma-pipe-ragged)" : "matmul(mfma-pipe)");
 }
 
+// fp32 on matrix cores: 64-cycle MFMAs on 128 x 128 tiles. Below 32 tiles (e.g. C1's
+// 256^3 is 4) the SIMT kernel, which spreads small problems over every CU, finishes first.
+constexpr long long kF32MfmaMinTiles = 32;
+bool gemm_f32_mfma_pays(long long M, long long N, long long K) {
+  return cdiv(M, gemmf::kTile) * cdiv(N, gemmf::kTile) >= kF32MfmaMinTiles && K >= 4 * gemmf::kBK;
+}
+
+int launch_gemm_f32_mfma(const Mem& out, const Mem& lhs, const Mem& rhs, const Mem& bias, int M, int N, int K) {
+  const float* A = static_cast<const float*>(lhs.data);
+  const float* B = static_cast<const float*>(rhs.data);
+  float* C = static_cast<float*>(out.data);
+  const float* bp = bias.present ? static_cast<const float*>(bias.data) : nullptr;
+  const bool ragged = M % gemmf::kTile || N % gemmf::kTile || K % gemmf::kBK;
+  const int grid = (int)(cdiv(M, gemmf::kTile) * cdiv(N, gemmf::kTile));
+  const long long lda = lhs.stride[0], ldb = rhs.stride[0], ldc = out.stride[0];
+#define KG_GEMM_F32(BIAS, RAG)                                                                                   \
+  hipLaunchKernelGGL((gemm_f32_mfma_kernel<BIAS, RAG>), dim3(grid), dim3(gemmf::kThreads), 0, g_stream, A, B, C, bp, \
+                     M, N, K, lda, ldb, ldc)
+  if (ragged) {
+    if (bp) KG_GEMM_F32(1, true); else KG_GEMM_F32(0, true);
+  } else {
+    if (bp) KG_GEMM_F32(1, false); else KG_GEMM_F32(0, false);
+  }
+#undef KG_GEMM_F32
+  return finish_launch(ragged ? "matmul(f32-mfma-ragged)" : "matmul(f32-mfma)");
+}
+
 int matmul_impl(const KgArgSlot* args, unsigned long long n) {
   if (args == nullptr) return fail(kInvalid, "ordered_args is null");
   if (n != 4 && n != 7 && n != 8) return fail(kInvalid, "matmul expects 4, 7 or 8 slots, got %llu", n);
@@ -310,8 +338,15 @@ int matmul_impl(const KgArgSlot* args, unsigned long long n) {
                        out.stride[0] % 8 == 0 && lhs.stride[0] <= kMaxPipeLd && rhs.stride[0] <= kMaxPipeLd &&
                        aligned16(lhs.data) && aligned16(rhs.data) && aligned16(out.data) &&
                        (!bias.present || bias.stride[0] == 1);
+  const bool f32_mfma_ok = out.dtype == KG_DTYPE_F32 && k % 4 == 0 && nn % 4 == 0 && lhs.stride[1] == 1 &&
+                           rhs.stride[1] == 1 && out.stride[1] == 1 && lhs.stride[0] % 4 == 0 &&
+                           rhs.stride[0] % 4 == 0 && out.stride[0] % 4 == 0 && lhs.stride[0] <= kMaxPipeLd &&
+                           rhs.stride[0] <= kMaxPipeLd && aligned16(lhs.data) && aligned16(rhs.data) &&
+                           aligned16(out.data) && (!bias.present || bias.stride[0] == 1) && gemm_f32_mfma_pays(M, N, K);
   if (g_cost) {
     long long mfma = 0;
+    if (f32_mfma_ok)  // 4 waves x 2 x 2 blocks x 8 k-steps (32x32x2) per 16-deep slice of a 128 x 128 tile
+      mfma = cdiv(M, gemmf::kTile) * cdiv(N, gemmf::kTile) * cdiv(K, gemmf::kBK) * 128;
     if (mfma_ok && M > 0 && N > 0) {
       // 8 waves x tm/16 MFMAs (32x32x16) per 32-deep slice of a tm x 256 tile; ragged edges
       // are covered by whole tiles and slices
@@ -324,6 +359,7 @@ int matmul_impl(const KgArgSlot* args, unsigned long long n) {
   if (M == 0 || N == 0) return finish_launch("matmul(empty)");
 
   if (out.dtype == KG_DTYPE_F32) {
+    if (f32_mfma_ok) return launch_gemm_f32_mfma(out, lhs, rhs, bias, m, nn, k);
     return launch_gemm_simt<float, float>(out, lhs, rhs, bias, m, nn, k);
   }
   if (out.dtype == KG_DTYPE_BF16) {

@@ -5,10 +5,11 @@ counter run can be laid beside the model:
 
 Every case makes exactly one library kernel dispatch, in the order printed, and nothing
 else dispatches a kernel (inputs are generated on the host and copied), so dispatch i of the
-counter run is case i. Cases cover every kernel choice the model distinguishes:
-the pipelined MFMA GEMM with 256- and 128-row tiles and with ragged edges, the SIMT GEMM,
-the MFMA conv with four and with two live waves and a ragged last row block, and the MFMA attention kernels for D=128 and D=64,
-causal and not, with ragged query and key tails.
+counter run is case i. Cases cover every kernel choice the model distinguishes: the
+pipelined MFMA GEMM with 256- and 128-row tiles and with ragged edges, the fp32 MFMA GEMM
+aligned and ragged, the SIMT GEMM, the MFMA conv with four and with two live waves and a
+ragged last row block, and the MFMA attention kernels for D=128 and D=64, causal and not,
+with ragged query and key tails.
 """
 
 from __future__ import annotations
@@ -27,6 +28,8 @@ CASES = (
     ("gemm_f16_512x768x256", "matmul", "float16", ((512, 768), (512, 256), (256, 768)), ()),
     ("gemm_bf16_ragged_1000x1000x520", "matmul", "bfloat16", ((1000, 1000), (1000, 520), (520, 1000)), ()),
     ("gemm_f32_256", "matmul", "float32", ((256, 256), (256, 256), (256, 256)), ()),
+    ("gemm_f32_mfma_1024x256x1024", "matmul", "float32", ((1024, 1024), (1024, 256), (256, 1024)), ()),
+    ("gemm_f32_ragged_1000x1000x520", "matmul", "float32", ((1000, 1000), (1000, 520), (520, 1000)), ()),
     ("conv_f16_c3", "conv2d", "float16", ((32, 64, 56, 56), (32, 64, 56, 56), (64, 64, 3, 3)), (1, 1, 1, 1, 1, 1, 1, 1)),
     ("conv_bf16_3x64x20x40", "conv2d", "bfloat16", ((3, 64, 20, 40), (3, 64, 20, 40), (64, 64, 3, 3)),
      (1, 1, 1, 1, 1, 1, 1, 1)),

@@ -98,7 +98,15 @@ def test_matmul_counts(dtype, mnk):
     assert c["MAC"] == out.size * k  # one multiply-add per (row, column, k)
     assert c["HBM_READ"] == (lhs.size + rhs.size) * es + n * 4  # fp32 bias
     assert c["HBM_WRITE"] == out.size * es
-    if dtype == "float32" or k % 8 or n % 8:
+    if dtype == "float32":
+        tiles = -(-m // 128) * -(-n // 128)
+        if tiles >= 32 and k >= 64 and k % 4 == 0 and n % 4 == 0:  # fp32 MFMA: 32x32x2 = 2048 MACs each
+            assert c["MFMA"] * 2048 >= c["MAC"]
+            if m % 128 == 0 and n % 128 == 0 and k % 16 == 0:
+                assert c["MFMA"] * 2048 == c["MAC"]
+        else:
+            assert c["MFMA"] == 0  # SIMT path
+    elif k % 8 or n % 8:
         assert c["MFMA"] == 0  # SIMT path
     elif m % 256 == 0 and n % 256 == 0 and k % 64 == 0:
         assert c["MFMA"] * MFMA_MACS == c["MAC"]  # exact tiles: no wasted MFMA work

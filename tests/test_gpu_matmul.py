@@ -163,6 +163,48 @@ def test_ragged_edges_store_only_inside(device, oracle_mod, shape, rows):
 
 
 @pytest.mark.parametrize(
+    "shape,rows,with_bias",
+    [
+        ((1024, 256, 1024), None, False),  # 64 aligned 128 x 128 tiles
+        ((1000, 520, 1000), None, True),  # every edge ragged, 8-deep last K slice
+        ((777, 64, 2052), None, True),  # 4 columns past the last full tile
+        ((4096, 4096, 4096), [(0, 32), (4064, 4096)], False),
+    ],
+    ids=["1024x256x1024", "1000x520x1000", "777x64x2052", "4096^3"],
+)
+def test_f32_matrix_core_shapes(device, oracle_mod, shape, rows, with_bias):
+    """fp32 operands large enough for the fp32 MFMA kernel (v_mfma_f32_32x32x2_f32), which
+    sums K in a different order than the oracle's sequential loop. Tolerance: the demo's
+    rtol 1e-4 / atol 1e-5 plus the rounding that two fp32 summation orders of K products can
+    differ by, 4 sqrt(K) 2^-24 (|A| |B|)[m, n] (the probabilistic bound of Higham and Mary,
+    SIAM J. Sci. Comput. 41 (2019)): it reaches 1e-4 of the result only where K is large and
+    the result is small against its terms. The output is a window of a NaN-filled buffer
+    (3 extra rows, 4 extra columns) that must stay NaN outside it."""
+
+    import torch
+
+    m, k, n = shape
+    rng = np.random.default_rng(m + 5 * k + 11 * n)
+    lhs = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    rhs = rng.uniform(-1, 1, (k, n)).astype(np.float32)
+    bias = rng.uniform(-1, 1, n).astype(np.float32) if with_bias else None
+    big = torch.full((m + 3, n + 4), float("nan"), dtype=torch.float32, device=device)
+    out = big[:m, :n]
+    print(f"[matmul] f32 matrix cores M={m} K={k} N={n} bias={with_bias}", flush=True)
+    native.matmul(out, torch.from_numpy(lhs).to(device), torch.from_numpy(rhs).to(device),
+                  None if bias is None else torch.from_numpy(bias).to(device))
+    got = to_numpy(big)
+    assert np.isnan(got[m:]).all() and np.isnan(got[:, n:]).all(), "store outside the output window"
+    for r0, r1 in rows or [(0, m)]:
+        ref = oracle_mod.matmul_demo(np.ascontiguousarray(lhs[r0:r1]), rhs, bias, (64, 64, 64))
+        terms = np.abs(lhs[r0:r1]).astype(np.float64) @ np.abs(rhs).astype(np.float64)
+        tol = 1e-4 * np.abs(ref) + 1e-5 + 4 * np.sqrt(k) * 2.0 ** -24 * terms
+        err = np.abs(got[r0:r1, :n].astype(np.float64) - ref)
+        worst = np.unravel_index(np.argmax(err - tol), err.shape)
+        assert (err <= tol).all(), f"{shape} rows {r0}:{r1}: err {err[worst]:.3g} > tol {tol[worst]:.3g} at {worst}"
+
+
+@pytest.mark.parametrize(
     "cfg",
     [
         ("C2", 4096, 4096, 4096, 20261202, [(0, 96), (2016, 2112), (4000, 4096)]),
