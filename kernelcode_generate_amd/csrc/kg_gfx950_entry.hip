@@ -20,6 +20,7 @@
 #include "kg_gfx950/gemm_f32.h"
 #include "kg_gfx950/conv2d_mfma.h"
 #include "kg_gfx950/flash_attn_mfma.h"
+#include "kg_gfx950/flash_attn_f32.h"
 
 namespace {
 
@@ -550,6 +551,24 @@ int flash_attention_impl(const KgArgSlot* args, unsigned long long n) {
       }
       mfma = B_H * tiles * waves * (s.d / 4);
     }
+    if (out.dtype == KG_DTYPE_F32 && fa_f32_mfma_supported(s) && out.numel() > 0) {
+      // per workgroup and key tile: D MFMAs (32x32x2: D/2 for S^T, D/2 for PV) per wave that
+      // has a query and (causal) a visible key in the tile
+      const int nqb = (s.s_q + faf::kBM - 1) / faf::kBM;
+      long long waves_tiles = 0;
+      for (int qb = 0; qb < nqb; ++qb) {
+        const int q_wg = qb * faf::kBM;
+        const int n_tiles_all = (s.s_kv + faf::kBC - 1) / faf::kBC;
+        const int n_tiles =
+            s.causal ? std::min(n_tiles_all, (std::min(q_wg + faf::kBM, s.s_q) + faf::kBC - 1) / faf::kBC) : n_tiles_all;
+        for (int w = 0; w < faf::kWaves; ++w) {
+          const int q0 = q_wg + 32 * w;
+          if (q0 >= s.s_q) continue;
+          waves_tiles += s.causal ? std::min(n_tiles, q0 / faf::kBC + 1) : n_tiles;
+        }
+      }
+      mfma = B_H * waves_tiles * s.d;
+    }
     const long long es = esize(out.dtype);
     return record_cost(2 * B_H * pairs * D, mfma, (q.numel() + k.numel() + v.numel()) * es, out.numel() * es);
   }
@@ -565,6 +584,13 @@ int flash_attention_impl(const KgArgSlot* args, unsigned long long n) {
                                                     g_stream);
     if (e != hipSuccess) return fail(kHipFailure, "flash_attention(mfma): %s", hipGetErrorString(e));
     return finish_launch("flash_attention(mfma)");
+  }
+  if (out.dtype == KG_DTYPE_F32 && fa_f32_mfma_supported(s) && aligned16(q.data) && aligned16(k.data) &&
+      aligned16(v.data) && aligned16(out.data)) {
+    hipError_t e = launch_fa_fwd_f32_mfma(static_cast<const float*>(q.data), static_cast<const float*>(k.data),
+                                          static_cast<const float*>(v.data), static_cast<float*>(out.data), s, g_stream);
+    if (e != hipSuccess) return fail(kHipFailure, "flash_attention(f32-mfma): %s", hipGetErrorString(e));
+    return finish_launch("flash_attention(f32-mfma)");
   }
   switch (out.dtype) {
     case KG_DTYPE_F32: return launch_fa_simt<float>(out, q, k, v, s);

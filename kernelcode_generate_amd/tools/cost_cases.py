@@ -8,8 +8,8 @@ else dispatches a kernel (inputs are generated on the host and copied), so dispa
 counter run is case i. Cases cover every kernel choice the model distinguishes: the
 pipelined MFMA GEMM with 256- and 128-row tiles and with ragged edges, the fp32 MFMA GEMM
 aligned and ragged, the SIMT GEMM, the MFMA conv with four and with two live waves and a
-ragged last row block, and the MFMA attention kernels for D=128 and D=64, causal and not,
-with ragged query and key tails.
+ragged last row block, and the 16-bit and fp32 MFMA attention kernels for D=128 and D=64,
+causal and not, with ragged query and key tails.
 """
 
 from __future__ import annotations
@@ -39,6 +39,8 @@ CASES = (
     ("fa_bf16_causal_1x4x4096x128", "flash_attention", "bfloat16", ((1, 4, 4096, 128),) * 4, (128, 64, 0.088388, 1)),
     ("fa_f16_causal_1x2x1000x64", "flash_attention", "float16", ((1, 2, 1000, 64),) * 4, (128, 64, 0.125, 1)),
     ("fa_bf16_2x3x130x128", "flash_attention", "bfloat16", ((2, 3, 130, 128),) * 4, (128, 64, 0.088388, 0)),
+    ("fa_f32_causal_1x2x700x128", "flash_attention", "float32", ((1, 2, 700, 128),) * 4, (64, 64, 0.088388, 1)),
+    ("fa_f32_2x1x130x64", "flash_attention", "float32", ((2, 1, 130, 64),) * 4, (64, 64, 0.125, 0)),
 )
 
 

@@ -17,6 +17,7 @@ import numpy as np
 import pytest
 
 from kernelcode_generate_amd import native
+from tests.golden.make_golden import attention_closed_form
 from tests.gpu_util import assert_f32_close, assert_h16_close, round_to, to_numpy
 
 pytestmark = pytest.mark.gpu
@@ -76,6 +77,54 @@ def test_extensions_f32(device, oracle_mod, scale, causal):
     ref = oracle_mod.flash_attention_demo(q, k, v, 48, 80, scale=scale, causal=causal)
     out = run(device, torch.float32, q, k, v, 48, 80, scale, causal)
     assert_f32_close(to_numpy(out), ref, rtol=1e-4, atol=1e-4, what=f"scale={scale} causal={causal}")
+
+
+@pytest.mark.parametrize(
+    "shape,s_kv,causal",
+    [
+        ((1, 2, 256, 128), 256, False),
+        ((1, 2, 700, 128), 700, True),  # ragged causal over several 128-query blocks
+        ((2, 1, 130, 64), 300, False),  # one partial query block, ragged key tail, S_q != S_kv
+        ((1, 1, 1000, 64), 1000, True),
+        ((1, 2, 1, 128), 1, False),  # one query, one key
+        ((1, 1, 33, 64), 1000, False),
+    ],
+)
+def test_f32_matrix_cores(device, oracle_mod, shape, s_kv, causal):
+    """fp32 Q/K/V with D in {64, 128} take the fp32 MFMA kernel; the oracle's demo loop nest
+    is the reference where S_q == S_kv, the float64 closed form of the demo's check
+    (kernel/flash_attention/inputs_static_tile_static.py:57-87) otherwise."""
+
+    import torch
+
+    b, h, sq, d = shape
+    scale = 1.0 / np.sqrt(d)
+    rng = np.random.default_rng(sq * 3 + s_kv + d)
+    q = rng.standard_normal(shape, dtype=np.float32)
+    k, v = (rng.standard_normal((b, h, s_kv, d), dtype=np.float32) for _ in range(2))
+    if sq == s_kv:
+        ref = oracle_mod.flash_attention_demo(q, k, v, 64, 64, scale=scale, causal=causal)
+    else:
+        ref = attention_closed_form(q, k, v, scale).astype(np.float32)
+    out = run(device, torch.float32, q, k, v, 64, 64, scale, causal)
+    assert_f32_close(to_numpy(out), ref, rtol=1e-4, atol=1e-4, what=f"{shape} s_kv={s_kv} causal={causal}")
+
+
+def test_f32_c4_shape_sampled_heads(device):
+    """BASELINE C4's shape (B=4, H=32, S=2048, D=128) in fp32: two heads against the float64
+    closed form of the demo's check."""
+
+    import torch
+
+    shape = (4, 32, 2048, 128)
+    gen = torch.Generator(device=device).manual_seed(4)
+    q, k, v = (torch.randn(shape, generator=gen, device=device) for _ in range(3))
+    out = torch.full(shape, float("nan"), device=device)
+    print("[fa] f32 C4 shape", flush=True)
+    native.flash_attention(out, q, k, v, 64, 64, 1.0 / np.sqrt(128), False)
+    for bi, hi in ((0, 0), (3, 31)):
+        ref = attention_closed_form(*(to_numpy(t[bi, hi]) for t in (q, k, v)), 1.0 / np.sqrt(128))
+        assert_f32_close(to_numpy(out[bi, hi]), ref.astype(np.float32), rtol=1e-4, atol=1e-4, what=f"head {bi},{hi}")
 
 
 @pytest.mark.parametrize("dtype_name", ["bfloat16", "float16"])
