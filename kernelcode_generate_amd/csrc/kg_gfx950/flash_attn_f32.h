@@ -60,7 +60,9 @@ __global__ __launch_bounds__(faf::kThreads, D == 128 ? 2 : 4) void fa_fwd_f32_mf
   const int nqb = (s_q + kBM - 1) / kBM;
   const int logical = fa::xcd_block(blockIdx.x, gridDim.x);
   const int bh = logical / nqb;
-  const int q_wg = (logical - bh * nqb) * kBM;
+  int qb = logical - bh * nqb;
+  if (kCausal) qb = nqb - 1 - qb;  // longest query blocks of a (b,h) first
+  const int q_wg = qb * kBM;
   const int q0 = q_wg + 32 * wave;
   const int frag = lane & 31;
   const int h = lane >> 5;
