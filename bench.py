@@ -19,9 +19,10 @@ The JSON line also carries
             and run on 2 host threads (npu_demo block_num = 2) over a bounded sample of
             the same workload (the first 384 output rows), plus the same sample built with
             -O2 (optimized_value) and the host CPU model;
-  secondary: the other BASELINE configs (C1, C2', C3, C4, C5 D=128/64), each after 0.15 s
-            of untimed launches, over >= 200 (C1, C2'), 1000 (C3), 100 (C4) or 25 (C5)
-            back-to-back launches.
+  secondary: the other BASELINE configs (C1, C2', C3, C4, C5 D=128/64) and two fp32 extension
+            lines (C2's and C4's shapes in the reference demos' fp32), each after 0.15 s
+            of untimed launches, over >= 200 (C1, C2'), 1000 (C3), 100 (C4), 25 (C5), 50
+            (fp32 matmul) or 20 (fp32 attention) back-to-back launches.
 """
 
 from __future__ import annotations
@@ -157,7 +158,7 @@ def cpu_model() -> str:
     return "unknown"
 
 
-SECONDARY_KEYS = ("c1", "c2s", "c3", "c4", "c5d128", "c5d64")
+SECONDARY_KEYS = ("c1", "c2s", "c3", "c4", "c5d128", "c5d64", "f32gemm", "f32fa")
 
 
 SECONDARY_WARMUP_S = 0.15  # untimed back-to-back launches per secondary workload, seconds
@@ -195,6 +196,10 @@ def secondary(dev, steps: int, warmup: int, only=None):
     for d, key in ((128, "c5d128"), (64, "c5d64")):
         if key in keys:
             c5(dev, add, steps, d)
+    if "f32gemm" in keys:
+        f32_gemm(dev, add, steps)
+    if "f32fa" in keys:
+        f32_fa(dev, add, steps)
     return out
 
 
@@ -250,6 +255,30 @@ def c5(dev, add, steps, d):
     add(f"C5 bf16 flash-attn fwd B=1 H=32 S=16384 D={d} causal", 4 * 32 * 16384 * 16384 * d // 2,
         PreparedCall("kg_gfx950_flash_attention_entry", (o, q, k, v, 128, 64, 1.0 / math.sqrt(d), 1)),
         PEAK_BF16_TFLOPS, max(20, steps // 4))
+
+
+def f32_gemm(dev, add, steps):
+    """Extension: C2's shape with fp32 operands (the reference demos' dtype) on matrix cores."""
+    import torch
+
+    g = torch.Generator(device=dev).manual_seed(20261208)
+    a, b = (torch.rand(4096, 4096, generator=g, device=dev) * 2 - 1 for _ in range(2))
+    c = torch.empty(4096, 4096, device=dev)
+    add("fp32 matmul M=N=K=4096 (extension: C2 shape in the demos' fp32)", 2 * 4096**3,
+        PreparedCall("kg_gfx950_matmul_entry", (c, a, b, None)), PEAK_FP32_TFLOPS, max(20, steps // 4))
+
+
+def f32_fa(dev, add, steps):
+    """Extension: C4's shape with fp32 Q/K/V on matrix cores."""
+    import torch
+
+    g = torch.Generator(device=dev).manual_seed(20261209)
+    q, k, v = (torch.randn(4, 32, 2048, 128, generator=g, device=dev) for _ in range(3))
+    o = torch.empty_like(q)
+    add("fp32 flash-attn fwd B=4 H=32 S=2048 D=128 non-causal (extension: C4 shape in fp32)",
+        4 * 4 * 32 * 2048 * 2048 * 128,
+        PreparedCall("kg_gfx950_flash_attention_entry", (o, q, k, v, 64, 64, 1.0 / math.sqrt(128.0), 0)),
+        PEAK_FP32_TFLOPS, max(10, steps // 10))
 
 
 def main() -> int:
