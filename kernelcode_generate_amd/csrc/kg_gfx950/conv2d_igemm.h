@@ -1,0 +1,326 @@
+// Implicit-GEMM conv2d on gfx950 matrix cores for any NCHW shape, kernel size, stride,
+// dilation and padding: bf16/f16 (v_mfma_f32_32x32x16) or fp32 (v_mfma_f32_32x32x2_f32)
+// operands, fp32 accumulation.
+//
+// GEMM view: Y[n][f][p] = sum_k W[f][k] Xcol[k][(n, p)], with k = (c, kh, kw) in the
+// weight's own order (K = C KH KW, so W[F][K] is read as stored) and the columns running
+// over all N Ho Wo output pixels. A workgroup (4 waves, 2 x 2) computes a BM x 128 tile
+// (BM = 64 or 128 filters) and walks K in slices of 64 bytes per row (32 16-bit or 16 fp32
+// values). Each thread owns one output column of the tile for the whole K loop (its
+// image, input row/column origin and bounds are worked out once) and gathers that column's
+// im2col values of the next slice into registers while the MFMAs of the current slice run;
+// taps that fall in the padding read nothing and store zeros. Weights are staged the same
+// way, as 16-byte row chunks when K allows. Both operands sit in LDS as 64-byte k-rows
+// ([filter][k] and [column][k]) with 16-byte chunk c of row r at c ^ ((r >> 2) & 3), so every
+// MFMA fragment is one conflict-free ds_read_b128; the MFMA runs as Y^T = Xcol^T W^T
+// (columns as operand A) and each lane ends with 4 consecutive output pixels of one filter.
+// Divisions by runtime extents (KH KW, KW, Ho Wo, Wo) use precomputed multipliers.
+#pragma once
+
+#include "common.h"
+#include "conv2d.h"
+
+namespace kg_gfx950 {
+
+// n / d for 0 <= n < 2^32 and 1 <= d < 2^31: q = (umulhi(n, mul) + n) >> shift with
+// shift = ceil(log2 d) and mul = floor(2^32 (2^shift - d) / d) + 1 (division by invariant
+// integers using multiplication, Granlund and Montgomery, PLDI 1994).
+struct FastDiv {
+  uint32_t d, mul, shift;
+};
+inline FastDiv make_fast_div(uint32_t d) {
+  uint32_t l = 0;
+  while ((1ull << l) < d) ++l;
+  const unsigned long long mul = ((1ull << 32) * ((1ull << l) - d)) / d + 1;
+  return FastDiv{d, (uint32_t)mul, l};
+}
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, FastDiv f) {
+  const uint32_t hi = __umulhi(n, f.mul);
+  return (uint32_t)(((unsigned long long)hi + n) >> f.shift);
+}
+
+struct F32Tag {};
+
+namespace convg {
+constexpr int kBN = 128;  // output pixels per tile
+constexpr int kThreads = 256;
+__device__ __forceinline__ int slot(int row, int c) { return row * 4 + (c ^ ((row >> 2) & 3)); }
+
+struct Params {
+  int n, c, h, w, f, kh, kw, ho, wo, sh, sw, dh, dw, pt, pl;
+  int K, P;   // C KH KW, Ho Wo
+  int NP;     // N Ho Wo
+  FastDiv div_khw, div_kw, div_p, div_wo;
+};
+
+template <typename Tag>
+struct IgElem {  // 16-bit operands: 8 values per 16-byte chunk, 32 per slice row
+  using T = uint16_t;
+  static constexpr int kPerChunk = 8;
+  static __device__ __forceinline__ uint32_t bits(T v) { return v; }
+  static __device__ __forceinline__ float to_float(T v) { return Half16<Tag>::to_float(v); }
+};
+template <>
+struct IgElem<F32Tag> {  // fp32 operands: 4 values per chunk, 16 per slice row
+  using T = float;
+  static constexpr int kPerChunk = 4;
+  static __device__ __forceinline__ uint32_t bits(T v) { return __builtin_bit_cast(uint32_t, v); }
+  static __device__ __forceinline__ float to_float(T v) { return v; }
+};
+}  // namespace convg
+
+// kMI: 32-row filter blocks per wave (BM = 64 kMI); kBias: 0 none, 1 fp32, 2 same dtype;
+// kVecW: K % (values per chunk) == 0 and 16-byte aligned weights (chunk loads).
+template <typename Tag, int kMI, int kBias, bool kVecW>
+__global__ __launch_bounds__(convg::kThreads) void conv2d_igemm_kernel(
+    const typename convg::IgElem<Tag>::T* __restrict__ x, const typename convg::IgElem<Tag>::T* __restrict__ wt,
+    typename convg::IgElem<Tag>::T* __restrict__ y, const void* __restrict__ bias, convg::Params s) {
+  using namespace convg;
+  using E = IgElem<Tag>;
+  using T = typename E::T;
+  constexpr int V = E::kPerChunk;
+  constexpr int BK = 4 * V;  // k per slice
+  constexpr int BM = 64 * kMI;
+  constexpr int kStage = (BM + kBN) * 64;  // bytes
+  __shared__ __attribute__((aligned(1024))) u32x4 lds[2 * kStage / 16];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int tiles_m = (s.f + BM - 1) / BM;
+  const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int m0 = (logical % tiles_m) * BM;  // the filter tiles of one column tile are adjacent
+  const int n0 = (logical / tiles_m) * kBN;
+
+  // ---- this thread's column: output pixel j = n0 + (tid & 127), chunks cb and cb + 2 ----
+  const int jj = tid & (kBN - 1);
+  const int cb = tid >> 7;
+  const int j = n0 + jj;
+  const bool col_ok = j < s.NP;
+  const uint32_t jn = fdiv(col_ok ? j : 0, s.div_p);
+  const uint32_t jp = (col_ok ? j : 0) - jn * s.P;
+  const uint32_t jho = fdiv(jp, s.div_wo);
+  const int hi0 = (int)jho * s.sh - s.pt;
+  const int wi0 = (int)(jp - jho * s.wo) * s.sw - s.pl;
+  const int hw = s.h * s.w;
+  const T* xn = x + (long long)jn * s.c * hw;
+
+  auto gather_chunk = [&](int k0) -> u32x4 {  // Xcol[k0 .. k0+V-1][j]
+    uint32_t c = fdiv(k0, s.div_khw);
+    const uint32_t r = k0 - c * (s.kh * s.kw);
+    uint32_t kh = fdiv(r, s.div_kw);
+    uint32_t kw = r - kh * s.kw;
+    T v[V];
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      const int hi = hi0 + (int)kh * s.dh, wi = wi0 + (int)kw * s.dw;
+      const bool ok = col_ok && k0 + e < s.K && (unsigned)hi < (unsigned)s.h && (unsigned)wi < (unsigned)s.w;
+      v[e] = ok ? xn[(int)c * hw + hi * s.w + wi] : T(0);
+      if (++kw == (uint32_t)s.kw) {
+        kw = 0;
+        if (++kh == (uint32_t)s.kh) {
+          kh = 0;
+          ++c;
+        }
+      }
+    }
+    u32x4 out;
+    if constexpr (V == 8) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) out[q] = E::bits(v[2 * q]) | (E::bits(v[2 * q + 1]) << 16);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) out[q] = E::bits(v[q]);
+    }
+    return out;
+  };
+  auto weight_chunk = [&](int f, int k0) -> u32x4 {  // W[f][k0 .. k0+V-1]
+    const bool row_ok = f < s.f;
+    if constexpr (kVecW) {
+      if (row_ok && k0 < s.K) return ld16(wt + (long long)f * s.K + k0);
+      return u32x4{0, 0, 0, 0};
+    } else {
+      T v[V];
+#pragma unroll
+      for (int e = 0; e < V; ++e) v[e] = (row_ok && k0 + e < s.K) ? wt[(long long)f * s.K + k0 + e] : T(0);
+      u32x4 out;
+      if constexpr (V == 8) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) out[q] = E::bits(v[2 * q]) | (E::bits(v[2 * q + 1]) << 16);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) out[q] = E::bits(v[q]);
+      }
+      return out;
+    }
+  };
+
+  u32x4 rb[2], ra[kMI];
+  auto load_regs = [&](int kt) {
+    const int kb = kt * BK;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) rb[i] = gather_chunk(kb + (cb + 2 * i) * V);
+#pragma unroll
+    for (int i = 0; i < kMI; ++i) {
+      const int ci = tid + kThreads * i;  // weight chunk: row ci >> 2, chunk ci & 3
+      ra[i] = weight_chunk(m0 + (ci >> 2), kb + (ci & 3) * V);
+    }
+  };
+  auto store_lds = [&](int buf) {
+    u32x4* st = lds + buf * (kStage / 16);
+#pragma unroll
+    for (int i = 0; i < kMI; ++i) {
+      const int ci = tid + kThreads * i;
+      st[slot(ci >> 2, ci & 3)] = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) st[BM * 4 + slot(jj, cb + 2 * i)] = rb[i];
+  };
+
+  f32x16 acc[kMI][2];
+#pragma unroll
+  for (int i = 0; i < kMI; ++i)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][b][e] = 0.f;
+
+  const int frag = lane & 31, h = lane >> 5;
+  const int nk = (s.K + BK - 1) / BK;
+  load_regs(0);
+  store_lds(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt + 1 < nk) load_regs(kt + 1);  // gathers in flight during the MFMAs below
+    const u32x4* st = lds + (kt & 1) * (kStage / 16);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      u32x4 af[kMI], bf[2];
+#pragma unroll
+      for (int i = 0; i < kMI; ++i) af[i] = st[slot(wm * (BM / 2) + 32 * i + frag, 2 * ks + h)];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) bf[b] = st[BM * 4 + slot(wn * 64 + 32 * b + frag, 2 * ks + h)];
+#pragma unroll
+      for (int i = 0; i < kMI; ++i)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          if constexpr (V == 8) {
+            acc[i][b] = Half16<Tag>::mfma32(bf[b], af[i], acc[i][b]);
+          } else {
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+              const uint32_t bu = bf[b][kk], au = af[i][kk];
+              acc[i][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(__builtin_bit_cast(float, bu),
+                                                               __builtin_bit_cast(float, au), acc[i][b], 0, 0, 0);
+            }
+          }
+        }
+    }
+    if (kt + 1 < nk) store_lds((kt + 1) & 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: lane holds Y[f][j0 .. j0+3], f = tile row wm*BM/2 + 32 i + lane % 32,
+  // j0 = tile column wn*64 + 32 b + 8 q + 4 (lane / 32) ----
+  const bool vec_out = (s.P & 3) == 0;  // then j0 .. j0+3 lie in one image, p % 4 == 0
+#pragma unroll
+  for (int i = 0; i < kMI; ++i) {
+    const int f = m0 + wm * (BM / 2) + 32 * i + frag;
+    if (f >= s.f) continue;
+    float bv = 0.f;
+    if constexpr (kBias == 1) bv = static_cast<const float*>(bias)[f];
+    if constexpr (kBias == 2) bv = E::to_float(static_cast<const T*>(bias)[f]);
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int j0 = n0 + wn * 64 + 32 * b + 8 * q + 4 * h;
+        if (j0 >= s.NP) continue;
+        float r[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = acc[i][b][4 * q + e] + bv;
+        if (vec_out) {
+          const uint32_t n = fdiv(j0, s.div_p);
+          const uint32_t p = j0 - n * s.P;
+          T* yp = y + ((long long)n * s.f + f) * s.P + p;
+          if constexpr (V == 8) {
+            u32x2 packed;
+            packed[0] = Half16<Tag>::pack2(r[0], r[1]);
+            packed[1] = Half16<Tag>::pack2(r[2], r[3]);
+            st8(yp, packed);
+          } else {
+            *reinterpret_cast<f32x4*>(yp) = f32x4{r[0], r[1], r[2], r[3]};
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int jv = j0 + e;
+            if (jv >= s.NP) break;
+            const uint32_t n = fdiv(jv, s.div_p);
+            const uint32_t p = jv - n * s.P;
+            T* yp = y + ((long long)n * s.f + f) * s.P + p;
+            if constexpr (V == 8) {
+              const uint32_t pk = Half16<Tag>::pack2(r[e], 0.f);
+              *yp = (uint16_t)(pk & 0xffffu);
+            } else {
+              *yp = r[e];
+            }
+          }
+        }
+      }
+  }
+}
+
+inline bool conv_igemm_supported(const ConvShape& s) {
+  const long long K = (long long)s.c * s.kh * s.kw;
+  const long long P = (long long)s.ho * s.wo;
+  return K >= 1 && K < (1ll << 30) && (long long)s.n * P < (1ll << 31) && (long long)s.c * s.h * s.w < (1ll << 31) &&
+         (long long)s.n * s.c * s.h * s.w < (1ll << 40);
+}
+
+inline convg::Params conv_igemm_params(const ConvShape& s) {
+  convg::Params p;
+  p.n = s.n; p.c = s.c; p.h = s.h; p.w = s.w; p.f = s.f; p.kh = s.kh; p.kw = s.kw; p.ho = s.ho; p.wo = s.wo;
+  p.sh = s.sh; p.sw = s.sw; p.dh = s.dh; p.dw = s.dw; p.pt = s.pt; p.pl = s.pl;
+  p.K = s.c * s.kh * s.kw;
+  p.P = s.ho * s.wo;
+  p.NP = s.n * p.P;
+  p.div_khw = make_fast_div((uint32_t)(s.kh * s.kw));
+  p.div_kw = make_fast_div((uint32_t)s.kw);
+  p.div_p = make_fast_div((uint32_t)p.P);
+  p.div_wo = make_fast_div((uint32_t)s.wo);
+  return p;
+}
+
+// BM = 128 filters per tile when F > 64, else 64.
+inline int conv_igemm_mi(const ConvShape& s) { return s.f > 64 ? 2 : 1; }
+
+template <typename Tag>
+hipError_t launch_conv2d_igemm(const void* x, const void* w, void* y, const void* bias, int bias_kind, bool vec_w,
+                               const ConvShape& s, hipStream_t stream) {
+  using T = typename convg::IgElem<Tag>::T;
+  const convg::Params p = conv_igemm_params(s);
+  const int mi = conv_igemm_mi(s);
+  const int grid = ((s.f + 64 * mi - 1) / (64 * mi)) * ((p.NP + convg::kBN - 1) / convg::kBN);
+  const T* xp = static_cast<const T*>(x);
+  const T* wp = static_cast<const T*>(w);
+  T* yp = static_cast<T*>(y);
+#define KG_CONV_IG(MI, B, VW)                                                                                  \
+  hipLaunchKernelGGL((conv2d_igemm_kernel<Tag, MI, B, VW>), dim3(grid), dim3(convg::kThreads), 0, stream, xp, wp, yp, \
+                     bias, p)
+#define KG_CONV_IG_B(MI, VW)                  \
+  if (bias_kind == 0) KG_CONV_IG(MI, 0, VW);   \
+  else if (bias_kind == 1) KG_CONV_IG(MI, 1, VW); \
+  else KG_CONV_IG(MI, 2, VW)
+  if (mi == 2) {
+    if (vec_w) { KG_CONV_IG_B(2, true); } else { KG_CONV_IG_B(2, false); }
+  } else {
+    if (vec_w) { KG_CONV_IG_B(1, true); } else { KG_CONV_IG_B(1, false); }
+  }
+#undef KG_CONV_IG_B
+#undef KG_CONV_IG
+  return hipGetLastError();
+}
+
+}  // namespace kg_gfx950

@@ -19,6 +19,7 @@
 #include "kg_gfx950/gemm.h"
 #include "kg_gfx950/gemm_f32.h"
 #include "kg_gfx950/conv2d_mfma.h"
+#include "kg_gfx950/conv2d_igemm.h"
 #include "kg_gfx950/flash_attn_mfma.h"
 #include "kg_gfx950/flash_attn_f32.h"
 
@@ -442,8 +443,16 @@ int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
   if (bias.present && bias.shape[0] != w.shape[0]) return fail(kInvalid, "conv2d: bias extent != F");
   if (g_cost) {
     long long mfma = 0;
-    if (out.dtype != KG_DTYPE_F32 && conv_mfma_supported(s))  // live waves x 252 MFMAs per 7-row block
+    if (out.dtype != KG_DTYPE_F32 && conv_mfma_supported(s)) {  // live waves x 252 MFMAs per 7-row block
       mfma = (long long)s.n * ((s.h + convk::kRows - 1) / convk::kRows) * (s.w > 32 ? 4 : 2) * 252;
+    } else if (conv_igemm_supported(s)) {
+      // implicit GEMM: per tile and 64-byte k slice, 4 waves x MI x 2 blocks x (2 MFMAs of
+      // 32x32x16, or 8 of 32x32x2 for fp32)
+      const long long mi = conv_igemm_mi(s), K = (long long)s.c * s.kh * s.kw;
+      const long long per = out.dtype == KG_DTYPE_F32 ? 8 : 2, bk = out.dtype == KG_DTYPE_F32 ? 16 : 32;
+      const long long tiles = cdiv(s.f, 64 * mi) * cdiv((long long)s.n * s.ho * s.wo, convg::kBN);
+      mfma = tiles * cdiv(K, bk) * 4 * mi * 2 * per;
+    }
     const long long es = esize(out.dtype);
     return record_cost(out.numel() * w.shape[1] * w.shape[2] * w.shape[3], mfma,
                        (x.numel() + w.numel()) * es + (bias.present ? bias.shape[0] * esize(bias.dtype) : 0),
@@ -466,6 +475,17 @@ int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
                                                bias_kind, s, g_stream);
     if (e != hipSuccess) return fail(kHipFailure, "conv2d(mfma): %s", hipGetErrorString(e));
     return finish_launch("conv2d(mfma)");
+  }
+  if (conv_igemm_supported(s) && aligned16(out.data)) {
+    const int bias_kind = !bias.present ? 0 : (bias.dtype == KG_DTYPE_F32 ? 1 : 2);
+    const long long K = (long long)s.c * s.kh * s.kw;
+    const bool vec_w = aligned16(w.data) && K % (out.dtype == KG_DTYPE_F32 ? 4 : 8) == 0;
+    const void* bp = bias.present ? bias.data : nullptr;
+    hipError_t e = out.dtype == KG_DTYPE_F32   ? launch_conv2d_igemm<F32Tag>(x.data, w.data, out.data, bp, bias_kind, vec_w, s, g_stream)
+                   : out.dtype == KG_DTYPE_BF16 ? launch_conv2d_igemm<Bf16Tag>(x.data, w.data, out.data, bp, bias_kind, vec_w, s, g_stream)
+                                                : launch_conv2d_igemm<F16Tag>(x.data, w.data, out.data, bp, bias_kind, vec_w, s, g_stream);
+    if (e != hipSuccess) return fail(kHipFailure, "conv2d(igemm): %s", hipGetErrorString(e));
+    return finish_launch("conv2d(igemm)");
   }
   const bool f32_bias = bias.present && bias.dtype == KG_DTYPE_F32;
   switch (out.dtype) {

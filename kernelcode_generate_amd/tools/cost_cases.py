@@ -8,7 +8,7 @@ else dispatches a kernel (inputs are generated on the host and copied), so dispa
 counter run is case i. Cases cover every kernel choice the model distinguishes: the
 pipelined MFMA GEMM with 256- and 128-row tiles and with ragged edges, the fp32 MFMA GEMM
 aligned and ragged, the SIMT GEMM, the MFMA conv with four and with two live waves and a
-ragged last row block, and the 16-bit and fp32 MFMA attention kernels for D=128 and D=64,
+ragged last row block, the implicit-GEMM conv (16-bit and fp32), and the 16-bit and fp32 MFMA attention kernels for D=128 and D=64,
 causal and not, with ragged query and key tails.
 """
 
@@ -35,6 +35,10 @@ CASES = (
      (1, 1, 1, 1, 1, 1, 1, 1)),
     ("conv_f16_2x64x12x24", "conv2d", "float16", ((2, 64, 12, 24), (2, 64, 12, 24), (64, 64, 3, 3)),
      (1, 1, 1, 1, 1, 1, 1, 1)),
+    ("conv_f16_igemm_2x64x56x56_s2", "conv2d", "float16", ((2, 64, 28, 28), (2, 64, 56, 56), (64, 64, 3, 3)),
+     (2, 2, 1, 1, 1, 1, 1, 1)),
+    ("conv_f32_igemm_1x40x19x23_f96", "conv2d", "float32", ((1, 96, 18, 12), (1, 40, 19, 23), (96, 40, 3, 3)),
+     (1, 2, 2, 1, 2, 1, 0, 3)),
     ("fa_bf16_c4", "flash_attention", "bfloat16", ((4, 32, 2048, 128),) * 4, (128, 64, 0.088388, 0)),
     ("fa_bf16_causal_1x4x4096x128", "flash_attention", "bfloat16", ((1, 4, 4096, 128),) * 4, (128, 64, 0.088388, 1)),
     ("fa_f16_causal_1x2x1000x64", "flash_attention", "float16", ((1, 2, 1000, 64),) * 4, (128, 64, 0.125, 1)),

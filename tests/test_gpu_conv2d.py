@@ -110,6 +110,60 @@ def test_general_params_f32(device, oracle_mod, xs, ws, stride, dil, pad):
         assert_f32_close(to_numpy(run(device, torch.float32, x, w, b, stride, dil, pad)), ref, what=str(xs))
 
 
+@pytest.mark.parametrize("dtype_name", ["float32", "float16", "bfloat16"])
+@pytest.mark.parametrize(
+    "xs,ws,stride,dil,pad,bias",
+    [
+        ((2, 64, 56, 56), (64, 64, 3, 3), (2, 2), (1, 1), (1, 1, 1, 1), None),  # stride 2
+        ((2, 128, 28, 28), (128, 128, 3, 3), (1, 1), (1, 1), (1, 1, 1, 1), "f32"),  # 128-filter tiles
+        ((4, 256, 14, 14), (256, 256, 1, 1), (1, 1), (1, 1), (0, 0, 0, 0), None),  # 1x1
+        ((2, 3, 64, 64), (64, 3, 7, 7), (2, 2), (1, 1), (3, 3, 3, 3), "same"),  # K = 147: scalar weights
+        ((1, 40, 19, 23), (96, 40, 3, 3), (1, 2), (2, 1), (2, 1, 0, 3), "f32"),  # F = 96, Ho*Wo odd
+        ((3, 24, 10, 10), (20, 24, 5, 5), (1, 1), (2, 2), (4, 4, 4, 4), None),  # dilated, F < 32
+    ],
+    ids=["s2", "c128", "1x1", "7x7s2", "f96_ragged", "dilated"],
+)
+def test_implicit_gemm_shapes(device, oracle_mod, dtype_name, xs, ws, stride, dil, pad, bias):
+    """Every conv the 3x3 kernel does not take runs as an implicit GEMM on matrix cores (16-bit
+    or fp32 MFMA). Reference: the oracle's demo loop nest on the identically rounded inputs.
+    fp32 tolerance: the demo's rtol 1e-4 / atol 1e-5 plus the rounding that two fp32 summation
+    orders of K = C KH KW products can differ by, 4 sqrt(K) 2^-24 (|W| * |X|) (the
+    probabilistic bound of Higham and Mary, SIAM J. Sci. Comput. 41 (2019))."""
+
+    import torch
+
+    dt = getattr(torch, dtype_name)
+    rng = np.random.default_rng(sum(xs) + sum(ws))
+    k = ws[1] * ws[2] * ws[3]
+    bound = np.sqrt(6.0 / k)
+    if dt == torch.float32:
+        x = rng.standard_normal(xs).astype(np.float32)
+        w = rng.uniform(-bound, bound, size=ws).astype(np.float32)
+        xt, wt = torch.from_numpy(x), torch.from_numpy(w)
+    else:
+        xt, x = round_to(rng.standard_normal(xs), dt)
+        wt, w = round_to(rng.uniform(-bound, bound, size=ws), dt)
+    b = bt = None
+    if bias == "f32":
+        b = bt = rng.normal(size=(ws[0],)).astype(np.float32)
+    elif bias == "same":
+        if dt == torch.float32:
+            b = bt = rng.normal(size=(ws[0],)).astype(np.float32)
+        else:
+            bt, b = round_to(rng.normal(size=(ws[0],)).astype(np.float32), dt)
+    tiles = (16, 16, 1, 8, 16)
+    ref = oracle_mod.conv2d_demo(x, w, b, stride, dil, pad, tiles)
+    out = to_numpy(run(device, dt, xt, wt, bt, stride, dil, pad))
+    what = f"{dtype_name} {xs} {ws} s={stride} d={dil} p={pad} bias={bias}"
+    if dt == torch.float32:
+        terms = oracle_mod.conv2d_demo(np.abs(x), np.abs(w), None, stride, dil, pad, tiles).astype(np.float64)
+        tol = 1e-4 * np.abs(ref) + 1e-5 + 4 * np.sqrt(k) * 2.0 ** -24 * terms
+        err = np.abs(out.astype(np.float64) - ref)
+        assert (err <= tol).all(), f"{what}: max err/tol {np.max(err / tol):.3g}"
+    else:
+        assert_h16_close(out, ref, what=what)
+
+
 @pytest.mark.parametrize("dtype_name", ["float16", "bfloat16"])
 @pytest.mark.parametrize(
     "xs,ws,bias",
@@ -118,7 +172,7 @@ def test_general_params_f32(device, oracle_mod, xs, ws, stride, dil, pad):
         ((1, 64, 12, 24), (64, 64, 3, 3), "f32"),  # MFMA: 7-row blocks with a 5-row tail, W <= 32
         ((3, 64, 20, 40), (64, 64, 3, 3), "h16"),  # MFMA: 6-row tail, second pixel block partly live
         ((1, 64, 1, 8), (64, 64, 3, 3), "f32"),  # MFMA: one row, one 8-column block
-        ((1, 64, 12, 20), (64, 64, 3, 3), "f32"),  # W % 8 != 0: direct kernel
+        ((1, 64, 12, 20), (64, 64, 3, 3), "f32"),  # W % 8 != 0: implicit GEMM
         ((3, 16, 9, 13), (32, 16, 3, 3), "f32"),
         ((1, 8, 7, 7), (5, 8, 3, 3), None),
     ],
