@@ -14,7 +14,7 @@
 // ([filter][k] and [column][k]) with 16-byte chunk c of row r at c ^ ((r >> 2) & 3), so every
 // MFMA fragment is one conflict-free ds_read_b128; the MFMA runs as Y^T = Xcol^T W^T
 // (columns as operand A) and each lane ends with 4 consecutive output pixels of one filter.
-// Divisions by runtime extents (KH KW, KW, Ho Wo, Wo) use precomputed multipliers.
+// Divisions by runtime extents (KH KW, KW, C, Ho Wo, Wo) use precomputed multipliers.
 #pragma once
 
 #include "common.h"
@@ -50,7 +50,8 @@ struct Params {
   int n, c, h, w, f, kh, kw, ho, wo, sh, sw, dh, dw, pt, pl;
   int K, P;   // C KH KW, Ho Wo
   int NP;     // N Ho Wo
-  FastDiv div_khw, div_kw, div_p, div_wo;
+  int w_vec;  // tap-major order with KH KW == 1 and 16-byte aligned weights: chunk loads
+  FastDiv div_khw, div_kw, div_p, div_wo, div_c;
 };
 
 template <typename Tag>
@@ -69,9 +70,14 @@ struct IgElem<F32Tag> {  // fp32 operands: 4 values per chunk, 16 per slice row
 };
 }  // namespace convg
 
-// kMI: 32-row filter blocks per wave (BM = 64 kMI); kBias: 0 none, 1 fp32, 2 same dtype;
-// kVecW: K % (values per chunk) == 0 and 16-byte aligned weights (chunk loads).
-template <typename Tag, int kMI, int kBias, bool kVecW>
+// kMI: 32-row filter blocks per wave (BM = 64 kMI); kBias: 0 none, 1 fp32, 2 same dtype.
+// kOrder: the contraction order. kChannelMajor: k = (c, kh, kw) as the weight is stored,
+// weights read as scalars; kChannelMajorVecW: the same with K % (values per chunk) == 0 and
+// 16-byte aligned weights, read as chunks; kTapMajor (C % values per chunk == 0): k =
+// (kh, kw, c), so the values of one chunk share a tap: one bounds check and one address
+// per chunk (channels H W apart), weights read as scalars KH KW apart (as chunks for 1x1).
+enum ConvOrder { kChannelMajor = 0, kChannelMajorVecW = 1, kTapMajor = 2 };
+template <typename Tag, int kMI, int kBias, int kOrder>
 __global__ __launch_bounds__(convg::kThreads) void conv2d_igemm_kernel(
     const typename convg::IgElem<Tag>::T* __restrict__ x, const typename convg::IgElem<Tag>::T* __restrict__ wt,
     typename convg::IgElem<Tag>::T* __restrict__ y, const void* __restrict__ bias, convg::Params s) {
@@ -106,7 +112,30 @@ __global__ __launch_bounds__(convg::kThreads) void conv2d_igemm_kernel(
   const int hw = s.h * s.w;
   const T* xn = x + (long long)jn * s.c * hw;
 
+  auto pack = [&](const T (&v)[V]) -> u32x4 {
+    u32x4 out;
+    if constexpr (V == 8) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) out[q] = E::bits(v[2 * q]) | (E::bits(v[2 * q + 1]) << 16);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) out[q] = E::bits(v[q]);
+    }
+    return out;
+  };
   auto gather_chunk = [&](int k0) -> u32x4 {  // Xcol[k0 .. k0+V-1][j]
+    if constexpr (kOrder == kTapMajor) {
+      const uint32_t tap = fdiv(k0, s.div_c);
+      const uint32_t c0 = k0 - tap * s.c;
+      const uint32_t kh = fdiv(tap, s.div_kw);
+      const int hi = hi0 + (int)kh * s.dh, wi = wi0 + (int)(tap - kh * s.kw) * s.dw;
+      const bool ok = col_ok && k0 < s.K && (unsigned)hi < (unsigned)s.h && (unsigned)wi < (unsigned)s.w;
+      T v[V];
+      const T* src = xn + (int)c0 * hw + hi * s.w + wi;
+#pragma unroll
+      for (int e = 0; e < V; ++e) v[e] = ok ? src[e * hw] : T(0);
+      return pack(v);
+    }
     uint32_t c = fdiv(k0, s.div_khw);
     const uint32_t r = k0 - c * (s.kh * s.kw);
     uint32_t kh = fdiv(r, s.div_kw);
@@ -125,34 +154,32 @@ __global__ __launch_bounds__(convg::kThreads) void conv2d_igemm_kernel(
         }
       }
     }
-    u32x4 out;
-    if constexpr (V == 8) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) out[q] = E::bits(v[2 * q]) | (E::bits(v[2 * q + 1]) << 16);
-    } else {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) out[q] = E::bits(v[q]);
-    }
-    return out;
+    return pack(v);
   };
-  auto weight_chunk = [&](int f, int k0) -> u32x4 {  // W[f][k0 .. k0+V-1]
+  auto weight_chunk = [&](int f, int k0) -> u32x4 {  // W in contraction order: k0 .. k0+V-1
     const bool row_ok = f < s.f;
-    if constexpr (kVecW) {
+    if constexpr (kOrder == kChannelMajorVecW) {
       if (row_ok && k0 < s.K) return ld16(wt + (long long)f * s.K + k0);
       return u32x4{0, 0, 0, 0};
+    } else if constexpr (kOrder == kTapMajor) {
+      if (s.w_vec) {  // KH KW == 1: the chunk is contiguous
+        if (row_ok && k0 < s.K) return ld16(wt + (long long)f * s.K + k0);
+        return u32x4{0, 0, 0, 0};
+      }
+      const uint32_t tap = fdiv(k0, s.div_c);
+      const uint32_t c0 = k0 - tap * s.c;
+      const int khw = s.kh * s.kw;
+      const bool ok = row_ok && k0 < s.K;
+      const T* src = wt + (long long)f * s.K + (long long)c0 * khw + tap;
+      T v[V];
+#pragma unroll
+      for (int e = 0; e < V; ++e) v[e] = ok ? src[e * khw] : T(0);
+      return pack(v);
     } else {
       T v[V];
 #pragma unroll
       for (int e = 0; e < V; ++e) v[e] = (row_ok && k0 + e < s.K) ? wt[(long long)f * s.K + k0 + e] : T(0);
-      u32x4 out;
-      if constexpr (V == 8) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) out[q] = E::bits(v[2 * q]) | (E::bits(v[2 * q + 1]) << 16);
-      } else {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) out[q] = E::bits(v[q]);
-      }
-      return out;
+      return pack(v);
     }
   };
 
@@ -290,34 +317,46 @@ inline convg::Params conv_igemm_params(const ConvShape& s) {
   p.div_kw = make_fast_div((uint32_t)s.kw);
   p.div_p = make_fast_div((uint32_t)p.P);
   p.div_wo = make_fast_div((uint32_t)s.wo);
+  p.div_c = make_fast_div((uint32_t)s.c);
+  p.w_vec = 0;
   return p;
 }
 
-// BM = 128 filters per tile when F > 64, else 64.
-inline int conv_igemm_mi(const ConvShape& s) { return s.f > 64 ? 2 : 1; }
+// BM = 128 filters per tile when F > 64 and such tiles still give every CU of the MI355X
+// (256) two workgroups; else 64 (more, smaller workgroups fill the chip).
+inline int conv_igemm_mi(const ConvShape& s) {
+  const long long cols = ((long long)s.n * s.ho * s.wo + convg::kBN - 1) / convg::kBN;
+  return s.f > 64 && ((s.f + 127) / 128) * cols >= 512 ? 2 : 1;
+}
 
 template <typename Tag>
-hipError_t launch_conv2d_igemm(const void* x, const void* w, void* y, const void* bias, int bias_kind, bool vec_w,
-                               const ConvShape& s, hipStream_t stream) {
+hipError_t launch_conv2d_igemm(const void* x, const void* w, void* y, const void* bias, int bias_kind, int order,
+                               bool w_vec, const ConvShape& s, hipStream_t stream) {
   using T = typename convg::IgElem<Tag>::T;
-  const convg::Params p = conv_igemm_params(s);
+  convg::Params p = conv_igemm_params(s);
+  p.w_vec = w_vec ? 1 : 0;
   const int mi = conv_igemm_mi(s);
   const int grid = ((s.f + 64 * mi - 1) / (64 * mi)) * ((p.NP + convg::kBN - 1) / convg::kBN);
   const T* xp = static_cast<const T*>(x);
   const T* wp = static_cast<const T*>(w);
   T* yp = static_cast<T*>(y);
-#define KG_CONV_IG(MI, B, VW)                                                                                  \
-  hipLaunchKernelGGL((conv2d_igemm_kernel<Tag, MI, B, VW>), dim3(grid), dim3(convg::kThreads), 0, stream, xp, wp, yp, \
+#define KG_CONV_IG(MI, B, O)                                                                                  \
+  hipLaunchKernelGGL((conv2d_igemm_kernel<Tag, MI, B, O>), dim3(grid), dim3(convg::kThreads), 0, stream, xp, wp, yp, \
                      bias, p)
-#define KG_CONV_IG_B(MI, VW)                  \
-  if (bias_kind == 0) KG_CONV_IG(MI, 0, VW);   \
-  else if (bias_kind == 1) KG_CONV_IG(MI, 1, VW); \
-  else KG_CONV_IG(MI, 2, VW)
+#define KG_CONV_IG_B(MI, O)                  \
+  if (bias_kind == 0) KG_CONV_IG(MI, 0, O);   \
+  else if (bias_kind == 1) KG_CONV_IG(MI, 1, O); \
+  else KG_CONV_IG(MI, 2, O)
+#define KG_CONV_IG_O(MI)                                                 \
+  if (order == kTapMajor) { KG_CONV_IG_B(MI, kTapMajor); }                \
+  else if (order == kChannelMajorVecW) { KG_CONV_IG_B(MI, kChannelMajorVecW); } \
+  else { KG_CONV_IG_B(MI, kChannelMajor); }
   if (mi == 2) {
-    if (vec_w) { KG_CONV_IG_B(2, true); } else { KG_CONV_IG_B(2, false); }
+    KG_CONV_IG_O(2)
   } else {
-    if (vec_w) { KG_CONV_IG_B(1, true); } else { KG_CONV_IG_B(1, false); }
+    KG_CONV_IG_O(1)
   }
+#undef KG_CONV_IG_O
 #undef KG_CONV_IG_B
 #undef KG_CONV_IG
   return hipGetLastError();

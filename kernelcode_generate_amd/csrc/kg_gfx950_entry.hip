@@ -479,11 +479,21 @@ int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
   if (conv_igemm_supported(s) && aligned16(out.data)) {
     const int bias_kind = !bias.present ? 0 : (bias.dtype == KG_DTYPE_F32 ? 1 : 2);
     const long long K = (long long)s.c * s.kh * s.kw;
-    const bool vec_w = aligned16(w.data) && K % (out.dtype == KG_DTYPE_F32 ? 4 : 8) == 0;
+    // Contraction order (measured on MI355X): 16-bit convs are bound by their load count,
+    // so they keep the weight's own order and read weights as 16-byte chunks; fp32 and 1x1
+    // convs gain more from the tap-major gather (one bounds check and address per chunk).
+    const int per_chunk = out.dtype == KG_DTYPE_F32 ? 4 : 8;
+    const bool tap_ok = s.c % per_chunk == 0;
+    const bool vec_ok = aligned16(w.data) && K % per_chunk == 0;
+    const bool one_tap = s.kh * s.kw == 1;
+    const int order = tap_ok && (out.dtype == KG_DTYPE_F32 || one_tap || !vec_ok) ? kTapMajor
+                      : vec_ok                                                       ? kChannelMajorVecW
+                                                                                     : kChannelMajor;
+    const bool w_vec = order == kTapMajor && one_tap && vec_ok;
     const void* bp = bias.present ? bias.data : nullptr;
-    hipError_t e = out.dtype == KG_DTYPE_F32   ? launch_conv2d_igemm<F32Tag>(x.data, w.data, out.data, bp, bias_kind, vec_w, s, g_stream)
-                   : out.dtype == KG_DTYPE_BF16 ? launch_conv2d_igemm<Bf16Tag>(x.data, w.data, out.data, bp, bias_kind, vec_w, s, g_stream)
-                                                : launch_conv2d_igemm<F16Tag>(x.data, w.data, out.data, bp, bias_kind, vec_w, s, g_stream);
+    hipError_t e = out.dtype == KG_DTYPE_F32   ? launch_conv2d_igemm<F32Tag>(x.data, w.data, out.data, bp, bias_kind, order, w_vec, s, g_stream)
+                   : out.dtype == KG_DTYPE_BF16 ? launch_conv2d_igemm<Bf16Tag>(x.data, w.data, out.data, bp, bias_kind, order, w_vec, s, g_stream)
+                                                : launch_conv2d_igemm<F16Tag>(x.data, w.data, out.data, bp, bias_kind, order, w_vec, s, g_stream);
     if (e != hipSuccess) return fail(kHipFailure, "conv2d(igemm): %s", hipGetErrorString(e));
     return finish_launch("conv2d(igemm)");
   }
