@@ -2,12 +2,12 @@
 //
 // The copies are issued through inline asm so that the compiler neither tracks nor waits
 // for them (its own tracking of global_load_lds inserts vmcnt(0) before every LDS read).
-// Each statement sets M0 itself and lists it as clobbered; clang warns that M0 is a
-// reserved register. Nothing else in these kernels reads M0 (gfx9 LDS instructions do not
-// use it), so no value the compiler keeps there can be lost.
 // The waits below are therefore the only synchronisation: a wave waits for its own copies
 // with s_waitcnt vmcnt, then meets the other waves at s_barrier; the empty asm statement
 // after the barrier keeps LDS reads from being moved across it.
+// Each copy statement sets M0 itself and lists it as clobbered; clang warns that M0 is a
+// reserved register. Nothing else in these kernels reads M0 (gfx9 LDS instructions do not
+// use it), so no value the compiler keeps there can be lost.
 #pragma once
 
 #include "common.h"
