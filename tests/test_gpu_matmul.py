@@ -169,8 +169,9 @@ def test_ragged_edges_store_only_inside(device, oracle_mod, shape, rows):
         ((1000, 520, 1000), None, True),  # every edge ragged, 8-deep last K slice
         ((777, 64, 2052), None, True),  # 4 columns past the last full tile
         ((4096, 4096, 4096), [(0, 32), (4064, 4096)], False),
+        ((1024, 300, 1000), None, True),  # lhs and rhs as column windows of wider buffers
     ],
-    ids=["1024x256x1024", "1000x520x1000", "777x64x2052", "4096^3"],
+    ids=["1024x256x1024", "1000x520x1000", "777x64x2052", "4096^3", "strided"],
 )
 def test_f32_matrix_core_shapes(device, oracle_mod, shape, rows, with_bias):
     """fp32 operands large enough for the fp32 MFMA kernel (v_mfma_f32_32x32x2_f32), which
@@ -190,9 +191,13 @@ def test_f32_matrix_core_shapes(device, oracle_mod, shape, rows, with_bias):
     bias = rng.uniform(-1, 1, n).astype(np.float32) if with_bias else None
     big = torch.full((m + 3, n + 4), float("nan"), dtype=torch.float32, device=device)
     out = big[:m, :n]
-    print(f"[matmul] f32 matrix cores M={m} K={k} N={n} bias={with_bias}", flush=True)
-    native.matmul(out, torch.from_numpy(lhs).to(device), torch.from_numpy(rhs).to(device),
-                  None if bias is None else torch.from_numpy(bias).to(device))
+    lt, rt = torch.from_numpy(lhs).to(device), torch.from_numpy(rhs).to(device)
+    if shape == (1024, 300, 1000):  # the "strided" case: row strides k + 12 and n + 20 (multiples of 4)
+        lt = torch.cat([lt, torch.zeros(m, 12, device=device)], 1)[:, :k]
+        rt = torch.cat([rt, torch.zeros(k, 20, device=device)], 1)[:, :n]
+        assert not lt.is_contiguous() and not rt.is_contiguous()
+    print(f"[matmul] f32 matrix cores M={m} K={k} N={n} bias={with_bias} lda={lt.stride(0)} ldb={rt.stride(0)}", flush=True)
+    native.matmul(out, lt, rt, None if bias is None else torch.from_numpy(bias).to(device))
     got = to_numpy(big)
     assert np.isnan(got[m:]).all() and np.isnan(got[:, n:]).all(), "store outside the output window"
     for r0, r1 in rows or [(0, m)]:
