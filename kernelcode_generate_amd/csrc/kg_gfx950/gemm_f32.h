@@ -193,3 +193,67 @@ __global__ __launch_bounds__(gemmf::kThreads, 3) void gemm_f32_mfma_kernel(
 }
 
 }  // namespace kg_gfx950
+
+namespace kg_gfx950 {
+
+// Split-K fp32 GEMM for small outputs (C1's 256^3 is 64 blocks of 32 x 32): one 1024-thread
+// workgroup per 32 x 32 output block; its 16 waves take interleaved 16-deep K slices (wave
+// w: k = 16 (w + 16 i) ..), load their operands straight from HBM/L2 into registers (lhs as
+// 16-byte row pieces, rhs as 32 consecutive columns of one k-row per lane half) and run
+// v_mfma_f32_32x32x2_f32 with the k order of gemm_f32_mfma_kernel; the 16 partial blocks are
+// summed through LDS, wave by wave in order, and the sum is stored once. No workspace: the
+// reduction never leaves the workgroup. Host requirements: M % 32 == 0, N % 32 == 0,
+// K % 16 == 0, unit inner strides, lhs row stride a multiple of 4, 16-byte aligned lhs.
+namespace gemmk {
+constexpr int kWaves = 16;
+constexpr int kThreads = 64 * kWaves;
+}  // namespace gemmk
+
+template <int kBias>
+__global__ __launch_bounds__(gemmk::kThreads, 1) void gemm_f32_splitk_kernel(
+    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, const float* __restrict__ bias,
+    int M, int N, int K, long long lda, long long ldb, long long ldc) {
+  using namespace gemmk;
+  __shared__ float part[kWaves][16][64];  // [wave][accumulator element][lane], 64 KiB
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int frag = lane & 31, h = lane >> 5;
+  const int tiles_n = N / 32;
+  const int m0 = (blockIdx.x / tiles_n) * 32;
+  const int n0 = (blockIdx.x % tiles_n) * 32;
+  const float* a_row = A + (long long)(m0 + frag) * lda + 4 * h;  // + k0 + 8 g
+  const float* b_col = B + (long long)(4 * h) * ldb + n0 + frag;  // + (k0 + 8 g + kk) ldb
+
+  f32x16 acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+  for (int k0 = 16 * wave; k0 < K; k0 += 16 * kWaves) {
+    f32x4 a[2];
+    float b[2][4];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      a[g] = *reinterpret_cast<const f32x4*>(a_row + k0 + 8 * g);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) b[g][kk] = b_col[(long long)(k0 + 8 * g + kk) * ldb];
+    }
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(b[g][kk], a[g][kk], acc, 0, 0, 0);
+  }
+#pragma unroll
+  for (int e = 0; e < 16; ++e) part[wave][e][lane] = acc[e];
+  __syncthreads();
+  // thread t sums element e = t / 64 of lane l = t % 64 over the waves:
+  // C[m0 + l % 32][n0 + 8 (e / 4) + 4 (l / 32) + e % 4]
+  const int l = tid & 63, e = tid >> 6;
+  float v = 0.f;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) v += part[w][e][l];
+  const int n = n0 + 8 * (e >> 2) + 4 * (l >> 5) + (e & 3);
+  if constexpr (kBias) v += bias[n];
+  C[(long long)(m0 + (l & 31)) * ldc + n] = v;
+}
+
+}  // namespace kg_gfx950

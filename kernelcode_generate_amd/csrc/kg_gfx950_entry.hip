@@ -301,6 +301,29 @@ int launch_gemm_f32_mfma(const Mem& out, const Mem& lhs, const Mem& rhs, const M
   return finish_launch(ragged ? "matmul(f32-mfma-ragged)" : "matmul(f32-mfma)");
 }
 
+// Small fp32 outputs (fewer than kF32MfmaMinTiles tiles of 128 x 128) with 32-aligned
+// extents: split-K inside a workgroup per 32 x 32 block.
+bool gemm_f32_splitk_ok(const Mem& out, const Mem& lhs, const Mem& rhs, long long M, long long N, long long K) {
+  return M % 32 == 0 && N % 32 == 0 && K % 16 == 0 && K > 0 && M > 0 && N > 0 && lhs.stride[1] == 1 &&
+         rhs.stride[1] == 1 && out.stride[1] == 1 && lhs.stride[0] % 4 == 0 && aligned16(lhs.data) &&
+         (M / 32) * (N / 32) < (1LL << 31);
+}
+
+int launch_gemm_f32_splitk(const Mem& out, const Mem& lhs, const Mem& rhs, const Mem& bias, int M, int N, int K) {
+  const int grid = (M / 32) * (N / 32);
+  const float* A = static_cast<const float*>(lhs.data);
+  const float* B = static_cast<const float*>(rhs.data);
+  float* C = static_cast<float*>(out.data);
+  const float* bp = bias.present ? static_cast<const float*>(bias.data) : nullptr;
+  if (bp)
+    hipLaunchKernelGGL((gemm_f32_splitk_kernel<1>), dim3(grid), dim3(gemmk::kThreads), 0, g_stream, A, B, C, bp, M, N, K,
+                       lhs.stride[0], rhs.stride[0], out.stride[0]);
+  else
+    hipLaunchKernelGGL((gemm_f32_splitk_kernel<0>), dim3(grid), dim3(gemmk::kThreads), 0, g_stream, A, B, C, bp, M, N, K,
+                       lhs.stride[0], rhs.stride[0], out.stride[0]);
+  return finish_launch("matmul(f32-splitk)");
+}
+
 int matmul_impl(const KgArgSlot* args, unsigned long long n) {
   if (args == nullptr) return fail(kInvalid, "ordered_args is null");
   if (n != 4 && n != 7 && n != 8) return fail(kInvalid, "matmul expects 4, 7 or 8 slots, got %llu", n);
@@ -349,6 +372,9 @@ int matmul_impl(const KgArgSlot* args, unsigned long long n) {
     long long mfma = 0;
     if (f32_mfma_ok)  // 4 waves x 2 x 2 blocks x 8 k-steps (32x32x2) per 16-deep slice of a 128 x 128 tile
       mfma = cdiv(M, gemmf::kTile) * cdiv(N, gemmf::kTile) * cdiv(K, gemmf::kBK) * 128;
+    else if (out.dtype == KG_DTYPE_F32 && gemm_f32_splitk_ok(out, lhs, rhs, M, N, K) &&
+             (!bias.present || bias.stride[0] == 1))  // 8 MFMAs (32x32x2) per 32 x 32 block and 16-deep slice
+      mfma = (M / 32) * (N / 32) * (K / 16) * 8;
     if (mfma_ok && M > 0 && N > 0) {
       // 8 waves x tm/16 MFMAs (32x32x16) per 32-deep slice of a tm x 256 tile; ragged edges
       // are covered by whole tiles and slices
@@ -362,6 +388,8 @@ int matmul_impl(const KgArgSlot* args, unsigned long long n) {
 
   if (out.dtype == KG_DTYPE_F32) {
     if (f32_mfma_ok) return launch_gemm_f32_mfma(out, lhs, rhs, bias, m, nn, k);
+    if (gemm_f32_splitk_ok(out, lhs, rhs, M, N, K) && (!bias.present || bias.stride[0] == 1))
+      return launch_gemm_f32_splitk(out, lhs, rhs, bias, m, nn, k);
     return launch_gemm_simt<float, float>(out, lhs, rhs, bias, m, nn, k);
   }
   if (out.dtype == KG_DTYPE_BF16) {

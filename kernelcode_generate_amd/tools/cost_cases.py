@@ -7,7 +7,7 @@ Every case makes exactly one library kernel dispatch, in the order printed, and 
 else dispatches a kernel (inputs are generated on the host and copied), so dispatch i of the
 counter run is case i. Cases cover every kernel choice the model distinguishes: the
 pipelined MFMA GEMM with 256- and 128-row tiles and with ragged edges, the fp32 MFMA GEMM
-aligned and ragged, the SIMT GEMM, the MFMA conv with four and with two live waves and a
+aligned and ragged, the fp32 split-K GEMM, the SIMT GEMM, the MFMA conv with four and with two live waves and a
 ragged last row block, the implicit-GEMM conv (16-bit and fp32), and the 16-bit and fp32 MFMA attention kernels for D=128 and D=64,
 causal and not, with ragged query and key tails.
 """
@@ -28,6 +28,8 @@ CASES = (
     ("gemm_f16_512x768x256", "matmul", "float16", ((512, 768), (512, 256), (256, 768)), ()),
     ("gemm_bf16_ragged_1000x1000x520", "matmul", "bfloat16", ((1000, 1000), (1000, 520), (520, 1000)), ()),
     ("gemm_f32_256", "matmul", "float32", ((256, 256), (256, 256), (256, 256)), ()),
+    ("gemm_f32_splitk_512x512x4096", "matmul", "float32", ((512, 512), (512, 4096), (4096, 512)), ()),
+    ("gemm_f32_simt_250x250x250", "matmul", "float32", ((250, 250), (250, 250), (250, 250)), ()),
     ("gemm_f32_mfma_1024x256x1024", "matmul", "float32", ((1024, 1024), (1024, 256), (256, 1024)), ()),
     ("gemm_f32_ragged_1000x1000x520", "matmul", "float32", ((1000, 1000), (1000, 520), (520, 1000)), ()),
     ("conv_f16_c3", "conv2d", "float16", ((32, 64, 56, 56), (32, 64, 56, 56), (64, 64, 3, 3)), (1, 1, 1, 1, 1, 1, 1, 1)),

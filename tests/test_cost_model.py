@@ -104,6 +104,8 @@ def test_matmul_counts(dtype, mnk):
             assert c["MFMA"] * 2048 >= c["MAC"]
             if m % 128 == 0 and n % 128 == 0 and k % 16 == 0:
                 assert c["MFMA"] * 2048 == c["MAC"]
+        elif m % 32 == 0 and n % 32 == 0 and k % 16 == 0:  # split-K blocks of 32 x 32: exact
+            assert c["MFMA"] * 2048 == c["MAC"]
         else:
             assert c["MFMA"] == 0  # SIMT path
     elif k % 8 or n % 8:

@@ -210,6 +210,36 @@ def test_f32_matrix_core_shapes(device, oracle_mod, shape, rows, with_bias):
 
 
 @pytest.mark.parametrize(
+    "shape,with_bias,strided",
+    [((256, 256, 256), True, False), ((64, 96, 4096), False, False), ((512, 512, 4096), True, True)],
+    ids=["c1_bias", "k_heavy", "strided_lhs"],
+)
+def test_f32_split_k(device, oracle_mod, shape, with_bias, strided):
+    """Small fp32 outputs with 32-aligned extents: one workgroup per 32 x 32 block sums K
+    across its 16 waves (MFMA 32x32x2) and reduces the partial blocks in LDS. Tolerance as in
+    test_f32_matrix_core_shapes: the demo's rtol/atol plus 4 sqrt(K) 2^-24 (|A| |B|)."""
+
+    import torch
+
+    m, k, n = shape
+    rng = np.random.default_rng(m + k + n)
+    lhs = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    rhs = rng.uniform(-1, 1, (k, n)).astype(np.float32)
+    bias = rng.uniform(-1, 1, n).astype(np.float32) if with_bias else None
+    lt, rt = torch.from_numpy(lhs).to(device), torch.from_numpy(rhs).to(device)
+    if strided:  # lhs row stride k + 8
+        lt = torch.cat([lt, torch.zeros(m, 8, device=device)], 1)[:, :k]
+    out = torch.full((m, n), float("nan"), device=device)
+    print(f"[matmul] f32 split-K M={m} K={k} N={n} bias={with_bias} lda={lt.stride(0)}", flush=True)
+    native.matmul(out, lt, rt, None if bias is None else torch.from_numpy(bias).to(device))
+    ref = oracle_mod.matmul_demo(lhs, rhs, bias, (64, 64, 64))
+    terms = np.abs(lhs).astype(np.float64) @ np.abs(rhs).astype(np.float64)
+    tol = 1e-4 * np.abs(ref) + 1e-5 + 4 * np.sqrt(k) * 2.0 ** -24 * terms
+    err = np.abs(to_numpy(out).astype(np.float64) - ref)
+    assert (err <= tol).all(), f"{shape}: max err/tol {np.max(err / tol):.3g}"
+
+
+@pytest.mark.parametrize(
     "cfg",
     [
         ("C2", 4096, 4096, 4096, 20261202, [(0, 96), (2016, 2112), (4000, 4096)]),
