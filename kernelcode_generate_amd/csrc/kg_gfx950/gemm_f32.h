@@ -207,6 +207,7 @@ namespace kg_gfx950 {
 namespace gemmk {
 constexpr int kWaves = 16;
 constexpr int kThreads = 64 * kWaves;
+static_assert(16 % kWaves == 0, "reduction: 16 accumulator elements per lane over the waves");
 }  // namespace gemmk
 
 template <int kBias>
@@ -245,15 +246,18 @@ __global__ __launch_bounds__(gemmk::kThreads, 1) void gemm_f32_splitk_kernel(
 #pragma unroll
   for (int e = 0; e < 16; ++e) part[wave][e][lane] = acc[e];
   __syncthreads();
-  // thread t sums element e = t / 64 of lane l = t % 64 over the waves:
+  // thread t sums elements e = t / 64 + kWaves i of lane l = t % 64 over the waves:
   // C[m0 + l % 32][n0 + 8 (e / 4) + 4 (l / 32) + e % 4]
-  const int l = tid & 63, e = tid >> 6;
-  float v = 0.f;
+  const int l = tid & 63;
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) v += part[w][e][l];
-  const int n = n0 + 8 * (e >> 2) + 4 * (l >> 5) + (e & 3);
-  if constexpr (kBias) v += bias[n];
-  C[(long long)(m0 + (l & 31)) * ldc + n] = v;
+  for (int e = tid >> 6; e < 16; e += kWaves) {
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) v += part[w][e][l];
+    const int n = n0 + 8 * (e >> 2) + 4 * (l >> 5) + (e & 3);
+    if constexpr (kBias) v += bias[n];
+    C[(long long)(m0 + (l & 31)) * ldc + n] = v;
+  }
 }
 
 }  // namespace kg_gfx950
