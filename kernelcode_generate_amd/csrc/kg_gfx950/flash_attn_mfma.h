@@ -2,7 +2,8 @@
 // fp32 online softmax, optional scale and causal mask.
 //
 // Work split: a workgroup holds query rows of one (b,h), 32 per wave (Cfg<D>: 8 waves for
-// D=128, 4 for D=64; two waves per SIMD either way). Key/value tiles of 64 keys are copied
+// D=128, 4 for D=64 and for D=128 grids too small to give every CU an 8-wave workgroup;
+// two waves per SIMD either way). Key/value tiles of 64 keys are copied
 // HBM -> LDS (two buffers each for K and V) and shared by the workgroup's waves. Workgroup
 // ids are dealt to the 8 XCDs round-robin; they are remapped so that each XCD runs the query
 // blocks of the same (b,h) together and its L2 serves their K/V.
@@ -49,9 +50,11 @@ constexpr int kBC = 64;  // keys per tile
 // Waves per workgroup (32 queries each): D=128 uses one 8-wave workgroup per CU (K/V tiles
 // shared by 256 queries halve the HBM/L2 -> LDS copy traffic per query), D=64 two 4-wave
 // workgroups per CU. Either way two waves share each SIMD.
-template <int D>
+// A D=128 launch whose 8-wave grid would leave CUs without a workgroup takes 4-wave
+// workgroups (two per CU) instead: twice the workgroups for the same queries.
+template <int D, int W = (D == 128 ? 8 : 4)>
 struct Cfg {
-  static constexpr int kWaves = D == 128 ? 8 : 4;
+  static constexpr int kWaves = W;
   static constexpr int kBM = 32 * kWaves;  // queries per workgroup
   static constexpr int kThreads = 64 * kWaves;
   static constexpr int kPerCU = 8 / kWaves;
@@ -73,23 +76,22 @@ __host__ __device__ constexpr int v_mask(int key) {
   return D == 128 ? 4 * (key & 3) : 4 * ((key >> 1) & 1);
 }
 
-// Copy instruction p of wave w covers tile rows (w*PW + p)*RPP + lane/DCH. Per-lane HBM
-// offsets are kept for p = 0 and 1 (K) or p = 0 (V); the other instructions move the
-// wave-uniform base by whole KiB, which needs the masks of their rows to repeat.
-template <int D>
-constexpr bool copy_masks_repeat() {
-  constexpr int kWaves = Cfg<D>::kWaves;
-  constexpr int RB = 2 * D, PW = kBC * RB / 1024 / kWaves, RPP = 1024 / RB, DCH = D / 8;
-  for (int w = 0; w < kWaves; ++w)
+// Copy instruction p of wave w covers tile rows (w*PW + p)*RPP + lane/DCH. K keeps a
+// per-lane HBM offset for every p; V keeps the one of p = 0 and moves the wave-uniform base
+// by whole KiB, which needs the V masks of the rows to repeat.
+template <int D, int W>
+constexpr bool v_copy_masks_repeat() {
+  constexpr int RB = 2 * D, PW = kBC * RB / 1024 / W, RPP = 1024 / RB, DCH = D / 8;
+  for (int w = 0; w < W; ++w)
     for (int lane = 0; lane < 64; ++lane)
       for (int p = 0; p < PW; ++p) {
         const int row = (w * PW + p) * RPP + lane / DCH;
-        if (k_mask<D>(row) != k_mask<D>((w * PW + (p & 1)) * RPP + lane / DCH)) return false;
         if (v_mask<D>(row) != v_mask<D>((w * PW) * RPP + lane / DCH)) return false;
       }
   return true;
 }
-static_assert(copy_masks_repeat<128>() && copy_masks_repeat<64>(), "copy offsets");
+static_assert(v_copy_masks_repeat<128, 8>() && v_copy_masks_repeat<128, 4>() && v_copy_masks_repeat<64, 4>(),
+              "copy offsets");
 
 // Bijection of workgroup ids: XCD x (ids with id % 8 == x) gets one contiguous range.
 __device__ __forceinline__ int xcd_block(int pid, int total) {
@@ -105,16 +107,16 @@ __device__ __forceinline__ float max3f(float a, float b, float c) {
 
 }  // namespace fa
 
-template <typename Tag, int D, bool kCausal, bool kMasked>
-__global__ __launch_bounds__(fa::Cfg<D>::kThreads, fa::Cfg<D>::kPerCU) void fa_fwd_mfma_kernel(const uint16_t* __restrict__ Q,
+template <typename Tag, int D, bool kCausal, bool kMasked, int W>
+__global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU)) void fa_fwd_mfma_kernel(const uint16_t* __restrict__ Q,
                                                                       const uint16_t* __restrict__ K,
                                                                       const uint16_t* __restrict__ V,
                                                                       uint16_t* __restrict__ O, int bh_count, int s_q,
                                                                       int s_kv, float scale_log2) {
   using namespace fa;
   using H = Half16<Tag>;
-  constexpr int kWaves = Cfg<D>::kWaves;
-  constexpr int kBM = Cfg<D>::kBM;
+  constexpr int kWaves = Cfg<D, W>::kWaves;
+  constexpr int kBM = Cfg<D, W>::kBM;
   constexpr int RB = 2 * D;          // bytes per K/V row
   constexpr int TB = kBC * RB;       // bytes per K or V tile
   constexpr int DCH = D / 8;         // 16-byte chunks per row
@@ -160,9 +162,9 @@ __global__ __launch_bounds__(fa::Cfg<D>::kThreads, fa::Cfg<D>::kPerCU) void fa_f
   const uint32_t lds0 = lds_addr(&lds[0]);
   const int c_row0 = wave * PW * RPP + lane / DCH;
   const int c_slot = lane % DCH;
-  uint32_t k_goff[2];
+  uint32_t k_goff[PW];
 #pragma unroll
-  for (int p = 0; p < 2; ++p) {
+  for (int p = 0; p < PW; ++p) {
     const int row = c_row0 + p * RPP;
     k_goff[p] = (uint32_t)(row * RB + 16 * (c_slot ^ k_mask<D>(row)));
   }
@@ -179,7 +181,7 @@ __global__ __launch_bounds__(fa::Cfg<D>::kThreads, fa::Cfg<D>::kPerCU) void fa_f
     } else {
       const char* base = src + (long long)n0 * RB;
       if (kV) g2lds16_s(v_goff, base + p * 1024, m);
-      else g2lds16_s(k_goff[p & 1], base + (p & ~1) * 1024, m);
+      else g2lds16_s(k_goff[p], base, m);
     }
   };
   auto copy_k = [&](int t, int buf) {
@@ -436,36 +438,42 @@ inline bool fa_mfma_supported(const FaShape& s) {
          (long long)((s.s_q + fa::Cfg<64>::kBM - 1) / fa::Cfg<64>::kBM) * s.bh < (1ll << 31);
 }
 
-template <typename Tag, int D>
-hipError_t launch_fa_fwd_mfma_d(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, const FaShape& s,
-                                hipStream_t stream) {
-  const int nmb = (s.s_q + fa::Cfg<D>::kBM - 1) / fa::Cfg<D>::kBM;
+template <typename Tag, int D, int W>
+hipError_t launch_fa_fwd_mfma_dw(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, const FaShape& s,
+                                 hipStream_t stream) {
+  using C = fa::Cfg<D, W>;
+  const int nmb = (s.s_q + C::kBM - 1) / C::kBM;
   const dim3 grid(nmb * s.bh);
-  const bool masked = (s.s_q % fa::Cfg<D>::kBM) != 0 || (s.s_kv % fa::kBC) != 0;
+  const bool masked = (s.s_q % C::kBM) != 0 || (s.s_kv % fa::kBC) != 0;
   const float scale_log2 = s.scale * 1.4426950408889634f;
+#define KG_FA(CAUSAL, MASKED)                                                                                    \
+  hipLaunchKernelGGL((fa_fwd_mfma_kernel<Tag, D, CAUSAL, MASKED, W>), grid, dim3(C::kThreads), 0, stream, q, k, v, o, \
+                     s.bh, s.s_q, s.s_kv, scale_log2)
   if (s.causal) {
-    if (masked)
-      hipLaunchKernelGGL((fa_fwd_mfma_kernel<Tag, D, true, true>), grid, dim3(fa::Cfg<D>::kThreads), 0, stream, q, k, v, o, s.bh,
-                         s.s_q, s.s_kv, scale_log2);
-    else
-      hipLaunchKernelGGL((fa_fwd_mfma_kernel<Tag, D, true, false>), grid, dim3(fa::Cfg<D>::kThreads), 0, stream, q, k, v, o, s.bh,
-                         s.s_q, s.s_kv, scale_log2);
+    if (masked) KG_FA(true, true); else KG_FA(true, false);
   } else {
-    if (masked)
-      hipLaunchKernelGGL((fa_fwd_mfma_kernel<Tag, D, false, true>), grid, dim3(fa::Cfg<D>::kThreads), 0, stream, q, k, v, o, s.bh,
-                         s.s_q, s.s_kv, scale_log2);
-    else
-      hipLaunchKernelGGL((fa_fwd_mfma_kernel<Tag, D, false, false>), grid, dim3(fa::Cfg<D>::kThreads), 0, stream, q, k, v, o, s.bh,
-                         s.s_q, s.s_kv, scale_log2);
+    if (masked) KG_FA(false, true); else KG_FA(false, false);
   }
+#undef KG_FA
   return hipGetLastError();
+}
+
+// Waves per workgroup the launch uses: D=128 drops to 4 when 8-wave workgroups would not
+// give every CU of the MI355X (256) one.
+inline int fa_mfma_waves(const FaShape& s) {
+  if (s.d != 128) return fa::Cfg<64>::kWaves;
+  const long long wg8 = (long long)s.bh * ((s.s_q + fa::Cfg<128, 8>::kBM - 1) / fa::Cfg<128, 8>::kBM);
+  return wg8 < 256 ? 4 : 8;
 }
 
 template <typename Tag>
 hipError_t launch_fa_fwd_mfma(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, const FaShape& s,
                               hipStream_t stream) {
-  if (s.d == 128) return launch_fa_fwd_mfma_d<Tag, 128>(q, k, v, o, s, stream);
-  return launch_fa_fwd_mfma_d<Tag, 64>(q, k, v, o, s, stream);
+  if (s.d == 128) {
+    if (fa_mfma_waves(s) == 4) return launch_fa_fwd_mfma_dw<Tag, 128, 4>(q, k, v, o, s, stream);
+    return launch_fa_fwd_mfma_dw<Tag, 128, 8>(q, k, v, o, s, stream);
+  }
+  return launch_fa_fwd_mfma_dw<Tag, 64, 4>(q, k, v, o, s, stream);
 }
 
 }  // namespace kg_gfx950

@@ -599,7 +599,7 @@ int flash_attention_impl(const KgArgSlot* args, unsigned long long n) {
     long long mfma = 0;
     if ((out.dtype == KG_DTYPE_BF16 || out.dtype == KG_DTYPE_F16) && fa_mfma_supported(s) && out.numel() > 0) {
       // per workgroup: waves x key tiles x (D/8 MFMAs for S^T + D/8 for PV)
-      const int waves = s.d == 128 ? fa::Cfg<128>::kWaves : fa::Cfg<64>::kWaves;
+      const int waves = fa_mfma_waves(s);
       const int bm = 32 * waves;
       const int nmb = (s.s_q + bm - 1) / bm;
       long long tiles = 0;

@@ -184,6 +184,29 @@ def test_c4_full_size(device, oracle_mod):
     assert ((got >= vmin - slack) & (got <= vmax + slack)).all()
 
 
+@pytest.mark.parametrize(
+    "shape,causal",
+    [((2, 64, 1000, 128), False), ((1, 128, 700, 128), True), ((1, 8, 2048, 128), False)],
+    ids=["8wave_ragged", "8wave_ragged_causal", "4wave_small_grid"],
+)
+def test_workgroup_shapes_d128(device, oracle_mod, shape, causal):
+    """D=128 takes 8-wave workgroups (256 queries) when they give every CU one and 4-wave
+    workgroups (128 queries) otherwise: the first two shapes are 512 and 384 ragged 8-wave
+    workgroups, the third 128 4-wave ones. Sampled heads and row blocks against the oracle."""
+
+    import torch
+
+    b, h, s, d = shape
+    rng = np.random.default_rng(s + h)
+    (qt, q), (kt, k), (vt, v) = (round_to(rng.standard_normal(shape, dtype=np.float32), torch.bfloat16) for _ in range(3))
+    scale = 1.0 / np.sqrt(128.0)
+    got = to_numpy(run(device, torch.bfloat16, qt, kt, vt, 128, 64, scale, causal))
+    assert np.isfinite(got).all()
+    heads = [(0, 0), (b - 1, h - 1)]
+    blocks = [(0, 64), (s - 64 - s % 7, s - s % 7), (s - 40, s)]
+    _sampled_check(oracle_mod, got, q, k, v, heads, blocks, scale, causal, f"{shape}")
+
+
 @pytest.mark.parametrize("d,seed", [(128, 20261206), (64, 20261207)])
 def test_c5_full_size_causal(device, oracle_mod, d, seed):
     import torch
