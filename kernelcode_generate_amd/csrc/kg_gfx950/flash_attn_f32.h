@@ -137,14 +137,23 @@ __global__ __launch_bounds__(faf::kThreads, D == 128 ? 2 : 4) void fa_fwd_f32_mf
     const uint32_t kb = lds0 + (t & 1) * kTileBytes;
     const uint32_t vb = lds0 + (2 + (t & 1)) * kTileBytes;
 
+    // Operands are read one step ahead of their MFMAs, so an LDS read's latency overlaps the
+    // MFMAs of the step before instead of stalling its own.
     f32x16 s;
 #pragma unroll
     for (int e = 0; e < 16; ++e) s[e] = 0.f;
+    auto read_k = [&](int g) {
+      return *(const __attribute__((address_space(3))) f32x4*)(uintptr_t)(kb + k_rd[g]);
+    };
+    f32x4 kf = read_k(0);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const f32x4 kf = *(const __attribute__((address_space(3))) f32x4*)(uintptr_t)(kb + k_rd[g]);
+      const f32x4 kn = g + 1 < G ? read_k(g + 1) : kf;
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[kk], qf[g][kk], s, 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      kf = kn;
     }
 
     // mask: keys past S_kv, and (causal) keys after the query
@@ -174,16 +183,25 @@ __global__ __launch_bounds__(faf::kThreads, D == 128 ? 2 : 4) void fa_fwd_f32_mf
 #pragma unroll
       for (int e = 0; e < 16; ++e) o[b][e] *= alpha;
 
+    // PV step t = 4 ep + i pairs keys 8 ep + i and 8 ep + 4 + i
+    auto read_v = [&](int t, int b) {
+      return *(const __attribute__((address_space(3))) float*)(uintptr_t)(vb + v_rd[b] + (8 * (t >> 2) + (t & 3)) * D * 4);
+    };
+    float vc[NB];
 #pragma unroll
-    for (int ep = 0; ep < 4; ++ep)
+    for (int b = 0; b < NB; ++b) vc[b] = read_v(0, b);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+    for (int t = 0; t < 16; ++t) {
+      float vn[NB];
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-          const float vv =
-              *(const __attribute__((address_space(3))) float*)(uintptr_t)(vb + v_rd[b] + (8 * ep + i) * D * 4);
-          o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, s[4 * ep + i], o[b], 0, 0, 0);
-        }
+      for (int b = 0; b < NB; ++b) vn[b] = t + 1 < 16 ? read_v(t + 1, b) : vc[b];
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vc[b], s[t], o[b], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) vc[b] = vn[b];
+    }
   }
 
   if (!active) return;
