@@ -151,26 +151,31 @@ __global__ __launch_bounds__(gemmf::kThreads, 3) void gemm_f32_mfma_kernel(
     else wait_and_barrier<0>();
     if (kt + 2 < ktiles) issue(kt + 2);
     const uint32_t st = lds0 + (kt % kStages) * kStageBytes;
+    // all fragments of the slice are read before its MFMAs: the reads of half 1 land while
+    // the MFMAs of half 0 run
+    f32x4 a[2][2];
+    float b[2][2][4];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      f32x4 a[2];
-      float b[2][4];
 #pragma unroll
       for (int i = 0; i < 2; ++i)
-        a[i] = *(const __attribute__((address_space(3))) f32x4*)(uintptr_t)(st + a_rd[i][ks]);
+        a[ks][i] = *(const __attribute__((address_space(3))) f32x4*)(uintptr_t)(st + a_rd[i][ks]);
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk)
-          b[j][kk] = *(const __attribute__((address_space(3))) float*)(uintptr_t)(st + b_rd[j] + (8 * ks + kk) * 512);
+          b[ks][j][kk] = *(const __attribute__((address_space(3))) float*)(uintptr_t)(st + b_rd[j] + (8 * ks + kk) * 512);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
           for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[j][kk], a[i][kk], acc[i][j], 0, 0, 0);
-    }
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[ks][j][kk], a[ks][i][kk], acc[i][j], 0, 0, 0);
   }
 
   // Epilogue: lane l holds C[m][n .. n+3], m = row block + l % 32, n = column block
