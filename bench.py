@@ -22,7 +22,10 @@ The JSON line also carries
   secondary: the other BASELINE configs (C1, C2', C3, C4, C5 D=128/64) and two fp32 extension
             lines (C2's and C4's shapes in the reference demos' fp32), each after 0.15 s
             of untimed launches, over >= 200 (C1, C2'), 1000 (C3), 100 (C4), 25 (C5), 50
-            (fp32 matmul) or 20 (fp32 attention) back-to-back launches.
+            (fp32 matmul) or 20 (fp32 attention) back-to-back launches. Each carries its
+            own cpu_baseline: the same restated loop nest (-O0, 2 threads), C1 in full
+            (median of 5), the others on a fixed sample of outer tiles extrapolated to the
+            full problem (cpu_baselines()).
 """
 
 from __future__ import annotations
@@ -148,6 +151,96 @@ def cpu_baseline_matmul(rows: int = 384):
     }
 
 
+def _timed(fn, repeats: int = 1) -> float:
+    """Median wall seconds of `repeats` calls of fn."""
+
+    times = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2]
+
+
+def cpu_baselines(keys) -> dict:
+    """CPU baseline of every secondary workload: the oracle's restatement of the
+    reference's npu_demo loop nest for it (kernel/{matmul,conv2d,flash_attention}/
+    inputs_static_tile_static.py on include/npu_demo/Kernel.h), compiled without -O like
+    the reference's build and run on 2 host threads (npu_demo block_num = 2, the
+    block-strided top-level loop). C1 runs in full (median of 5); the others run a fixed
+    sample of outer tiles and are extrapolated to the full problem by algorithmic FLOP
+    (causal: kept query-key pairs), labelled "extrapolated". Inputs have the workloads'
+    shapes and distributions (numpy generators, same seeds)."""
+
+    import numpy as np
+
+    import oracle
+
+    out = {}
+    model = cpu_model()
+
+    def rec(value_flop, seconds, full_flop, sample, cores=2, extrapolated=True):
+        r = {"value": value_flop / seconds / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+             "sample": sample, "sample_s": round(seconds, 3), "extrapolated": extrapolated,
+             "full_problem_s": round(full_flop / (value_flop / seconds), 2), "cpu_model": model}
+        return r
+
+    tiles_mm = (48, 80, 56)
+    if "c1" in keys:
+        rng = np.random.default_rng(20261201)
+        a = rng.uniform(-1, 1, (256, 256)).astype(np.float32)
+        b = rng.uniform(-1, 1, (256, 256)).astype(np.float32)
+        oracle.matmul_demo(a, b, None, tiles_mm, threads=2, optimized=False)  # warm
+        dt = _timed(lambda: oracle.matmul_demo(a, b, None, tiles_mm, threads=2, optimized=False), 5)
+        f = 2.0 * 256**3
+        out["c1"] = rec(f, dt, f, "the whole 256^3 fp32 matmul through the restated npu_demo tile loop "
+                        "(tiles 48x80x56), median of 5 runs", extrapolated=False)
+    if "c2s" in keys:
+        rng = np.random.default_rng(20261203)
+        rows = 128
+        a = rng.standard_normal((rows, 4096), dtype=np.float32) * 0.02
+        b = rng.standard_normal((4096, 1024), dtype=np.float32) * 0.02
+        dt = _timed(lambda: oracle.matmul_demo(a, b, None, tiles_mm, threads=2, optimized=False))
+        out["c2s"] = rec(2.0 * rows * 1024 * 4096, dt, 2.0 * 8192 * 1024 * 4096,
+                         f"output rows 0-{rows - 1} of 8192 (tiles 48x80x56, fp32)")
+    if "c3" in keys:
+        rng = np.random.default_rng(20261204)
+        x = rng.standard_normal((32, 64, 56, 56), dtype=np.float32)
+        bound = math.sqrt(6.0 / 576.0)
+        w = rng.uniform(-bound, bound, (64, 64, 3, 3)).astype(np.float32)
+        nf = 16
+        dt = _timed(lambda: oracle.conv2d_demo(x, w, None, (1, 1), (1, 1), (1, 1, 1, 1), (8, 16, 4, 8, 9), threads=2,
+                                               f_range=(0, nf), optimized=False))
+        full = 2.0 * 32 * 64 * 56 * 56 * 64 * 9
+        out["c3"] = rec(full * nf / 64, dt, full, f"filters 0-{nf - 1} of 64 (2 of 8 outer filter tiles; "
+                        "tiles f8 c16 n4 ho8 wo9, fp32 img2col + matmul)")
+    if "c4" in keys:
+        rng = np.random.default_rng(20261205)
+        heads, rows = 8, 128
+        q, k, v = (rng.standard_normal((4, heads, 2048, 128), dtype=np.float32) for _ in range(3))
+        dt = _timed(lambda: oracle.flash_attention_demo(q, k, v, 64, 80, scale=1 / math.sqrt(128), threads=2,
+                                                        m_range=(0, rows), optimized=False))
+        full = 4.0 * 4 * 32 * 2048 * 2048 * 128
+        out["c4"] = rec(full * (heads / 32) * (rows / 2048), dt, full,
+                        f"query rows 0-{rows - 1} of {heads} of 32 heads, all 4 batches (tiles br64 bc80, fp32)")
+    for d, key, seed in ((128, "c5d128", 20261206), (64, "c5d64", 20261207)):
+        if key not in keys:
+            continue
+        rng = np.random.default_rng(seed)
+        heads, r0, r1 = 4, 8192, 8320
+        q, k, v = (rng.standard_normal((1, heads, 16384, d), dtype=np.float32) for _ in range(3))
+        dt = _timed(lambda: oracle.flash_attention_demo(q, k, v, 64, 80, scale=1 / math.sqrt(d), causal=True,
+                                                        threads=2, m_range=(r0, r1), optimized=False))
+        kept = sum(i + 1 for i in range(r0, r1))  # query-key pairs the mask keeps in the sample, per head
+        full = 4.0 * 32 * 16384 * 16384 * d / 2
+        # B = 1: the block-strided loop over batches gives one of the two threads work
+        out[key] = rec(4.0 * d * heads * kept, dt, full,
+                       f"query rows {r0}-{r1 - 1} of {heads} of 32 heads (causal: extrapolated by kept "
+                       f"query-key pairs; tiles br64 bc80, fp32; B=1 leaves one of the 2 threads idle)", cores=1)
+    return out
+
+
 def cpu_model() -> str:
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -159,6 +252,7 @@ def cpu_model() -> str:
 
 
 SECONDARY_KEYS = ("c1", "c2s", "c3", "c4", "c5d128", "c5d64", "f32gemm", "f32fa")
+PROFILE_KEYS = ("c2",) + SECONDARY_KEYS  # --only also takes the headline GEMM, for counter runs
 
 
 SECONDARY_WARMUP_S = 0.15  # untimed back-to-back launches per secondary workload, seconds
@@ -169,11 +263,12 @@ def secondary(dev, steps: int, warmup: int, only=None):
 
     out = []
     keys = set(SECONDARY_KEYS if only is None else only)
+    current = [None]
 
     def add(name, flop, call, peak, nsteps, byts=None, traffic_file=None):
         wall, ev, nwarm = time_steps(call, nsteps, min(warmup, 10), SECONDARY_WARMUP_S)
         tf = flop / (ev * 1e-3) / 1e12
-        rec = {"workload": name, "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ev, 5),
+        rec = {"key": current[0], "workload": name, "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ev, 5),
                "frac_of_peak": round(tf / peak, 4), "peak": peak, "steps": nsteps, "warmup_launches": nwarm}
         if byts is not None:
             gbs = byts / (ev * 1e-3) / 1e9
@@ -184,22 +279,14 @@ def secondary(dev, steps: int, warmup: int, only=None):
         log(f"[bench] {name}: {ev * 1e3:.1f} us  {tf:.1f} TFLOP/s  wall/step {wall * 1e3:.1f} us")
         out.append(rec)
 
-    # C1 fp32 256^3
-    if "c1" in keys:
-        c1(dev, add, steps)
-    if "c2s" in keys:
-        c2s(dev, add, steps)
-    if "c3" in keys:
-        c3(dev, add, steps)
-    if "c4" in keys:
-        c4(dev, add, steps)
-    for d, key in ((128, "c5d128"), (64, "c5d64")):
+    runs = {"c1": lambda: c1(dev, add, steps), "c2": lambda: c2(dev, add, steps), "c2s": lambda: c2s(dev, add, steps), "c3": lambda: c3(dev, add, steps),
+            "c4": lambda: c4(dev, add, steps), "c5d128": lambda: c5(dev, add, steps, 128),
+            "c5d64": lambda: c5(dev, add, steps, 64), "f32gemm": lambda: f32_gemm(dev, add, steps),
+            "f32fa": lambda: f32_fa(dev, add, steps)}
+    for key in PROFILE_KEYS:
         if key in keys:
-            c5(dev, add, steps, d)
-    if "f32gemm" in keys:
-        f32_gemm(dev, add, steps)
-    if "f32fa" in keys:
-        f32_fa(dev, add, steps)
+            current[0] = key
+            runs[key]()
     return out
 
 
@@ -212,6 +299,12 @@ def c1(dev, add, steps):
     c = torch.empty(256, 256, device=dev)
     add("C1 fp32 matmul 256^3", 2 * 256**3, PreparedCall("kg_gfx950_matmul_entry", (c, a, b, None)), PEAK_FP32_TFLOPS,
         max(steps, 200))
+
+
+def c2(dev, add, steps):
+    a, b, c = gemm_workload(dev, 4096, 4096, 4096, 20261202)
+    add("C2 bf16 matmul M=N=K=4096", 2 * 4096**3, PreparedCall("kg_gfx950_matmul_entry", (c, a, b, None)),
+        PEAK_BF16_TFLOPS, max(steps, 200))
 
 
 def c2s(dev, add, steps):
@@ -289,7 +382,7 @@ def main() -> int:
                     help="untimed launches before them (500 x ~115 us: the clock has settled)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
-    ap.add_argument("--only", nargs="+", choices=SECONDARY_KEYS,
+    ap.add_argument("--only", nargs="+", choices=PROFILE_KEYS,
                     help="profiling aid: run only these secondary workloads (no headline GEMM, no CPU baseline)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (reference point for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -369,6 +462,18 @@ def main() -> int:
         cb = cpu_baseline_matmul()
         log(f"[bench] cpu baseline: {cb['value'] * 1e3:.3f} GFLOP/s ({cb['sample']})")
         result["cpu_baseline"] = cb
+        if "secondary" in result:
+            # the fp32 extension lines share C2's and C4's loop nests: their baselines are those
+            keys = {r["key"] for r in result["secondary"]}
+            baselines = cpu_baselines(keys | ({"c4"} if "f32fa" in keys else set()))
+            baselines["f32gemm"] = dict(cb, note="the headline's sample: the same 4096^3 loop nest in fp32")
+            if "c4" in baselines:
+                baselines["f32fa"] = dict(baselines["c4"], note="C4's sample: the same loop nest in fp32")
+            for r in result["secondary"]:
+                if r["key"] in baselines:
+                    r["cpu_baseline"] = baselines[r["key"]]
+                    log(f"[bench] cpu baseline {r['key']}: {baselines[r['key']]['value'] * 1e3:.3f} GFLOP/s "
+                        f"({baselines[r['key']]['sample_s'] if 'sample_s' in baselines[r['key']] else ''} s)")
     print(json.dumps(result), flush=True)
     return 0
 

@@ -5,7 +5,7 @@
 // acc' = acc*exp(m - m_new) + P V, O = acc / l (scale 1, no mask).
 //
 // fa_fwd_simt_kernel: any dtype, any S and D <= 512; one 128-thread block per (b*h, query
-//   row), keys processed in blocks of 128 with the same online-softmax recurrence.
+//   row), on a one-dimensional grid, keys processed in blocks of 128 with the same online-softmax recurrence.
 #pragma once
 
 #include "common.h"
@@ -32,8 +32,9 @@ __global__ __launch_bounds__(128) void fa_fwd_simt_kernel(const T* __restrict__ 
   __shared__ float ps[kThreads];
   __shared__ float red[kThreads / 64];
 
-  const int row = blockIdx.x;
-  const int bh = blockIdx.y;
+  // one-dimensional grid: block b is query row b % S_q of head b / S_q
+  const int row = (int)(blockIdx.x % (unsigned)s.s_q);
+  const int bh = (int)(blockIdx.x / (unsigned)s.s_q);
   const int tid = threadIdx.x;
   const long long base_q = ((long long)bh * s.s_q + row) * s.d;
   const long long base_kv = (long long)bh * s.s_kv * s.d;

@@ -317,8 +317,10 @@ __global__ __launch_bounds__(256) void gemm_simt_kernel(const TA* __restrict__ A
   const int tid = threadIdx.x;
   const int tx = tid & 15;
   const int ty = tid >> 4;
-  const int m0 = blockIdx.y * T;
-  const int n0 = blockIdx.x * T;
+  // one-dimensional grid: block b covers tile column b % ceil(N/T), tile row b / ceil(N/T)
+  const int n_tiles = (N + T - 1) / T;
+  const int m0 = (int)(blockIdx.x / n_tiles) * T;
+  const int n0 = (int)(blockIdx.x % n_tiles) * T;
   float acc[MT][MT];
 #pragma unroll
   for (int i = 0; i < MT; ++i)

@@ -32,9 +32,12 @@ constexpr int kInvalid = -1;
 constexpr int kHipFailure = -2;
 constexpr int kUnsupported = -3;
 
+// Per-thread state: the last failure text and the launch mode. Two host threads calling
+// the entries concurrently (ctypes releases the GIL) each keep their own mode and stream,
+// so a synchronous caller never has its kernel moved onto another thread's stream.
 thread_local char g_last_error[512] = "";
-bool g_synchronous = true;
-hipStream_t g_stream = nullptr;
+thread_local bool g_synchronous = true;
+thread_local hipStream_t g_stream = nullptr;
 
 int fail(int code, const char* fmt, ...) {
   va_list ap;
@@ -211,8 +214,10 @@ int launch_gemm_simt(const Mem& out, const Mem& lhs, const Mem& rhs, const Mem& 
   auto blocks = [&](int t) { return (long long)((N + t - 1) / t) * ((M + t - 1) / t); };
   // the largest tile that still gives every CU a block (256-thread blocks of T x T outputs)
   const int t = blocks(64) >= 256 ? 64 : blocks(32) >= 256 ? 32 : 16;
+  // one-dimensional grid (gridDim.y is limited to 65535; x to 2^31 - 1)
+  if (blocks(t) > 0x7fffffffLL) return fail(kUnsupported, "matmul(simt): %lld tiles exceed the grid limit", blocks(t));
 #define KG_GEMM_SIMT(T)                                                                                          \
-  hipLaunchKernelGGL((gemm_simt_kernel<TA, TA, TA, TBias, T>), dim3((N + T - 1) / T, (M + T - 1) / T), dim3(256), 0, \
+  hipLaunchKernelGGL((gemm_simt_kernel<TA, TA, TA, TBias, T>), dim3((unsigned)blocks(T)), dim3(256), 0, \
                      g_stream, static_cast<const TA*>(lhs.data), static_cast<const TA*>(rhs.data),                   \
                      static_cast<TA*>(out.data), static_cast<const TBias*>(bias.present ? bias.data : nullptr), M, N, \
                      K, lhs.stride[0], lhs.stride[1], rhs.stride[0], rhs.stride[1], out.stride[0], out.stride[1],   \
@@ -460,9 +465,12 @@ int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
   s.pt = (int)p[4];
   s.pl = (int)p[6];
   if (w.shape[1] != x.shape[1]) return fail(kInvalid, "conv2d: weight C=%lld != input C=%lld", w.shape[1], x.shape[1]);
-  const long long ho = (x.shape[2] + p[4] + p[5] - p[2] * (w.shape[2] - 1) - 1) / p[0] + 1;
-  const long long wo = (x.shape[3] + p[6] + p[7] - p[3] * (w.shape[3] - 1) - 1) / p[1] + 1;
-  if (ho <= 0 || wo <= 0) return fail(kInvalid, "conv2d: empty output window (Ho=%lld, Wo=%lld)", ho, wo);
+  // Ho/Wo with floor division, as the demos compute them (kernel/conv2d/inputs_static_tile_static.py:
+  // 155-156, Python //): a window larger than the padded input gives an empty output
+  // (Ho or Wo = 0), never a row built from outside the input.
+  auto floor_div = [](long long a, long long b) { return a >= 0 ? a / b : -((-a + b - 1) / b); };
+  const long long ho = std::max(0LL, floor_div(x.shape[2] + p[4] + p[5] - p[2] * (w.shape[2] - 1) - 1, p[0]) + 1);
+  const long long wo = std::max(0LL, floor_div(x.shape[3] + p[6] + p[7] - p[3] * (w.shape[3] - 1) - 1, p[1]) + 1);
   s.ho = (int)ho;
   s.wo = (int)wo;
   if (out.shape[0] != x.shape[0] || out.shape[1] != w.shape[0] || out.shape[2] != ho || out.shape[3] != wo)
@@ -542,8 +550,10 @@ int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
 
 template <typename T>
 int launch_fa_simt(const Mem& out, const Mem& q, const Mem& k, const Mem& v, const FaShape& s) {
-  dim3 grid(s.s_q, s.bh);
-  hipLaunchKernelGGL((fa_fwd_simt_kernel<T>), grid, dim3(128), 0, g_stream, static_cast<const T*>(q.data),
+  // one block per (b*h, query row) on a one-dimensional grid (gridDim.y is limited to 65535)
+  const long long blocks = (long long)s.s_q * s.bh;
+  if (blocks > 0x7fffffffLL) return fail(kUnsupported, "flash_attention(simt): %lld query rows exceed the grid limit", blocks);
+  hipLaunchKernelGGL((fa_fwd_simt_kernel<T>), dim3((unsigned)blocks), dim3(128), 0, g_stream, static_cast<const T*>(q.data),
                      static_cast<const T*>(k.data), static_cast<const T*>(v.data), static_cast<T*>(out.data), s);
   return finish_launch("flash_attention(simt)");
 }

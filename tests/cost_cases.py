@@ -1,7 +1,7 @@
 """Run each cost-model case once on the GPU and print the modelled costs, so a hardware
 counter run can be laid beside the model:
 
-    rocprofv3 --pmc SQ_INSTS_MFMA -d <dir> -- python3 -m kernelcode_generate_amd.tools.cost_cases
+    rocprofv3 --pmc SQ_INSTS_MFMA -d <dir> -- python3 -m tests.cost_cases
 
 Every case makes exactly one library kernel dispatch, in the order printed, and nothing
 else dispatches a kernel (inputs are generated on the host and copied), so dispatch i of the
@@ -18,7 +18,7 @@ import argparse
 import json
 import sys
 
-from .. import native
+from kernelcode_generate_amd import native
 
 # (name, family, dtype, shapes, scalars): shapes are (out, in0, in1[, in2]) in the slot
 # order of the family's entry; bias is always absent.

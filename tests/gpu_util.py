@@ -48,3 +48,55 @@ def round_to(x: np.ndarray, torch_dtype):
 
     t = torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(torch_dtype)
     return t, t.float().numpy()
+
+
+def attention_f32_tolerance(q, k, v, scale=None, causal=False) -> np.ndarray:
+    """Per-element fp32 attention bar for kernels whose sums run in another order than the
+    oracle's sequential loops (MFMA dot products, exp2, tiled online softmax).
+
+    |out - oracle| <= 1e-5 + 1e-4 |oracle| (the north-star fp32 bar) plus first-order
+    rounding terms, all from float64 quantities of the inputs (Higham & Mary's probabilistic
+    bound 4 sqrt(n) 2^-24 for an n-term fp32 sum in any order):
+      - a score s_ij = scale * sum_d q_id k_jd off by e_ij moves O_i by at most
+        max_j e_ij * (P |V - O|)_i, with e_ij = 4 sqrt(D) 2^-24 scale (|Q| |K|^T)_ij plus
+        the exp argument's rounding, |s_ij - m_i| * log2(e) * 2^-24 + 2^-22 (exp2 and its
+        result each within an ulp);
+      - the P V sum over S_kv keys in any order: 4 sqrt(S_kv) 2^-24 (P |V|)_i / 1.
+    q, k, v: float arrays [..., S, D]; returns the atol array for the output shape."""
+
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    s_q, d = q.shape[-2], q.shape[-1]
+    s_kv = k.shape[-2]
+    sc = 1.0 if scale is None else float(scale)
+    s = sc * (q @ np.swapaxes(k, -1, -2))
+    if causal:
+        mask = np.tril(np.ones((s_q, s_kv), bool))
+        s = np.where(mask, s, -np.inf)
+    m = s.max(-1, keepdims=True)
+    p = np.exp(s - m)
+    p /= p.sum(-1, keepdims=True)
+    o = p @ v
+    dots = sc * (np.abs(q) @ np.swapaxes(np.abs(k), -1, -2))
+    arg = np.where(np.isfinite(s), np.abs(s - m), 0.0) * 1.4426950408889634
+    e = 4 * np.sqrt(d) * 2.0 ** -24 * dots + arg * 2.0 ** -24 + 2.0 ** -22
+    if causal:
+        e = np.where(mask, e, 0.0)
+    e_max = e.max(-1, keepdims=True)
+    dev = p @ np.abs(v) + np.abs(o)  # bounds (P |V - O|)_i elementwise
+    return 1e-5 + 1e-4 * np.abs(o) + e_max * dev + 4 * np.sqrt(s_kv) * 2.0 ** -24 * (p @ np.abs(v))
+
+
+def assert_within(out, ref, atol, what: str = "") -> None:
+    """|out - ref| <= atol elementwise (atol an array from a documented error bound)."""
+
+    out = np.asarray(out, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert out.shape == ref.shape, (out.shape, ref.shape)
+    err = np.abs(out - ref)
+    bad = ~(err <= atol)
+    if bad.any():
+        worst = np.unravel_index(np.argmax(np.where(bad, err / np.maximum(atol, 1e-30), 0)), err.shape)
+        raise AssertionError(f"{what}: {int(bad.sum())} of {bad.size} outside the bound; worst err {err[worst]:.3e} "
+                             f"> {np.broadcast_to(atol, err.shape)[worst]:.3e} at {worst}")

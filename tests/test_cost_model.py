@@ -7,7 +7,7 @@ MAC and byte counts are pinned by brute force (an oracle run gives the output sh
 mask count gives the causal pairs); MFMA counts are pinned by the MAC content of one
 32x32x16 MFMA (16384 MACs) on exact-tile shapes, and by the hardware counter
 SQ_INSTS_MFMA on every kernel choice (profiles/mfma_instruction_counts.txt, made by
-kernelcode_generate_amd/tools/cost_cases.py under rocprofv3 --pmc).
+tests/cost_cases.py under rocprofv3 --pmc).
 """
 
 from __future__ import annotations
@@ -33,7 +33,7 @@ from kernelcode_generate_amd.kernel.flash_attention.scaled import (
 from kernelcode_generate_amd.kernel.matmul.inputs_dynamic_tile_dynamic import matmul_inputs_dynamic_tile_dynamic_kernel
 from kernelcode_generate_amd.kernel.matmul.inputs_static_tile_static import matmul_inputs_static_tile_static_kernel
 from kernelcode_generate_amd.tools import VALID_DSL_COST_KINDS, dsl_cost_run
-from kernelcode_generate_amd.tools.cost_cases import CASES, modelled
+from tests.cost_cases import CASES, modelled
 
 T = native.TensorSpec
 PIPE = "gfx950-lowering"

@@ -211,17 +211,25 @@ def test_f32_matrix_core_shapes(device, oracle_mod, shape, rows, with_bias):
 
 @pytest.mark.parametrize(
     "shape,with_bias,strided",
-    [((256, 256, 256), True, False), ((64, 96, 4096), False, False), ((512, 512, 4096), True, True)],
+    [((256, 256, 256), True, False), ((64, 4096, 96), False, False), ((512, 4096, 512), True, True)],
     ids=["c1_bias", "k_heavy", "strided_lhs"],
 )
 def test_f32_split_k(device, oracle_mod, shape, with_bias, strided):
     """Small fp32 outputs with 32-aligned extents: one workgroup per 32 x 32 block sums K
-    across its 16 waves (MFMA 32x32x2) and reduces the partial blocks in LDS. Tolerance as in
-    test_f32_matrix_core_shapes: the demo's rtol/atol plus 4 sqrt(K) 2^-24 (|A| |B|)."""
+    across its 16 waves (MFMA 32x32x2) and reduces the partial blocks in LDS. Shapes are
+    (M, K, N): K = 4096 runs 16 slices per wave (the multi-slice loop), and the strided case
+    has lhs row stride K + 8. Tolerance as in test_f32_matrix_core_shapes: the demo's
+    rtol/atol plus 4 sqrt(K) 2^-24 (|A| |B|)."""
 
     import torch
 
     m, k, n = shape
+    # the entry must route the shape to the split-K kernel (fewer than 32 tiles of 128 x 128
+    # keep it off the fp32 MFMA GEMM): its cost record is the split-K MFMA count
+    spec = [native.TensorSpec((m, n), "float32"), native.TensorSpec((m, k), "float32", (k + 8 if strided else k, 1)),
+            native.TensorSpec((k, n), "float32"), native.TensorSpec((n,), "float32") if with_bias else None]
+    assert ((m + 127) // 128) * ((n + 127) // 128) < 32
+    assert native.cost("matmul", spec)["MFMA"] == (m // 32) * (n // 32) * (k // 16) * 8
     rng = np.random.default_rng(m + k + n)
     lhs = rng.uniform(-1, 1, (m, k)).astype(np.float32)
     rhs = rng.uniform(-1, 1, (k, n)).astype(np.float32)
