@@ -1,0 +1,377 @@
+/*
+ * gfx950/kg_tile.h - device runtime of the per-operation gfx950 emitter.
+ *
+ * The reference renders every operation of a final IR as a call into its target's
+ * runtime headers (include/npu_demo/{Kernel,Dma}.h for the host, include/cuda_sm89/*.h
+ * for its GPU sibling, where one thread of one block runs the whole body:
+ * kernel_gen/dsl/gen_kernel/emit/cuda_sm89/source_bundle.py:615-620). This header is the
+ * gfx950 counterpart used by kernels that the pattern pass does not map onto a
+ * hand-written kernel: each workgroup runs one iteration of the kernel's parallel outer
+ * loops at a time, and every operation is executed cooperatively by the workgroup's
+ * threads on strided views of global memory (arguments and the workgroup's slice of a
+ * scratch workspace), followed by a workgroup barrier.
+ *
+ * Arithmetic follows the reference's npu_demo primitives, so results match the host
+ * execution bit for bit where the reference's own arithmetic is deterministic:
+ *   matmul    sequential k, each product rounded to float before it is added
+ *             (include/npu_demo/Kernel.h:900-948), acc = keep the output's value;
+ *   exp       (float)exp((double)x)                               (Kernel.h:621-641);
+ *   reduce    max from element 0 with `v > cur`, sum from 0 ascending (Kernel.h:701-881);
+ *   truediv   (float)((double)a / (double)b); max `a > b ? a : b` (Kernel.h:348-443);
+ *   img2col2d out[n,c,kh,kw,ho,wo] = in[n,c,ho*sh+kh*dh-ph, wo*sw+kw*dw-pl] or 0
+ *             (Kernel.h:1041-1123; ph/pw are the top/bottom pads, pl/pr left/right).
+ *
+ * Every view an operation touches is checked against the memory it belongs to; a
+ * violation sets the error word (and the operation is skipped), which the generated
+ * entry reports as a failed call instead of reading or writing out of bounds.
+ */
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kg_tile {
+
+constexpr int kThreads = 256;
+
+// ---- elements -------------------------------------------------------------------------
+struct Bf16 {
+  uint16_t bits;
+};
+
+__device__ __forceinline__ float ld(const float* p) { return *p; }
+__device__ __forceinline__ float ld(const _Float16* p) { return (float)*p; }
+__device__ __forceinline__ float ld(const Bf16* p) { return __builtin_bit_cast(float, (uint32_t)p->bits << 16); }
+__device__ __forceinline__ void st(float* p, float v) { *p = v; }
+__device__ __forceinline__ void st(_Float16* p, float v) { *p = (_Float16)v; }
+__device__ __forceinline__ void st(Bf16* p, float v) {
+  uint32_t u = __builtin_bit_cast(uint32_t, v);
+  if ((u & 0x7fffffffu) > 0x7f800000u) {
+    p->bits = (uint16_t)((u >> 16) | 0x40u);  // NaN stays NaN
+    return;
+  }
+  u += 0x7fffu + ((u >> 16) & 1u);  // round to nearest even
+  p->bits = (uint16_t)(u >> 16);
+}
+
+// ---- integer helpers (Python semantics for // and %) ------------------------------------
+__host__ __device__ __forceinline__ long long kg_min(long long a, long long b) { return a < b ? a : b; }
+__host__ __device__ __forceinline__ long long kg_max(long long a, long long b) { return a > b ? a : b; }
+__host__ __device__ __forceinline__ long long kg_floordiv(long long a, long long b) {
+  if (b == 0) return 0;  // never reached: divisors are checked positive before launch
+  long long q = a / b;
+  if ((a % b != 0) && ((a < 0) != (b < 0))) --q;
+  return q;
+}
+__host__ __device__ __forceinline__ long long kg_mod(long long a, long long b) {
+  if (b == 0) return 0;
+  return a - kg_floordiv(a, b) * b;
+}
+__host__ __device__ __forceinline__ long long kg_trips(long long start, long long end, long long step) {
+  return (step <= 0 || end <= start) ? 0 : (end - start + step - 1) / step;
+}
+
+// ---- views ------------------------------------------------------------------------------
+template <typename T, int R>
+struct View {
+  T* p;
+  long long shape[R];
+  long long stride[R];
+};
+
+template <typename T, int R>
+__device__ __forceinline__ long long numel(const View<T, R>& v) {
+  long long n = 1;
+#pragma unroll
+  for (int d = 0; d < R; ++d) n *= v.shape[d] > 0 ? v.shape[d] : 0;
+  return n;
+}
+
+// element offset of the i-th element (row-major order over the view's shape)
+template <typename T, int R>
+__device__ __forceinline__ long long offset_of(const View<T, R>& v, long long i) {
+  long long off = 0;
+#pragma unroll
+  for (int d = R - 1; d >= 0; --d) {
+    const long long e = v.shape[d];
+    off += (i % e) * v.stride[d];
+    i /= e;
+  }
+  return off;
+}
+
+// A tile of the workspace: contiguous row-major.
+template <typename T, int R>
+__device__ __forceinline__ View<T, R> tile(char* base, const long long (&shape)[R]) {
+  View<T, R> v;
+  v.p = reinterpret_cast<T*>(base);
+  long long s = 1;
+#pragma unroll
+  for (int d = R - 1; d >= 0; --d) {
+    v.shape[d] = shape[d] > 0 ? shape[d] : 0;
+    v.stride[d] = s;
+    s *= v.shape[d] > 0 ? v.shape[d] : 1;
+  }
+  return v;
+}
+
+// Sub-view at offsets / sizes / steps; sets the error word (and returns an empty view)
+// when the region leaves the source.
+template <typename T, int R>
+__device__ __forceinline__ View<T, R> subview(const View<T, R>& src, const long long (&off)[R],
+                                              const long long (&size)[R], const long long (&step)[R], int* err) {
+  View<T, R> v;
+  bool ok = true, empty = false;
+  long long base = 0;
+#pragma unroll
+  for (int d = 0; d < R; ++d) {
+    if (size[d] < 0 || step[d] <= 0) ok = false;
+    if (size[d] == 0) empty = true;
+  }
+#pragma unroll
+  for (int d = 0; d < R; ++d) {
+    if (!empty && (off[d] < 0 || off[d] + (size[d] - 1) * step[d] >= src.shape[d])) ok = false;
+    base += off[d] * src.stride[d];
+    v.shape[d] = size[d] > 0 ? size[d] : 0;
+    v.stride[d] = src.stride[d] * step[d];
+  }
+  if (!ok) {
+    if (threadIdx.x == 0) atomicOr(err, 1);
+#pragma unroll
+    for (int d = 0; d < R; ++d) v.shape[d] = 0;
+    base = 0;
+  }
+  v.p = src.p + (empty ? 0 : base);
+  return v;
+}
+
+// Reshape of a row-major contiguous view (the error word is set otherwise, or when the
+// element counts differ).
+template <int RO, typename T, int R>
+__device__ __forceinline__ View<T, RO> reshape(const View<T, R>& src, const long long (&shape)[RO], int* err) {
+  bool ok = true;
+  long long s = 1;
+#pragma unroll
+  for (int d = R - 1; d >= 0; --d) {
+    if (src.shape[d] != 1 && src.stride[d] != s) ok = false;
+    s *= src.shape[d];
+  }
+  long long n = 1;
+#pragma unroll
+  for (int d = 0; d < RO; ++d) n *= shape[d] > 0 ? shape[d] : 0;
+  if (n != numel(src)) ok = false;
+  View<T, RO> v = tile<T, RO>(reinterpret_cast<char*>(src.p), shape);
+  if (!ok) {
+    if (threadIdx.x == 0) atomicOr(err, 2);
+#pragma unroll
+    for (int d = 0; d < RO; ++d) v.shape[d] = 0;
+  }
+  return v;
+}
+
+__device__ __forceinline__ void sync() { __syncthreads(); }
+
+// ---- dma ----------------------------------------------------------------------------------
+template <typename T, int R>
+__device__ void fill(const View<T, R>& t, float value) {
+  const long long n = numel(t);
+  for (long long i = threadIdx.x; i < n; i += kThreads) st(t.p + offset_of(t, i), value);
+  sync();
+}
+
+// dst <- src element by element in row-major order (deslice / slice after their region
+// views are formed); the element counts must agree.
+template <typename TD, int RD, typename TS, int RS>
+__device__ void copy(const View<TD, RD>& dst, const View<TS, RS>& src, int* err) {
+  const long long n = numel(dst);
+  if (n != numel(src)) {
+    if (threadIdx.x == 0 && n > 0) atomicOr(err, 4);
+    sync();
+    return;
+  }
+  for (long long i = threadIdx.x; i < n; i += kThreads) st(dst.p + offset_of(dst, i), ld(src.p + offset_of(src, i)));
+  sync();
+}
+
+// dst <- src expanded along its size-1 axes (trailing axes aligned, numpy rules).
+template <typename TD, int RD, typename TS, int RS>
+__device__ void broadcast(const View<TD, RD>& dst, const View<TS, RS>& src, int* err) {
+  static_assert(RS <= RD, "broadcast source rank");
+  bool ok = true;
+#pragma unroll
+  for (int d = 0; d < RS; ++d) {
+    const long long sd = src.shape[d], dd = dst.shape[RD - RS + d];
+    if (sd != 1 && sd != dd) ok = false;
+  }
+  if (!ok) {
+    if (threadIdx.x == 0) atomicOr(err, 8);
+    sync();
+    return;
+  }
+  const long long n = numel(dst);
+  for (long long i = threadIdx.x; i < n; i += kThreads) {
+    long long rem = i, so = 0, doff = 0;
+#pragma unroll
+    for (int d = RD - 1; d >= 0; --d) {
+      const long long idx = rem % dst.shape[d];
+      rem /= dst.shape[d];
+      doff += idx * dst.stride[d];
+      const int s = d - (RD - RS);
+      if (s >= 0 && src.shape[s] != 1) so += idx * src.stride[s];
+    }
+    st(dst.p + doff, ld(src.p + so));
+  }
+  sync();
+}
+
+// dst[i_0..i_{R-1}] = src[j] with j[perm[d]] = i_d.
+template <typename TD, typename TS, int R>
+__device__ void transpose(const View<TD, R>& dst, const View<TS, R>& src, const int (&perm)[R], int* err) {
+  bool ok = true;
+#pragma unroll
+  for (int d = 0; d < R; ++d)
+    if (dst.shape[d] != src.shape[perm[d]]) ok = false;
+  if (!ok) {
+    if (threadIdx.x == 0) atomicOr(err, 16);
+    sync();
+    return;
+  }
+  const long long n = numel(dst);
+  for (long long i = threadIdx.x; i < n; i += kThreads) {
+    long long rem = i, so = 0, doff = 0;
+#pragma unroll
+    for (int d = R - 1; d >= 0; --d) {
+      const long long idx = rem % dst.shape[d];
+      rem /= dst.shape[d];
+      doff += idx * dst.stride[d];
+      so += idx * src.stride[perm[d]];
+    }
+    st(dst.p + doff, ld(src.p + so));
+  }
+  sync();
+}
+
+// ---- kernel -------------------------------------------------------------------------------
+template <typename TO, typename TL, typename TR>
+__device__ void matmul(const View<TO, 2>& out, const View<TL, 2>& lhs, const View<TR, 2>& rhs, bool acc, int* err) {
+  const long long M = out.shape[0], N = out.shape[1], K = lhs.shape[1];
+  if (lhs.shape[0] != M || rhs.shape[0] != K || rhs.shape[1] != N) {
+    if (threadIdx.x == 0) atomicOr(err, 32);
+    sync();
+    return;
+  }
+  for (long long e = threadIdx.x; e < M * N; e += kThreads) {
+    const long long m = e / N, n = e % N;
+    TO* o = out.p + m * out.stride[0] + n * out.stride[1];
+    float a = acc ? ld(o) : 0.0f;
+    const TL* l = lhs.p + m * lhs.stride[0];
+    const TR* r = rhs.p + n * rhs.stride[1];
+    for (long long k = 0; k < K; ++k)
+      a = __fadd_rn(a, __fmul_rn(ld(l + k * lhs.stride[1]), ld(r + k * rhs.stride[0])));
+    st(o, a);
+  }
+  sync();
+}
+
+template <typename TO, typename TI>
+__device__ void img2col2d(const View<TO, 6>& out, const View<TI, 4>& in, long long kh, long long kw, long long sh,
+                          long long sw, long long dh, long long dw, long long ph, long long pw, long long pl,
+                          long long pr, int* err) {
+  const long long H = in.shape[2], W = in.shape[3];
+  const long long ho = kg_floordiv(H + ph + pw - dh * (kh - 1) - 1, sh) + 1;
+  const long long wo = kg_floordiv(W + pl + pr - dw * (kw - 1) - 1, sw) + 1;
+  if (out.shape[0] != in.shape[0] || out.shape[1] != in.shape[1] || out.shape[2] != kh || out.shape[3] != kw ||
+      out.shape[4] != (ho > 0 ? ho : 0) || out.shape[5] != (wo > 0 ? wo : 0) || sh <= 0 || sw <= 0) {
+    if (threadIdx.x == 0) atomicOr(err, 64);
+    sync();
+    return;
+  }
+  const long long n = numel(out);
+  for (long long i = threadIdx.x; i < n; i += kThreads) {
+    long long rem = i;
+    const long long x = rem % out.shape[5]; rem /= out.shape[5];
+    const long long y = rem % out.shape[4]; rem /= out.shape[4];
+    const long long q = rem % kw; rem /= kw;
+    const long long r = rem % kh; rem /= kh;
+    const long long c = rem % out.shape[1]; rem /= out.shape[1];
+    const long long b = rem;
+    const long long sy = y * sh + r * dh - ph, sx = x * sw + q * dw - pl;
+    float v = 0.0f;
+    if (sy >= 0 && sy < H && sx >= 0 && sx < W)
+      v = ld(in.p + b * in.stride[0] + c * in.stride[1] + sy * in.stride[2] + sx * in.stride[3]);
+    st(out.p + offset_of(out, i), v);
+  }
+  sync();
+}
+
+template <typename TO, int R, typename TI>
+__device__ void exp(const View<TO, R>& out, const View<TI, R>& in, int* err) {
+  const long long n = numel(out);
+  if (n != numel(in)) {
+    if (threadIdx.x == 0 && n > 0) atomicOr(err, 128);
+    sync();
+    return;
+  }
+  for (long long i = threadIdx.x; i < n; i += kThreads)
+    st(out.p + offset_of(out, i), (float)::exp((double)ld(in.p + offset_of(in, i))));
+  sync();
+}
+
+// kind 0 = max, 1 = sum; rows of a rank-2 input into out[rows, 1]
+template <typename TO, typename TI>
+__device__ void reduce_rows(const View<TO, 2>& out, const View<TI, 2>& in, int kind, int* err) {
+  const long long rows = in.shape[0], cols = in.shape[1];
+  if (out.shape[0] != rows || out.shape[1] != 1) {
+    if (threadIdx.x == 0) atomicOr(err, 256);
+    sync();
+    return;
+  }
+  for (long long i = threadIdx.x; i < rows; i += kThreads) {
+    const TI* row = in.p + i * in.stride[0];
+    float a;
+    if (kind == 0) {
+      a = cols > 0 ? ld(row) : -__builtin_inff();
+      for (long long j = 1; j < cols; ++j) {
+        const float v = ld(row + j * in.stride[1]);
+        a = v > a ? v : a;
+      }
+    } else {
+      a = 0.0f;
+      for (long long j = 0; j < cols; ++j) a = __fadd_rn(a, ld(row + j * in.stride[1]));
+    }
+    st(out.p + i * out.stride[0], a);
+  }
+  sync();
+}
+
+// kind 0 add, 1 sub, 2 mul, 3 truediv, 4 max; same shapes
+template <typename TO, typename TL, typename TR, int R>
+__device__ void binary(const View<TO, R>& out, const View<TL, R>& lhs, const View<TR, R>& rhs, int kind, int* err) {
+  bool ok = true;
+#pragma unroll
+  for (int d = 0; d < R; ++d)
+    if (lhs.shape[d] != out.shape[d] || rhs.shape[d] != out.shape[d]) ok = false;
+  if (!ok) {
+    if (threadIdx.x == 0) atomicOr(err, 512);
+    sync();
+    return;
+  }
+  const long long n = numel(out);
+  // every thread reads its elements before any is written (out may alias an operand)
+  for (long long i = threadIdx.x; i < n; i += kThreads) {
+    const float a = ld(lhs.p + offset_of(lhs, i));
+    const float b = ld(rhs.p + offset_of(rhs, i));
+    float r;
+    switch (kind) {
+      case 0: r = __fadd_rn(a, b); break;
+      case 1: r = __fsub_rn(a, b); break;
+      case 2: r = __fmul_rn(a, b); break;
+      case 3: r = (float)((double)a / (double)b); break;
+      default: r = a > b ? a : b; break;
+    }
+    st(out.p + offset_of(out, i), r);
+  }
+  sync();
+}
+
+}  // namespace kg_tile

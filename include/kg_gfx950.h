@@ -110,6 +110,29 @@ int kg_gfx950_flash_attention_entry(const KgArgSlot* ordered_args, unsigned long
  */
 int kg_gfx950_set_launch_mode(int synchronous, void* stream);
 
+/*
+ * Support for generated entries (no counterpart in the reference, whose generated sources
+ * include their runtime headers; here the runtime is this library). A generated
+ * kg_execute_entry (the gfx950 emitter's kernel.hip) validates its slots, launches on the
+ * calling thread's stream and reports failures through these, so the execute engine
+ * reads one error text per thread whichever code failed.
+ *
+ * kg_gfx950_fail: records `message` as the calling thread's last error; returns `code`.
+ * kg_gfx950_check_memory_slot: slot `index` must be a memory slot of rank `rank` holding
+ *   a device pointer whose strided view fits its allocation (the entries' own check);
+ *   allow_absent != 0 accepts data == NULL; dtype_code != 0 must equal the slot's. 0 or -1.
+ * kg_gfx950_launch_stream / kg_gfx950_launch_synchronous: the calling thread's launch mode
+ *   (kg_gfx950_set_launch_mode).
+ * kg_gfx950_finish_launch: checks the last launch and, in synchronous mode, waits for the
+ *   stream; 0, or -2 with the HIP error recorded.
+ */
+int kg_gfx950_fail(int code, const char* message);
+int kg_gfx950_check_memory_slot(const KgArgSlot* slots, int index, int rank, int allow_absent, int dtype_code,
+                                const char* name);
+void* kg_gfx950_launch_stream(void);
+int kg_gfx950_launch_synchronous(void);
+int kg_gfx950_finish_launch(const char* what);
+
 /* Text of the last failure on the calling thread ("" if none). */
 const char* kg_gfx950_last_error(void);
 

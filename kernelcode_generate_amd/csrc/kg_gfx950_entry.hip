@@ -683,6 +683,26 @@ int kg_gfx950_flash_attention_entry(const KgArgSlot* ordered_args, unsigned long
   return flash_attention_impl(ordered_args, arg_count);
 }
 
+int kg_gfx950_fail(int code, const char* message) { return fail(code, "%s", message ? message : ""); }
+
+int kg_gfx950_check_memory_slot(const KgArgSlot* slots, int index, int rank, int allow_absent, int dtype_code,
+                                const char* name) {
+  if (slots == nullptr) return fail(kInvalid, "ordered_args is null");
+  Mem m;
+  int rc = read_mem(slots, index, rank, allow_absent != 0, name ? name : "memory", &m);
+  if (rc != kOk) return rc;
+  if (m.present && dtype_code != 0 && m.dtype != dtype_code)
+    return fail(kInvalid, "slot %d (%s): dtype %s, the kernel was generated for %s", index, name ? name : "memory",
+                dtype_name(m.dtype), dtype_name(dtype_code));
+  return kOk;
+}
+
+void* kg_gfx950_launch_stream(void) { return g_stream; }
+
+int kg_gfx950_launch_synchronous(void) { return g_synchronous ? 1 : 0; }
+
+int kg_gfx950_finish_launch(const char* what) { return finish_launch(what ? what : "kernel"); }
+
 int kg_gfx950_set_launch_mode(int synchronous, void* stream) {
   g_synchronous = synchronous != 0;
   g_stream = static_cast<hipStream_t>(stream);

@@ -1,256 +1,159 @@
-"""gfx950 source generation for the three hot-path patterns.
+"""gfx950 source generation: lowered kernel IR -> SourceBundle.
 
-The reference's emitter walks the lowered IR of a DSL kernel and writes target source
+The reference's emitter walks a lowered module and writes target source
 (kernel_gen/dsl/gen_kernel/gen_kernel.py:150-180; per-target packages registered through
-``@emit_c_impl(ModuleOp, target=...)``, emit/register.py:187-215, 356). The gfx950 backend
-recognises the three loop nests the demos lower to -- the K-loop ``kernel.matmul`` with
-optional rank-1 bias, the ``img2col2d -> matmul -> transpose -> add`` conv nest, and the
-online-softmax flash-attention nest -- and emits a SourceBundle whose ``kernel.hip``
-defines the reference's entry ``extern "C" int kg_execute_entry(const _ArgSlot*, u64)``
-as a call into the hand-written CDNA4 kernels of libkg_gfx950.so, appending the constants
-the static demos bake into their bodies (tiles, strides, pads).
+``@emit_c_impl(ModuleOp, target=...)``, emit/register.py:187-215, 356) and, for its GPU
+target, a SourceBundle of files introduced by ``// __KG_BUNDLE_FILE__:<path>`` lines
+(emit/register.py:69). The gfx950 emitter writes a bundle whose ``kernel.hip`` defines the
+reference's entry ``extern "C" int kg_execute_entry(const _ArgSlot*, u64)`` in one of two
+forms:
 
-A ``KernelPattern`` is the recognised form of one DSL kernel: its family, parameter
-order, the constants baked into it and which argument may be absent. Patterns are
-registered per DSL function name (the nine demos of kernel/{matmul,conv2d,flash_attention}
-plus the scaled / causal flash-attention variants the BASELINE configs need).
+  - fused: kernel-pattern-fuse recognised the loop nest, and the entry forwards the
+    kernel's own slots to the hand-written CDNA4 kernel's entry of libkg_gfx950.so, with
+    the integer and float operands the nest implies (strides, pads, tiles, scale, causal)
+    computed from the slots at run time;
+  - per-operation: every other kernel, emitted by gen_kernel.per_op as one HIP kernel
+    that executes the IR operation by operation on the workgroups of the GPU.
+
+Both carry the reference's ``// kg.allow_absent_memory_args:`` metadata for memory
+parameters that may be absent (runtime_args.py:497-516).
 """
 
 from __future__ import annotations
 
 import hashlib
-from dataclasses import dataclass, field
-from typing import Callable, Sequence
+import math
 
 from ..core.error import ErrorKind, ErrorModule, KernelCodeError
+from ..ir import FVal, Func, Sym, format_func
+from ..passes import FusedCall
+from .per_op import emit_per_op
 
 BUNDLE_MARKER_PREFIX = "// __KG_BUNDLE_FILE__:"
 ENTRY_POINT = "kg_execute_entry"
 LIBRARY_ENTRY = {
-    "matmul": ("kg_gfx950_matmul_entry", (4, 7, 8)),
-    "conv2d": ("kg_gfx950_conv2d_entry", (12, 17)),
-    "flash_attention": ("kg_gfx950_flash_attention_entry", (4, 6, 8)),
+    "matmul": "kg_gfx950_matmul_entry",
+    "conv2d": "kg_gfx950_conv2d_entry",
+    "flash_attention": "kg_gfx950_flash_attention_entry",
 }
-
-
-@dataclass(frozen=True)
-class KernelPattern:
-    family: str                                  # matmul | conv2d | flash_attention
-    function: str                                # DSL function name
-    params: tuple[str, ...]                      # DSL parameter order = slot order
-    baked: tuple[tuple[str, int | float], ...]   # constants inserted after slot `insert_at`
-    insert_at: int                               # index where baked constants go
-    trailing: tuple[tuple[str, int | float], ...] = ()  # constants appended at the end
-    absent_index: int | None = None              # optional memory arg (bias)
-    absent_rank: int = 1
-    dtype: str = "float32"
-    notes: tuple[str, ...] = field(default_factory=tuple)
-
-    @property
-    def library_entry(self) -> str:
-        return LIBRARY_ENTRY[self.family][0]
-
-    @property
-    def forwarded_count(self) -> int:
-        return len(self.params) + len(self.baked) + len(self.trailing)
+_DTYPE_NAMES = {"f32": "float32", "f16": "float16", "bf16": "bfloat16"}
 
 
 def _error(message: str) -> KernelCodeError:
     return KernelCodeError(ErrorKind.CONTRACT, ErrorModule.GEN_KERNEL, message)
 
 
-def _c_literal(value: int | float) -> tuple[str, str]:
-    if isinstance(value, bool) or isinstance(value, int):
-        return "KG_ARG_INT", f"{int(value)}LL"
-    return "KG_ARG_FLOAT", repr(float(value))
+def library_slots(call: FusedCall, memory_stage: int | None = None) -> list:
+    """The library entry's slot list as (kind, value): ("mem", param | None), ("int", Sym),
+    ("float", FVal). Matmul calls carry the loop tiles only when a memory_stage slot
+    follows (the entry's 8-slot form)."""
+
+    slots: list = [("mem", name) for name in call.memory]
+    if call.family == "matmul" and memory_stage is not None:
+        tiles = call.ints if call.ints else (Sym.const(1),) * 3
+        slots += [("int", t) for t in tiles] + [("int", Sym.const(memory_stage))]
+    elif call.family != "matmul":
+        slots += [("int", e) for e in call.ints]
+        slots += [("float", v) for v in call.floats]
+        slots += [("int", e) for e in call.trailing_ints]
+    return slots
 
 
-def gen_kernel(pattern: KernelPattern) -> str:
-    """SourceBundle text for one recognised kernel pattern."""
+def _header(func: Func, kind: str, notes: list[str]) -> list[str]:
+    digest = hashlib.sha256(format_func(func).encode()).hexdigest()[:16]
+    lines = [f"{BUNDLE_MARKER_PREFIX}kernel.hip", f"// kg.gfx950.kernel: {func.name}", f"// kg.gfx950.path: {kind}",
+             f"// kg.gfx950.ir_hash: {digest}"]
+    lines += [f"// kg.gfx950.note: {n}" for n in notes]
+    absent = [f"{i}:{_DTYPE_NAMES[p.dtype]}:{p.rank}" for i, p in enumerate(func.params) if p.kind == "memory" and p.optional]
+    if absent:
+        lines.append(f"// kg.allow_absent_memory_args: {';'.join(absent)}")
+    return lines
 
-    entry, counts = LIBRARY_ENTRY[pattern.family]
-    total = pattern.forwarded_count
-    if total not in counts:
-        raise _error(f"{pattern.function}: {total} forwarded slots do not match {entry} ({counts})")
-    n_in = len(pattern.params)
-    digest = hashlib.sha256(repr(pattern).encode()).hexdigest()[:16]
-    lines = [
-        f"{BUNDLE_MARKER_PREFIX}kernel.hip",
-        f"// kg.gfx950.kernel: {pattern.function}",
-        f"// kg.gfx950.pattern: {pattern.family}",
-        f"// kg.gfx950.pattern_hash: {digest}",
-        f"// kg.gfx950.library_entry: {entry}",
-    ]
-    lines += [f"// kg.gfx950.note: {note}" for note in pattern.notes]
-    if pattern.absent_index is not None:
-        lines.append(f"// kg.allow_absent_memory_args: {pattern.absent_index}:{pattern.dtype}:{pattern.absent_rank}")
-    lines += [
+
+def emit_fused(func: Func, call: FusedCall, memory_stage: int | None = None) -> str:
+    index = {p.name: i for i, p in enumerate(func.params)}
+    entry = LIBRARY_ENTRY[call.family]
+    slots = library_slots(call, memory_stage)
+    checks: list[str] = []
+
+    def leaf(s: Sym) -> str:
+        if s.op == "arg":
+            i = index[s.args[0]]
+            checks.append(f'  if (s[{i}].kind != KG_ARG_INT) return kg_gfx950_fail(-1, "slot {i} ({s.args[0]}): '
+                          f'expected int slot");')
+            return f"s[{i}].int_value"
+        if s.op == "dim":
+            i = index[s.args[0]]
+            checks.append(f'  if (s[{i}].kind != KG_ARG_MEMORY || s[{i}].shape == nullptr || s[{i}].rank <= {s.args[1]}ULL) '
+                          f'return kg_gfx950_fail(-1, "slot {i} ({s.args[0]}): expected a memory slot of rank > {s.args[1]}");')
+            return f"s[{i}].shape[{s.args[1]}]"
+        raise _error("fused operands cannot use loop indices")
+
+    body: list[str] = []
+    for k, (kind, value) in enumerate(slots):
+        if kind == "mem":
+            if value is None:
+                body.append(f"  slots[{k}] = KgArgSlot{{}};  // absent")
+                body.append(f"  slots[{k}].kind = KG_ARG_MEMORY; slots[{k}].shape = kZero; slots[{k}].stride = kOne; "
+                            f"slots[{k}].rank = 1;")
+            else:
+                body.append(f"  slots[{k}] = s[{index[value]}];  // {value}")
+        elif kind == "int":
+            body.append(f"  slots[{k}] = KgArgSlot{{}};")
+            body.append(f"  slots[{k}].kind = KG_ARG_INT; slots[{k}].int_value = {value.to_c(leaf)};")
+        else:
+            v: FVal = value
+            body.append(f"  slots[{k}] = KgArgSlot{{}};")
+            if v.arg is not None:
+                i = index[v.arg]
+                checks.append(f'  if (s[{i}].kind != KG_ARG_FLOAT && s[{i}].kind != KG_ARG_INT) return kg_gfx950_fail(-1, '
+                              f'"slot {i} ({v.arg}): expected float slot");')
+                body.append(f"  slots[{k}].kind = KG_ARG_FLOAT; slots[{k}].float_value = s[{i}].kind == KG_ARG_FLOAT ? "
+                            f"s[{i}].float_value : (double)s[{i}].int_value;")
+            else:
+                lit = "HUGE_VAL" if math.isinf(v.value) and v.value > 0 else "-HUGE_VAL" if math.isinf(v.value) else repr(v.value)
+                body.append(f"  slots[{k}].kind = KG_ARG_FLOAT; slots[{k}].float_value = {lit};")
+    # memory parameters the call does not read must still be valid arguments
+    for i, p in enumerate(func.params):
+        if p.kind == "memory" and p.name not in call.memory:
+            checks.append(f'  if (kg_gfx950_check_memory_slot(s, {i}, {p.rank}, {1 if p.optional else 0}, 0, "{p.name}") '
+                          f'!= 0) return -1;')
+    seen = set()
+    uniq_checks = [c for c in checks if not (c in seen or seen.add(c))]
+    notes = [f"fused: {entry}"] + list(call.notes)
+    lines = _header(func, "fused", notes) + [
+        "#include <cmath>",
         '#include "kg_gfx950.h"',
+        '#include "gfx950/kg_tile.h"',
         "",
-        f"// runtime entry for {pattern.function} as {ENTRY_POINT}",
-        f'extern "C" int {ENTRY_POINT}(const KgArgSlot* ordered_args, unsigned long long arg_count) {{',
-        "  if (ordered_args == nullptr) return -1;",
-        f"  if (arg_count != {n_in}ULL) return -1;",
+        "using kg_tile::kg_floordiv; using kg_tile::kg_max; using kg_tile::kg_min; using kg_tile::kg_mod;",
+        "",
+        f"// {func.name} as {ENTRY_POINT}: the {call.family} nest of this kernel runs as {entry}",
+        f'extern "C" int {ENTRY_POINT}(const KgArgSlot* s, unsigned long long n) {{',
+        "  static const long long kZero[1] = {0};",
+        "  static const long long kOne[1] = {1};",
+        "  (void)kZero; (void)kOne;",
+        '  if (s == nullptr) return kg_gfx950_fail(-1, "ordered_args is null");',
+        f'  if (n != {len(func.params)}ULL) return kg_gfx950_fail(-1, "{func.name} expects {len(func.params)} slots");',
+        *uniq_checks,
+        f"  KgArgSlot slots[{len(slots)}];",
+        *body,
+        f"  return {entry}(slots, {len(slots)}ULL);",
+        "}",
+        "",
     ]
-    if not pattern.baked and not pattern.trailing:
-        lines.append(f"  return {entry}(ordered_args, arg_count);")
-    else:
-        lines.append(f"  KgArgSlot slots[{total}];")
-        out = 0
-
-        def const_slot(name: str, value: int | float) -> None:
-            nonlocal out
-            kind, lit = _c_literal(value)
-            field_name = "int_value" if kind == "KG_ARG_INT" else "float_value"
-            lines.append(f"  slots[{out}] = KgArgSlot{{}};  // {name}")
-            lines.append(f"  slots[{out}].kind = {kind};")
-            lines.append(f"  slots[{out}].{field_name} = {lit};")
-            out += 1
-
-        for i in range(pattern.insert_at):
-            lines.append(f"  slots[{out}] = ordered_args[{i}];  // {pattern.params[i]}")
-            out += 1
-        for name, value in pattern.baked:
-            const_slot(name, value)
-        for i in range(pattern.insert_at, n_in):
-            lines.append(f"  slots[{out}] = ordered_args[{i}];  // {pattern.params[i]}")
-            out += 1
-        for name, value in pattern.trailing:
-            const_slot(name, value)
-        lines.append(f"  return {entry}(slots, {total}ULL);")
-    lines += ["}", ""]
     return "\n".join(lines)
 
 
-def forward_args(pattern: KernelPattern, args: Sequence) -> tuple:
-    """The slot list the generated entry forwards to the library entry for ``args``: the
-    runtime args with the baked constants inserted at ``insert_at`` and the trailing
-    constants appended (the same order gen_kernel writes into kernel.hip)."""
+def gen_kernel(lowered) -> str:
+    """SourceBundle text of a lowered kernel (pipeline.LoweredKernel)."""
 
-    args = tuple(args)
-    if len(args) != len(pattern.params):
-        raise _error(f"{pattern.function}: expected {len(pattern.params)} args, got {len(args)}")
-    baked = tuple(value for _, value in pattern.baked)
-    trailing = tuple(value for _, value in pattern.trailing)
-    return args[: pattern.insert_at] + baked + args[pattern.insert_at:] + trailing
+    func = lowered.func
+    if lowered.fused is not None:
+        return emit_fused(func, lowered.fused, lowered.memory_stage)
+    return "\n".join(_header(func, "per-op", ["every operation on the workgroups (gfx950/kg_tile.h)"])) + "\n" + \
+        emit_per_op(func, func.name)
 
 
-# ------------------------------------------------------------------------------------
-# pattern registry (recognition by DSL function name)
-# ------------------------------------------------------------------------------------
-
-PatternBuilder = Callable[[dict, str], KernelPattern]
-_PATTERNS: dict[str, PatternBuilder] = {}
-
-
-def register_pattern(function_name: str, builder: PatternBuilder) -> None:
-    _PATTERNS[function_name] = builder
-
-
-def recognise(func_obj: Callable, dtype: str = "float32") -> KernelPattern:
-    """Map a DSL kernel to its gfx950 pattern; module globals supply baked constants."""
-
-    name = getattr(func_obj, "__name__", "")
-    builder = _PATTERNS.get(name)
-    if builder is None:
-        raise _error(f"gfx950 has no pattern for DSL function {name!r}")
-    return builder(getattr(func_obj, "__globals__", {}), dtype)
-
-
-def known_patterns() -> tuple[str, ...]:
-    return tuple(sorted(_PATTERNS))
-
-
-def _g(globs: dict, key: str, default):
-    value = globs.get(key, default)
-    return value
-
-
-_MATMUL_PARAMS = ("out", "lhs", "rhs", "bias")
-_MATMUL_TILES = ("tile_h", "tile_w", "tile_k")
-_CONV_PARAMS = ("out", "input_tensor", "weight", "bias")
-_CONV_GEOM = ("stride_h", "stride_w", "dilation_h", "dilation_w", "pad_top", "pad_bottom", "pad_left", "pad_right")
-_CONV_TILES = ("tile_f", "tile_c", "tile_n", "tile_ho", "tile_wo")
-_FA_PARAMS = ("out", "q", "k", "v")
-
-
-def _matmul_static_static(globs: dict, dtype: str) -> KernelPattern:
-    # kernel/matmul/inputs_static_tile_static.py:56-110: tiles are module constants
-    tiles = (_g(globs, "_TILE_M", 48), _g(globs, "_TILE_N", 80), _g(globs, "_TILE_K", 56))
-    return KernelPattern("matmul", "matmul_inputs_static_tile_static_kernel", _MATMUL_PARAMS,
-                         tuple(zip(("tile_m", "tile_n", "tile_k"), tiles)), 4, absent_index=3, dtype=dtype)
-
-
-def _matmul_tile_dynamic(name: str) -> PatternBuilder:
-    def build(globs: dict, dtype: str) -> KernelPattern:
-        return KernelPattern("matmul", name, _MATMUL_PARAMS + _MATMUL_TILES, (), 7, absent_index=3, dtype=dtype)
-
-    return build
-
-
-def _conv_geometry(globs: dict) -> tuple[tuple[str, int], ...]:
-    # the static conv demos hard-code stride 8 and take dilation/pads from module constants
-    values = (8, 8, _g(globs, "_STATIC_DILATION_H", 1), _g(globs, "_STATIC_DILATION_W", 1),
-              _g(globs, "_STATIC_PAD_TOP", 0), _g(globs, "_STATIC_PAD_BOTTOM", 0),
-              _g(globs, "_STATIC_PAD_LEFT", 0), _g(globs, "_STATIC_PAD_RIGHT", 0))
-    return tuple(zip(_CONV_GEOM, values))
-
-
-def _conv_static_static(globs: dict, dtype: str) -> KernelPattern:
-    tiles = (_g(globs, "_STATIC_TILE_F", 8), _g(globs, "_STATIC_TILE_C", 16), _g(globs, "_STATIC_TILE_N", 4),
-             _g(globs, "_STATIC_TILE_HO", 8), _g(globs, "_STATIC_TILE_WO", 9))
-    return KernelPattern("conv2d", "conv2d_inputs_static_tile_static_kernel", _CONV_PARAMS,
-                         _conv_geometry(globs) + tuple(zip(_CONV_TILES, tiles)), 4, absent_index=3, dtype=dtype)
-
-
-def _conv_static_dynamic(globs: dict, dtype: str) -> KernelPattern:
-    return KernelPattern("conv2d", "conv2d_inputs_static_tile_dynamic_kernel", _CONV_PARAMS + _CONV_TILES,
-                         _conv_geometry(globs), 4, absent_index=3, dtype=dtype)
-
-
-def _conv_dynamic_dynamic(globs: dict, dtype: str) -> KernelPattern:
-    return KernelPattern("conv2d", "conv2d_inputs_dynamic_tile_dynamic_kernel", _CONV_PARAMS + _CONV_GEOM + _CONV_TILES,
-                         (), 17, absent_index=3, dtype=dtype)
-
-
-def _fa_static_static(globs: dict, dtype: str) -> KernelPattern:
-    tiles = (_g(globs, "_STATIC_BR", 64), _g(globs, "_STATIC_BC", 80))
-    return KernelPattern("flash_attention", "flash_attention_inputs_static_tile_static_kernel", _FA_PARAMS,
-                         tuple(zip(("br", "bc"), tiles)), 4, dtype=dtype)
-
-
-def _fa_tile_dynamic(name: str) -> PatternBuilder:
-    def build(globs: dict, dtype: str) -> KernelPattern:
-        return KernelPattern("flash_attention", name, _FA_PARAMS + ("br", "bc"), (), 6, dtype=dtype)
-
-    return build
-
-
-def _fa_scaled(name: str, causal: bool) -> PatternBuilder:
-    # scale = 1/sqrt(D) as a `kernel.mul` by a filled tile and, for causal, the
-    # `min(seq, m0 + br)` key bound plus the 0/-inf diagonal mask: the BASELINE variants
-    def build(globs: dict, dtype: str) -> KernelPattern:
-        scale = float(_g(globs, "_SOFTMAX_SCALE", 0.0))
-        return KernelPattern("flash_attention", name, _FA_PARAMS + ("br", "bc", "scale"), (), 7,
-                             trailing=(("causal", 1 if causal else 0),), dtype=dtype,
-                             notes=("scale = runtime FLOAT slot", "causal lower-triangular mask" if causal else "no mask"))
-
-    return build
-
-
-register_pattern("matmul_inputs_static_tile_static_kernel", _matmul_static_static)
-register_pattern("matmul_inputs_static_tile_dynamic_kernel", _matmul_tile_dynamic("matmul_inputs_static_tile_dynamic_kernel"))
-register_pattern("matmul_inputs_dynamic_tile_dynamic_kernel", _matmul_tile_dynamic("matmul_inputs_dynamic_tile_dynamic_kernel"))
-register_pattern("conv2d_inputs_static_tile_static_kernel", _conv_static_static)
-register_pattern("conv2d_inputs_static_tile_dynamic_kernel", _conv_static_dynamic)
-register_pattern("conv2d_inputs_dynamic_tile_dynamic_kernel", _conv_dynamic_dynamic)
-register_pattern("flash_attention_inputs_static_tile_static_kernel", _fa_static_static)
-register_pattern("flash_attention_inputs_static_tile_dynamic_kernel",
-                 _fa_tile_dynamic("flash_attention_inputs_static_tile_dynamic_kernel"))
-register_pattern("flash_attention_inputs_dynamic_tile_dynamic_kernel",
-                 _fa_tile_dynamic("flash_attention_inputs_dynamic_tile_dynamic_kernel"))
-register_pattern("flash_attention_scaled_kernel", _fa_scaled("flash_attention_scaled_kernel", False))
-register_pattern("flash_attention_scaled_causal_kernel", _fa_scaled("flash_attention_scaled_causal_kernel", True))
-
-__all__ = ["BUNDLE_MARKER_PREFIX", "ENTRY_POINT", "KernelPattern", "forward_args", "gen_kernel", "known_patterns",
-           "recognise", "register_pattern"]
+__all__ = ["BUNDLE_MARKER_PREFIX", "ENTRY_POINT", "LIBRARY_ENTRY", "emit_fused", "emit_per_op", "gen_kernel",
+           "library_slots"]

@@ -4,8 +4,9 @@
   ``run_numpy_demo`` with target ``gfx950`` and pipeline ``gfx950-lowering``: set the
   target and dump dir, ``dsl_run``, write ``source.hip``, compare ``output`` with
   ``expected`` (np.allclose, default atol = rtol = 1e-4), restore the config;
-- ``run_lowering_demo(case_name, kernel_fn, dtype)`` returns the lowered pattern and the
-  generated source without executing.
+- ``run_lowering_demo(case_name, kernel_fn, *compile_args)`` (:247-278) returns the lowered
+  kernel and the generated source without executing; ``compile_args`` stand for the
+  runtime arguments (arrays, tensors or native.TensorSpec for memory, ints, floats, None).
 """
 
 from __future__ import annotations
@@ -17,7 +18,8 @@ from typing import Any, Callable
 import numpy as np
 
 from ..core.config import restore_config, set_dump_dir, set_target, snapshot_config
-from ..gen_kernel import gen_kernel, recognise
+from ..dsl import mlir_gen
+from ..gen_kernel import gen_kernel
 from ..pipeline import build_gfx950_lowering_pipeline
 from ..tools.dsl_run import DslRunResult, dsl_run
 
@@ -59,11 +61,11 @@ def run_gfx950_demo(case_name: str, kernel_fn: Callable, real_args, output, expe
         restore_config(snapshot)
 
 
-def run_lowering_demo(case_name: str, kernel_fn: Callable, dtype: str = "float32"):
+def run_lowering_demo(case_name: str, kernel_fn: Callable, *compile_args):
     snapshot = snapshot_config()
     try:
         set_target("gfx950")
-        lowered = build_gfx950_lowering_pipeline().run(recognise(kernel_fn, dtype))
-        return lowered, gen_kernel(lowered.pattern)
+        lowered = build_gfx950_lowering_pipeline().run(mlir_gen(kernel_fn, compile_args))
+        return lowered, gen_kernel(lowered)
     finally:
         restore_config(snapshot)

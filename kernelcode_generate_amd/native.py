@@ -44,6 +44,11 @@ CONTROL_SYMBOLS = (
     "kg_gfx950_last_error",
     "kg_gfx950_abi_version",
     "kg_gfx950_cost",
+    "kg_gfx950_fail",
+    "kg_gfx950_check_memory_slot",
+    "kg_gfx950_launch_stream",
+    "kg_gfx950_launch_synchronous",
+    "kg_gfx950_finish_launch",
 )
 
 # kg_gfx950_cost: op codes (KG_OP_*) and the order of its output array (KG_COST_*).

@@ -2,22 +2,26 @@
 ``npu-demo-lowering`` / ``cuda-sm89-lowering`` (kernel_gen/pipeline/cuda_sm89_lowering.py:
 159-223, registry kernel_gen/passes/registry.py:343).
 
-In the reference the pipeline rewrites xDSL IR; the IR passes it shares with
-cuda-sm89-lowering are listed in ``IR_PASSES`` in their order (the memory-pool passes are
-left out: gfx950 kernels manage LDS themselves). xDSL is not part of this backend, so the
-steps that run here act on the recognised ``KernelPattern``: option checks, the K-loop
-fusion rule of KernelAggregatePass(matmul_acc=True) (sequential-k accumulation, which the
-GPU kernels honour by accumulating every k in fp32), the static-tile legality check, and
-attaching the gfx950 hardware description (CUs, wave width, LDS bytes).
+It runs on the kernel IR the front end builds (dsl.mlir_gen) and applies, in order:
 
-``memory_stage`` (option, 2-4) is the gfx950 reading of MultiBufferAnalysisPass's
-``memory_stage`` (kernel_gen/passes/memory/multi_buffer.py, npu-demo-lowering uses 2): the
-depth of the ring the staged operands cycle through. For matmul kernels it becomes the
-LDS ring depth of the pipelined MFMA GEMM, passed as a trailing INT slot; without the
-option the library uses 4. Like the reference pass on IR it cannot ring, it leaves conv2d
-and attention alone (their K/V and channel-group buffers are fixed double buffers). The
-software pipelining LoopSoftPipelinePass builds in IR (prologue, steady loop, epilogue) is
-what every gfx950 kernel does already, so that pass has no knob here.
+  kernel-aggregate{matmul-acc=true}   fold K-loop matmul + add into accumulating matmuls
+                                       (kernel_gen/passes/kernel/kernel_aggregate.py:292)
+  kernel-pattern-fuse                  map a recognised loop nest onto a hand-written
+                                       gfx950 kernel (passes/fuse.py)
+  multi-buffer{memory-stage=N}         (option) the LDS ring depth of the fused GEMM, the
+                                       gfx950 reading of MultiBufferAnalysisPass's
+                                       memory_stage (kernel_gen/passes/memory/multi_buffer.py)
+  arch-parallelize{target=gfx950}      the per-operation path's grid: the leading
+                                       perfectly nested loops (arch_parallelize.py:637-680)
+  attach-arch-information{target=gfx950}  the target's hardware description
+
+The memory-plan passes of the reference are not needed: a fused kernel manages LDS and
+registers itself, and the per-operation path sizes its tiles' workspace in the entry.
+LoopSoftPipelinePass's prologue / steady loop / epilogue is what every hand-written
+kernel already does, so that pass has no knob here.
+
+Options: ``target`` (gfx950), ``memory_stage`` (2, 3 or 4; fused matmul only) and
+``fuse`` (default true; false keeps every kernel on the per-operation path).
 """
 
 from __future__ import annotations
@@ -26,16 +30,10 @@ from dataclasses import dataclass, field, replace
 from typing import Callable
 
 from ..core.error import ErrorKind, ErrorModule, KernelCodeError
-from ..gen_kernel import KernelPattern
+from ..gen_kernel.per_op import parallel_loops
+from ..ir import Func
+from ..passes import FusedCall, kernel_aggregate, pattern_fuse
 from ..target import get_target_hardware
-
-IR_PASSES = (
-    "inline", "cse", "canonicalize", "decompass", "nn-lowering", "memory-plan", "symbol-hoist-pipeline",
-    "tile-analysis", "kernel-pattern-attach", "transform-apply", "memory-plan", "symbol-hoist-pipeline",
-    "kernel-aggregate{matmul-acc=true}", "kernel-decompose", "memory-plan", "symbol-hoist-pipeline",
-    "producer-consumer-analysis", "arch-parallelize{target=gfx950,parallel_level=block}",
-    "attach-arch-information{target=gfx950}", "outline-device-kernel", "template-name-infer",
-)
 
 _PIPELINES: dict[str, Callable[..., "PassManager"]] = {}
 
@@ -61,60 +59,56 @@ def get_pipeline(name: str, options: dict | None = None) -> "PassManager":
     return builder(options)
 
 
-@dataclass(frozen=True)
+@dataclass
 class LoweredKernel:
-    pattern: KernelPattern
-    hardware: dict[str, int]
-    applied: tuple[str, ...]
+    func: Func
+    fused: FusedCall | None = None
+    memory_stage: int | None = None
+    parallel: tuple[str, ...] = ()
+    hardware: dict[str, int] = field(default_factory=dict)
+    applied: tuple[str, ...] = ()
+    folds: int = 0
 
 
 @dataclass
 class PassManager:
     name: str
     passes: list[tuple[str, Callable[[LoweredKernel], LoweredKernel]]] = field(default_factory=list)
-    ir_passes: tuple[str, ...] = IR_PASSES
 
     def add_pass(self, name: str, fn: Callable[[LoweredKernel], LoweredKernel]) -> None:
         self.passes.append((name, fn))
 
-    def run(self, pattern: KernelPattern) -> LoweredKernel:
-        if not isinstance(pattern, KernelPattern):
-            raise _error(f"{self.name} runs on a recognised KernelPattern")
-        state = LoweredKernel(pattern, {}, ())
+    def run(self, func: Func) -> LoweredKernel:
+        if not isinstance(func, Func):
+            raise _error(f"{self.name} runs on kernel IR (dsl.mlir_gen)")
+        state = LoweredKernel(func)
         for name, fn in self.passes:
             state = fn(state)
             state = replace(state, applied=state.applied + (name,))
         return state
 
 
-def _check_static_tiles(state: LoweredKernel) -> LoweredKernel:
-    for name, value in state.pattern.baked:
-        if name.startswith("tile") or name in ("br", "bc"):
-            if not isinstance(value, int) or value <= 0:
-                raise _error(f"{state.pattern.function}: static {name}={value!r} must be a positive int")
-        if name.startswith("stride") or name.startswith("dilation"):
-            if not isinstance(value, int) or value <= 0:
-                raise _error(f"{state.pattern.function}: {name}={value!r} must be a positive int")
-        if name.startswith("pad") and (not isinstance(value, int) or value < 0):
-            raise _error(f"{state.pattern.function}: {name}={value!r} must be a non-negative int")
-    return state
-
-
 def _kernel_aggregate(state: LoweredKernel) -> LoweredKernel:
-    # matmul(acc = k_iter != k_start): one fp32 accumulation over all of K per output.
-    return state
+    return replace(state, folds=state.folds + kernel_aggregate(state.func))
+
+
+def _pattern_fuse(state: LoweredKernel) -> LoweredKernel:
+    return replace(state, fused=pattern_fuse(state.func))
 
 
 def _multi_buffer(stage: int) -> Callable[[LoweredKernel], LoweredKernel]:
     def run(state: LoweredKernel) -> LoweredKernel:
-        p = state.pattern
-        if p.family != "matmul":
-            return state
-        if len(p.params) + len(p.baked) != 7:
-            raise _error(f"{p.function}: memory_stage needs the tile slots (7 forwarded slots)")
-        return replace(state, pattern=replace(p, trailing=p.trailing + (("memory_stage", stage),)))
+        if state.fused is None or state.fused.family != "matmul":
+            return state  # like the reference pass on IR it cannot ring: left alone
+        return replace(state, memory_stage=stage)
 
     return run
+
+
+def _arch_parallelize(state: LoweredKernel) -> LoweredKernel:
+    if state.fused is not None:
+        return state
+    return replace(state, parallel=tuple(loop.attrs["iv"] for loop in parallel_loops(state.func)))
 
 
 def _attach_arch_information(state: LoweredKernel) -> LoweredKernel:
@@ -122,12 +116,21 @@ def _attach_arch_information(state: LoweredKernel) -> LoweredKernel:
     return replace(state, hardware={k: get_target_hardware("gfx950", k) for k in keys})
 
 
+def _flag(value, name: str) -> bool:
+    text = str(value).strip().lower()
+    if text in ("1", "true", "yes", "on"):
+        return True
+    if text in ("0", "false", "no", "off"):
+        return False
+    raise _error(f"gfx950-lowering {name} expects a bool, got {value!r}")
+
+
 @register_pipeline("gfx950-lowering")
 def build_gfx950_lowering_pipeline(options: dict | None = None) -> PassManager:
     opts = {} if options is None else dict(options)
-    unknown = sorted(set(opts) - {"target", "memory_stage"})
+    unknown = sorted(set(opts) - {"target", "memory_stage", "fuse"})
     if unknown:
-        raise _error(f"gfx950-lowering accepts target and memory_stage options; got {', '.join(unknown)}")
+        raise _error(f"gfx950-lowering accepts target, memory_stage and fuse options; got {', '.join(unknown)}")
     if opts.get("target", "gfx950") != "gfx950":
         raise _error("gfx950-lowering target must be gfx950")
     stage = None
@@ -138,10 +141,13 @@ def build_gfx950_lowering_pipeline(options: dict | None = None) -> PassManager:
             stage = None
         if stage not in (2, 3, 4):
             raise _error(f"gfx950-lowering memory_stage must be 2, 3 or 4, got {opts['memory_stage']!r}")
+    fuse = _flag(opts.get("fuse", True), "fuse")
     pm = PassManager(name="gfx950-lowering")
-    pm.add_pass("tile-analysis", _check_static_tiles)
     pm.add_pass("kernel-aggregate{matmul-acc=true}", _kernel_aggregate)
+    if fuse:
+        pm.add_pass("kernel-pattern-fuse", _pattern_fuse)
     if stage is not None:
         pm.add_pass(f"multi-buffer{{memory-stage={stage}}}", _multi_buffer(stage))
+    pm.add_pass("arch-parallelize{target=gfx950,parallel_level=block}", _arch_parallelize)
     pm.add_pass("attach-arch-information{target=gfx950}", _attach_arch_information)
     return pm

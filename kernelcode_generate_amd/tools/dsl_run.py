@@ -1,20 +1,21 @@
 """``dsl_run(func_obj, real_args, pipeline)`` for the gfx950 target
 (kernel_gen/tools/dsl_run.py:578-653): check the configured target and the arity against
-the kernel's signature, recognise the kernel (in place of mlir_gen), run the pipeline,
-generate the SourceBundle, compile it through ``ExecutionEngine("gfx950")`` and execute
-it with the real arguments.
+the kernel's signature, build the kernel's IR from its Python source (dsl.mlir_gen, the
+reference's mlir_gen), run the pipeline (gfx950-lowering), generate the SourceBundle,
+compile it through ``ExecutionEngine("gfx950")`` and execute it with the real arguments.
 
 Memory arguments may be ROCm torch tensors (used in place) or host numpy arrays /
 CPU tensors, which are staged to the device and copied back after the call -- what the
 reference's cuda_sm89 entry does per call (source_bundle.py:647-707). ``None`` is
-allowed for the bias slot only; ints and floats are passed as INT / FLOAT slots.
+allowed for memory parameters the kernel tests with `is None` / `is not None`; ints and
+floats are passed as INT / FLOAT slots.
 
 ``dsl_cost_run(func_obj, real_args, pipeline, cost_kind)`` (kernel_gen/tools/dsl_run.py:
 656-730) returns one integer cost of the same call without running it: the reference
 lowers to an npu_demo cost function whose kinds are DMA1..DMA4, MAC, VECTOR1, VECTOR2;
-here the library's kg_gfx950_cost runs the entry's validation and kernel choice and
+here the library's kg_gfx950_cost runs the fused kernel's validation and kernel choice and
 reports MAC, MFMA (wave-level matrix instructions of the chosen kernel), HBM_READ and
-HBM_WRITE (compulsory bytes).
+HBM_WRITE (compulsory bytes). Kernels on the per-operation path have no cost model.
 """
 
 from __future__ import annotations
@@ -28,8 +29,11 @@ from typing import Any, Callable
 
 from ..core.config import get_dump_dir, get_target
 from ..core.error import ErrorKind, ErrorModule, KernelCodeError
+from ..dsl import mlir_gen
 from ..execute_engine import CompiledKernel, ExecuteResult, ExecutionEngine
-from ..gen_kernel import KernelPattern, forward_args, gen_kernel, recognise
+from ..gen_kernel import gen_kernel, library_slots
+from ..ir import Sym
+from ..passes import FusedCall
 from ..pipeline import PassManager, get_pipeline
 from ..pipeline.gfx950_lowering import LoweredKernel
 
@@ -53,7 +57,7 @@ def _close_cached() -> None:
 
 @dataclass(frozen=True)
 class DslRunResult:
-    pattern: KernelPattern
+    fused: FusedCall | None
     module: LoweredKernel
     source: str
     compiled_kernel: CompiledKernel
@@ -117,13 +121,10 @@ def _is_scalar(arg: Any) -> bool:
     return arg is None or isinstance(arg, (Integral, Real))
 
 
-def _recognise(func_obj: Callable, args: tuple) -> KernelPattern:
-    memory = [a for a in args if not _is_scalar(a)]
-    dtype = _dtype_name(memory[0]) if memory else "float32"
-    pattern = recognise(func_obj, dtype)
-    if len(pattern.params) != len(args):
-        raise _error(f"{pattern.function}: expected {len(pattern.params)} args, got {len(args)}")
-    return pattern
+def lower(func_obj: Callable, args: tuple, pipeline: str | PassManager) -> LoweredKernel:
+    """Front end + pipeline: the lowered kernel for these runtime argument kinds."""
+
+    return _resolve_pipeline(pipeline).run(mlir_gen(func_obj, args))
 
 
 def dsl_run(func_obj: Callable, real_args: tuple | list, pipeline: str | PassManager) -> DslRunResult:
@@ -131,18 +132,16 @@ def dsl_run(func_obj: Callable, real_args: tuple | list, pipeline: str | PassMan
     if target != "gfx950":
         raise _error(f"DslRunInvalidTarget: core config target must be 'gfx950' for this backend, got {target!r}")
     args = _check_arity(func_obj, real_args)
-    pm = _resolve_pipeline(pipeline)
-    pattern = _recognise(func_obj, args)
-    lowered = pm.run(pattern)
-    source = gen_kernel(lowered.pattern)
+    lowered = lower(func_obj, args, pipeline)
+    source = gen_kernel(lowered)
     dump = get_dump_dir()
     if dump is not None:
-        out_dir = Path(dump) / pattern.function
+        out_dir = Path(dump) / lowered.func.name
         out_dir.mkdir(parents=True, exist_ok=True)
         (out_dir / "source.hip").write_text(source)
     compiled = _COMPILED.get(source)
     if compiled is None:
-        compiled = ExecutionEngine(target="gfx950").compile(source=source, function=pattern.function)
+        compiled = ExecutionEngine(target="gfx950").compile(source=source, function=lowered.func.name)
         _COMPILED[source] = compiled
     staged = []
     writebacks = []
@@ -157,8 +156,22 @@ def dsl_run(func_obj: Callable, real_args: tuple | list, pipeline: str | PassMan
     result = compiled.execute(args=tuple(staged))
     for back in writebacks:
         back()
-    return DslRunResult(pattern=pattern, module=lowered, source=source, compiled_kernel=compiled,
+    return DslRunResult(fused=lowered.fused, module=lowered, source=source, compiled_kernel=compiled,
                         execute_result=result, runtime_args=tuple(staged))
+
+
+def _evaluate(expr: Sym, func, args: tuple) -> int:
+    index = {p.name: i for i, p in enumerate(func.params)}
+
+    def leaf(s: Sym) -> int:
+        value = args[index[s.args[0]]]
+        if s.op == "arg":
+            return int(value)
+        if s.op == "dim":
+            return int(tuple(value.shape)[s.args[1]])
+        raise _error("fused operands cannot use loop indices")
+
+    return expr.evaluate(leaf)
 
 
 def dsl_cost_run(func_obj: Callable, real_args: tuple | list, pipeline: str | PassManager, cost_kind: str) -> int:
@@ -178,10 +191,22 @@ def dsl_cost_run(func_obj: Callable, real_args: tuple | list, pipeline: str | Pa
         raise _error(DSL_COST_TARGET_ERROR)
     pm = _resolve_pipeline(pipeline)
     args = _check_arity(func_obj, real_args)
-    pattern = pm.run(_recognise(func_obj, args)).pattern
-    slots = forward_args(pattern, [a if _is_scalar(a) else native.TensorSpec.of(a) for a in args])
+    lowered = pm.run(mlir_gen(func_obj, args))
+    if lowered.fused is None:
+        raise _error(f"{DSL_COST_OUTPUT_ERROR}: {lowered.func.name} runs on the per-operation path, which has no "
+                     "cost model")
+    index = {p.name: i for i, p in enumerate(lowered.func.params)}
+    slots = []
+    for kind, value in library_slots(lowered.fused, lowered.memory_stage):
+        if kind == "mem":
+            arg = None if value is None else args[index[value]]
+            slots.append(None if arg is None else native.TensorSpec.of(arg))
+        elif kind == "int":
+            slots.append(_evaluate(value, lowered.func, args))
+        else:
+            slots.append(float(args[index[value.arg]]) if value.arg is not None else float(value.value))
     try:
-        costs = native.cost(pattern.family, slots)
+        costs = native.cost(lowered.fused.family, slots)
     except native.NativeLibraryError as exc:
         raise _error(f"{DSL_COST_OUTPUT_ERROR}: {exc}") from exc
     return costs[cost_kind]

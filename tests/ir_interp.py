@@ -1,0 +1,174 @@
+"""TEST INFRASTRUCTURE ONLY: a numpy interpreter of the gfx950 kernel IR.
+
+It executes a lowered function (dsl.mlir_gen + passes) operation by operation on host
+arrays with the arithmetic the per-operation GPU path uses (include/gfx950/kg_tile.h:
+sequential-k fp32 matmul with every product and sum rounded to float, exp and division in
+double, row max from element 0, row sum from 0). Running a demo's IR here and comparing
+with the oracle's restatement of the reference's loop nest pins the front end and the
+passes on the CPU: if the IR a DSL kernel lowers to computed anything else, the two would
+differ.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+from kernelcode_generate_amd.ir import Cmp, FVal, Func, Mem, Op, Present, Sym
+
+NP = {"f32": np.float32, "f16": np.float16, "bf16": np.float32}
+
+
+class _Env:
+    def __init__(self, func: Func, args: tuple) -> None:
+        self.func = func
+        self.vals: dict[str, object] = {}
+        self.mems: dict[int, np.ndarray] = {}
+        for p, a in zip(func.params, args):
+            if p.kind == "memory":
+                self.vals[p.name] = a
+                if a is not None:
+                    self.mems[id(func.args[p.name])] = a
+            else:
+                self.vals[p.name] = a
+        self.ivs: dict[str, int] = {}
+
+    def sym(self, s: Sym) -> int:
+        def leaf(x: Sym) -> int:
+            if x.op == "arg":
+                return int(self.vals[x.args[0]])
+            if x.op == "dim":
+                a = self.vals[x.args[0]]
+                return int(a.shape[x.args[1]]) if a is not None else 0
+            return self.ivs[x.args[0]]
+
+        return s.evaluate(leaf)
+
+    def fval(self, v: FVal) -> np.float32:
+        return np.float32(self.vals[v.arg] if v.arg is not None else v.value)
+
+    def cond(self, c) -> bool:
+        if isinstance(c, bool):
+            return c
+        if isinstance(c, Present):
+            return self.vals[c.mem] is not None
+        if isinstance(c, Cmp):
+            return c.evaluate(lambda x: self.sym(x) if x.op != "iv" else self.ivs[x.args[0]])
+        raise TypeError(c)
+
+
+def _region(arr: np.ndarray, offsets, sizes, steps) -> np.ndarray:
+    idx = []
+    for o, z, st, ext in zip(offsets, sizes, steps, arr.shape):
+        if z < 0 or st <= 0 or (z > 0 and (o < 0 or o + (z - 1) * st >= ext)):
+            raise IndexError(f"view out of bounds: offsets {offsets} sizes {sizes} of {arr.shape}")
+        idx.append(slice(o, o + (z - 1) * st + 1, st) if z > 0 else slice(0, 0))
+    return arr[tuple(idx)]
+
+
+def _store(dst: np.ndarray, values: np.ndarray) -> None:
+    dst[...] = values.astype(dst.dtype, copy=False).reshape(dst.shape)
+
+
+def _run(block: list[Op], env: _Env) -> None:
+    for op in block:
+        n = op.name
+        a = op.attrs
+        if n == "symbol.for":
+            start, end, step = (env.sym(a[k]) for k in ("start", "end", "step"))
+            assert step > 0
+            for i in range(start, end, step):
+                env.ivs[a["iv"]] = i
+                _run(op.regions[0], env)
+            continue
+        if n == "scf.if":
+            _run(op.regions[0] if env.cond(a["cond"]) else op.regions[1], env)
+            continue
+        if n == "dma.alloc":
+            m = op.result
+            shape = tuple(max(env.sym(d), 0) for d in m.shape)
+            env.mems[id(m)] = np.full(shape, np.nan, NP[m.dtype])
+            continue
+        if n == "dma.view":
+            src = env.mems[id(op.operands[0])]
+            env.mems[id(op.result)] = _region(src, [env.sym(x) for x in a["offsets"]], [env.sym(x) for x in a["sizes"]],
+                                              [env.sym(x) for x in a["strides"]])
+            continue
+        if n == "dma.reshape":
+            src = env.mems[id(op.operands[0])]
+            shape = tuple(max(env.sym(d), 0) for d in op.result.shape)
+            view = src.reshape(shape)
+            assert np.shares_memory(view, src) or src.size == 0, "reshape of a non-contiguous view"
+            env.mems[id(op.result)] = view
+            continue
+        mems = [env.mems[id(m)] for m in op.operands]
+        if n == "dma.fill":
+            mems[0][...] = env.fval(a["value"])
+        elif n == "dma.deslice":
+            region = _region(mems[0], [env.sym(x) for x in a["offsets"]], [env.sym(x) for x in a["sizes"]],
+                             [env.sym(x) for x in a["strides"]])
+            _store(region, mems[1])
+        elif n == "dma.slice":
+            region = _region(mems[1], [env.sym(x) for x in a["offsets"]], [env.sym(x) for x in a["sizes"]],
+                             [env.sym(x) for x in a["strides"]])
+            _store(mems[0], region)
+        elif n == "dma.broadcast":
+            mems[0][...] = np.broadcast_to(mems[1], mems[0].shape)
+        elif n == "dma.transpose":
+            _store(mems[0], np.transpose(mems[1], a["perm"]))
+        elif n == "kernel.matmul":
+            out, lhs, rhs = (m.astype(np.float32) for m in mems)
+            acc = out.copy() if env.cond(a["acc"]) else np.zeros(out.shape, np.float32)
+            for k in range(lhs.shape[1]):
+                acc = (acc + (lhs[:, k, None] * rhs[None, k, :]).astype(np.float32)).astype(np.float32)
+            _store(mems[0], acc)
+        elif n == "kernel.img2col2d":
+            out, x = mems
+            g = {k: env.sym(v) for k, v in a.items()}
+            nb, c, h, w = x.shape
+            for r in range(g["kh"]):
+                for q in range(g["kw"]):
+                    for y in range(out.shape[4]):
+                        sy = y * g["sh"] + r * g["dh"] - g["ph"]
+                        for xx in range(out.shape[5]):
+                            sx = xx * g["sw"] + q * g["dw"] - g["pl"]
+                            ok = 0 <= sy < h and 0 <= sx < w
+                            out[:, :, r, q, y, xx] = x[:, :, sy, sx] if ok else 0.0
+        elif n == "kernel.exp":
+            _store(mems[0], np.exp(mems[1].astype(np.float64)).astype(np.float32))
+        elif n == "kernel.reduce":
+            x = mems[1].astype(np.float32)
+            if a["kind"] == "max":
+                cur = x[:, 0].copy()
+                for j in range(1, x.shape[1]):
+                    cur = np.where(x[:, j] > cur, x[:, j], cur)
+            else:
+                cur = np.zeros(x.shape[0], np.float32)
+                for j in range(x.shape[1]):
+                    cur = (cur + x[:, j]).astype(np.float32)
+            _store(mems[0], cur[:, None])
+        elif n == "kernel.binary_elewise":
+            l, r = mems[1].astype(np.float32), mems[2].astype(np.float32)
+            k = a["kind"]
+            with np.errstate(all="ignore"):
+                if k == "add":
+                    v = l + r
+                elif k == "sub":
+                    v = l - r
+                elif k == "mul":
+                    v = l * r
+                elif k == "truediv":
+                    v = (l.astype(np.float64) / r.astype(np.float64)).astype(np.float32)
+                else:
+                    v = np.where(l > r, l, r)
+            _store(mems[0], v.astype(np.float32))
+        else:
+            raise NotImplementedError(n)
+
+
+def run(func: Func, args: tuple) -> None:
+    """Execute ``func`` on host arrays (memory args are written in place)."""
+
+    with np.errstate(invalid="ignore", over="ignore"):
+        _run(func.body, _Env(func, args))

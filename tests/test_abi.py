@@ -19,7 +19,7 @@ HEADER = REPO / "include" / "kg_gfx950.h"
 
 def declared_functions() -> list[str]:
     text = HEADER.read_text()
-    return re.findall(r"^\s*(?:int|const char\*)\s+(kg_gfx950_\w+)\s*\(", text, flags=re.M)
+    return re.findall(r"^\s*(?:int|const char\*|void\*)\s+(kg_gfx950_\w+)\s*\(", text, flags=re.M)
 
 
 def test_header_declares_entries():

@@ -25,7 +25,8 @@ from kernelcode_generate_amd.execute_engine import (
 from kernelcode_generate_amd.execute_engine.compiler import CompiledKernel
 from kernelcode_generate_amd.execute_engine.gfx950_strategy import Gfx950CompileStrategy, unbundle
 from kernelcode_generate_amd.execute_engine.runtime_args import parse_allow_absent, validate_args
-from kernelcode_generate_amd.gen_kernel import gen_kernel, known_patterns, recognise
+from kernelcode_generate_amd.dsl import mlir_gen
+from kernelcode_generate_amd.gen_kernel import gen_kernel
 from kernelcode_generate_amd.kernel.conv2d.inputs_dynamic_tile_dynamic import conv2d_inputs_dynamic_tile_dynamic_kernel
 from kernelcode_generate_amd.kernel.conv2d.inputs_static_tile_dynamic import conv2d_inputs_static_tile_dynamic_kernel
 from kernelcode_generate_amd.kernel.conv2d.inputs_static_tile_static import conv2d_inputs_static_tile_static_kernel
@@ -43,16 +44,22 @@ from kernelcode_generate_amd.pipeline import build_gfx950_lowering_pipeline, get
 from kernelcode_generate_amd.target import get_target_hardware, is_arch_op_supported
 from kernelcode_generate_amd.tools import dsl_run
 
+T = native.TensorSpec
+_M2, _B1, _X4 = T((4, 5), "float32"), T((5,), "float32"), T((1, 2, 4, 5), "float32")
 ALL_DEMOS = [
-    matmul_inputs_static_tile_static_kernel,
-    matmul_inputs_static_tile_dynamic_kernel,
-    conv2d_inputs_static_tile_static_kernel,
-    conv2d_inputs_static_tile_dynamic_kernel,
-    conv2d_inputs_dynamic_tile_dynamic_kernel,
-    flash_attention_inputs_static_tile_static_kernel,
-    flash_attention_inputs_dynamic_tile_dynamic_kernel,
-    flash_attention_scaled_causal_kernel,
+    (matmul_inputs_static_tile_static_kernel, (_M2, _M2, _M2, None), "matmul"),
+    (matmul_inputs_static_tile_dynamic_kernel, (_M2, _M2, _M2, _B1, 2, 2, 2), "matmul"),
+    (conv2d_inputs_static_tile_static_kernel, (_X4, _X4, _X4, None), "conv2d"),
+    (conv2d_inputs_static_tile_dynamic_kernel, (_X4, _X4, _X4, _B1, 7, 18, 3, 9, 8), "conv2d"),
+    (conv2d_inputs_dynamic_tile_dynamic_kernel, (_X4, _X4, _X4, None) + (1,) * 8 + (7, 18, 3, 9, 8), "conv2d"),
+    (flash_attention_inputs_static_tile_static_kernel, (_X4,) * 4, "flash_attention"),
+    (flash_attention_inputs_dynamic_tile_dynamic_kernel, (_X4,) * 4 + (2, 2), "flash_attention"),
+    (flash_attention_scaled_causal_kernel, (_X4,) * 4 + (2, 2, 0.5), "flash_attention"),
 ]
+
+
+def lower(fn, *args, **options):
+    return get_pipeline("gfx950-lowering", options or None).run(mlir_gen(fn, args))
 
 
 def test_gfx950_target_spec():
@@ -77,42 +84,37 @@ def test_strategy_registry_phrases():
     assert err.value.failure_phrase == "compile_failed"  # duplicate without override
 
 
-def test_every_demo_has_a_pattern():
-    names = set(known_patterns())
-    for fn in ALL_DEMOS:
-        assert fn.__name__ in names
-        with pytest.raises(KernelCodeError):
-            fn(None, None, None, None) if fn.__code__.co_argcount == 4 else fn(*([None] * fn.__code__.co_argcount))
-
-
-@pytest.mark.parametrize("fn", ALL_DEMOS, ids=lambda f: f.__name__)
-def test_generated_sources(fn):
-    lowered, source = run_lowering_demo("case", fn)
+@pytest.mark.parametrize("fn,args,family", ALL_DEMOS, ids=lambda v: getattr(v, "__name__", ""))
+def test_generated_sources(fn, args, family):
+    lowered, source = run_lowering_demo("case", fn, *args)
+    assert lowered.fused is not None and lowered.fused.family == family
     assert source.startswith("// __KG_BUNDLE_FILE__:kernel.hip")
-    assert 'extern "C" int kg_execute_entry(const KgArgSlot* ordered_args, unsigned long long arg_count)' in source
-    assert lowered.pattern.library_entry in source
-    assert f"arg_count != {len(lowered.pattern.params)}ULL" in source
+    assert 'extern "C" int kg_execute_entry(const KgArgSlot* s, unsigned long long n)' in source
+    assert f"kg_gfx950_{family}_entry(slots," in source
+    assert f"n != {len(args)}ULL" in source
     assert lowered.hardware["subthread_num"] == 64
+    assert "kernel-pattern-fuse" in lowered.applied
     files = unbundle(source)
     assert set(files) == {"kernel.hip"}
+    # the per-operation path renders the same kernel as one HIP kernel of kg_tile calls
+    per_op = gen_kernel(lower(fn, *args, fuse="false"))
+    assert "kg_gfx950_generated_kernel" in per_op and "kg_tile::" in per_op and "kg_gfx950_" + family not in per_op
 
 
 def test_static_demo_constants_are_baked():
-    src = gen_kernel(recognise(conv2d_inputs_static_tile_static_kernel))
-    # stride 8 and the seeded pads/tiles of kernel/conv2d/inputs_static_tile_static.py
+    # stride 8 and the seeded pads of kernel/conv2d/inputs_static_tile_static.py: (3, 3, 4, 0)
+    lowered = lower(conv2d_inputs_static_tile_static_kernel, _X4, _X4, _X4, None)
+    src = gen_kernel(lowered)
     assert "slots[4].int_value = 8LL;" in src and "slots[5].int_value = 8LL;" in src
-    p = recognise(conv2d_inputs_static_tile_static_kernel)
-    baked = dict(p.baked)
-    assert (baked["pad_top"], baked["pad_bottom"], baked["pad_left"], baked["pad_right"]) == (3, 3, 4, 0)
-    assert (baked["tile_f"], baked["tile_c"], baked["tile_n"], baked["tile_ho"], baked["tile_wo"]) == (7, 18, 3, 9, 8)
-    mm = dict(recognise(matmul_inputs_static_tile_static_kernel).baked)
-    assert (mm["tile_m"], mm["tile_n"], mm["tile_k"]) == (48, 80, 56)
-    fa = gen_kernel(recognise(flash_attention_scaled_causal_kernel, "bfloat16"))
+    assert "slots[8].int_value = 3LL;" in src and "slots[10].int_value = 4LL;" in src
+    mm = lower(matmul_inputs_static_tile_static_kernel, _M2, _M2, _M2, None).fused
+    assert tuple(t.value for t in mm.ints) == (48, 80, 56)
+    fa = gen_kernel(lower(flash_attention_scaled_causal_kernel, *((T((1, 2, 8, 64), "bfloat16"),) * 4), 64, 64, 0.1))
     assert "slots[7].int_value = 1LL;" in fa  # causal flag appended after the scale slot
 
 
 def test_allow_absent_metadata_roundtrip():
-    src = gen_kernel(recognise(matmul_inputs_static_tile_static_kernel))
+    src = gen_kernel(lower(matmul_inputs_static_tile_static_kernel, _M2, _M2, _M2, None))
     specs = parse_allow_absent(src)
     assert len(specs) == 1 and specs[0].index == 3 and specs[0].dtype == "float32" and specs[0].rank == 1
     with pytest.raises(KernelCodeError) as err:
@@ -126,6 +128,8 @@ def test_pipeline_registry_and_options():
         build_gfx950_lowering_pipeline({"target": "cuda_sm89"})
     with pytest.raises(KernelCodeError):
         build_gfx950_lowering_pipeline({"fold": "true"})
+    with pytest.raises(KernelCodeError):
+        build_gfx950_lowering_pipeline({"fuse": "maybe"})
 
 
 @pytest.mark.parametrize(
@@ -165,7 +169,7 @@ def _fake_hipcc(tmp_path: Path, rc: int = 0) -> Path:
 
 def test_fake_compiler_command_line(tmp_path):
     fake = _fake_hipcc(tmp_path)
-    src = gen_kernel(recognise(matmul_inputs_static_tile_dynamic_kernel))
+    src = gen_kernel(lower(matmul_inputs_static_tile_dynamic_kernel, _M2, _M2, _M2, None, 2, 2, 2))
     kernel = ExecutionEngine("gfx950", compiler=str(fake)).compile(source=src, function="matmul")
     argv = (tmp_path / "argv.log").read_text()
     assert "--offload-arch=gfx950" in argv and "-shared" in argv and "-fPIC" in argv and "-std=c++17" in argv
@@ -185,11 +189,13 @@ def test_fake_compiler_failure_phrase(tmp_path):
     assert err.value.failure_phrase == "compile_failed"
 
 
-def test_real_hipcc_builds_generated_source():
-    """hipcc cross-compiles the generated glue for gfx950 here (no GPU needed) and the
-    shared object exports kg_execute_entry; it is loaded but not executed."""
+@pytest.mark.parametrize("fuse", ["true", "false"])
+def test_real_hipcc_builds_generated_source(fuse):
+    """hipcc cross-compiles the generated source for gfx950 here (no GPU needed), fused
+    glue and per-operation kernel alike, and the shared object exports kg_execute_entry;
+    it is loaded but not executed."""
 
-    src = gen_kernel(recognise(flash_attention_inputs_static_tile_static_kernel))
+    src = gen_kernel(lower(flash_attention_inputs_static_tile_static_kernel, *((_X4,) * 4), fuse=fuse))
     kernel = ExecutionEngine("gfx950").compile(source=src, function="fa")
     try:
         lib = ctypes.CDLL(kernel.soname_path)
@@ -198,7 +204,8 @@ def test_real_hipcc_builds_generated_source():
         fn.restype = ctypes.c_int
         fn.argtypes = [ctypes.POINTER(native.KgArgSlot), ctypes.c_ulonglong]
         slots = (native.KgArgSlot * 3)()
-        assert fn(slots, 3) == -1  # arity check in the generated shim, before any GPU work
+        assert fn(slots, 3) == -1  # arity check in the generated entry, before any GPU work
+        assert "expects 4 slots" in native.last_error()
     finally:
         kernel.close()
 
@@ -245,16 +252,17 @@ def test_memory_stage_option_drives_matmul_ring_depth():
     reaches the matmul entry as a trailing INT slot; conv2d and attention are left alone."""
 
     pm = get_pipeline("gfx950-lowering", {"memory_stage": "3"})
-    for fn in (matmul_inputs_static_tile_static_kernel, matmul_inputs_static_tile_dynamic_kernel):
-        lowered = pm.run(recognise(fn, "bfloat16"))
-        assert "multi-buffer{memory-stage=3}" in lowered.applied
-        assert lowered.pattern.trailing[-1] == ("memory_stage", 3)
-        src = gen_kernel(lowered.pattern)
+    b16 = T((256, 256), "bfloat16")
+    for fn, extra in ((matmul_inputs_static_tile_static_kernel, ()), (matmul_inputs_static_tile_dynamic_kernel, (64, 64, 64))):
+        lowered = pm.run(mlir_gen(fn, (b16, b16, b16, None) + extra))
+        assert "multi-buffer{memory-stage=3}" in lowered.applied and lowered.memory_stage == 3
+        src = gen_kernel(lowered)
         assert "slots[7].int_value = 3LL;" in src and "kg_gfx950_matmul_entry(slots, 8ULL)" in src
-    fa = pm.run(recognise(flash_attention_scaled_causal_kernel, "bfloat16")).pattern
-    assert ("memory_stage", 3) not in fa.trailing
-    conv = pm.run(recognise(conv2d_inputs_static_tile_static_kernel)).pattern
-    assert ("memory_stage", 3) not in conv.trailing
+    x = T((1, 2, 64, 64), "bfloat16")
+    fa = pm.run(mlir_gen(flash_attention_scaled_causal_kernel, (x, x, x, x, 64, 64, 0.1)))
+    assert fa.memory_stage is None
+    conv = pm.run(mlir_gen(conv2d_inputs_static_tile_static_kernel, (_X4, _X4, _X4, None)))
+    assert conv.memory_stage is None
     for bad in ("1", "5", "two"):
         with pytest.raises(KernelCodeError):
             build_gfx950_lowering_pipeline({"memory_stage": bad})
