@@ -2,7 +2,7 @@
  * gfx950/kg_tile.h - device runtime of the per-operation gfx950 emitter.
  *
  * The reference renders every operation of a final IR as a call into its target's
- * runtime headers (include/npu_demo/{Kernel,Dma}.h for the host, include/cuda_sm89/*.h
+ * runtime headers (include/npu_demo/{Kernel,Dma}.h for the host, the include/cuda_sm89 headers
  * for its GPU sibling, where one thread of one block runs the whole body:
  * kernel_gen/dsl/gen_kernel/emit/cuda_sm89/source_bundle.py:615-620). This header is the
  * gfx950 counterpart used by kernels that the pattern pass does not map onto a
@@ -29,6 +29,10 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+// Every sum and product below is rounded on its own, in program order, as the reference's
+// host code computes it (no fused multiply-add).
+#pragma clang fp contract(off)
 
 namespace kg_tile {
 
@@ -266,8 +270,10 @@ __device__ void matmul(const View<TO, 2>& out, const View<TL, 2>& lhs, const Vie
     float a = acc ? ld(o) : 0.0f;
     const TL* l = lhs.p + m * lhs.stride[0];
     const TR* r = rhs.p + n * rhs.stride[1];
-    for (long long k = 0; k < K; ++k)
-      a = __fadd_rn(a, __fmul_rn(ld(l + k * lhs.stride[1]), ld(r + k * rhs.stride[0])));
+    for (long long k = 0; k < K; ++k) {
+      const float prod = ld(l + k * lhs.stride[1]) * ld(r + k * rhs.stride[0]);
+      a = a + prod;
+    }
     st(o, a);
   }
   sync();
@@ -337,7 +343,7 @@ __device__ void reduce_rows(const View<TO, 2>& out, const View<TI, 2>& in, int k
       }
     } else {
       a = 0.0f;
-      for (long long j = 0; j < cols; ++j) a = __fadd_rn(a, ld(row + j * in.stride[1]));
+      for (long long j = 0; j < cols; ++j) a = a + ld(row + j * in.stride[1]);
     }
     st(out.p + i * out.stride[0], a);
   }
@@ -363,9 +369,9 @@ __device__ void binary(const View<TO, R>& out, const View<TL, R>& lhs, const Vie
     const float b = ld(rhs.p + offset_of(rhs, i));
     float r;
     switch (kind) {
-      case 0: r = __fadd_rn(a, b); break;
-      case 1: r = __fsub_rn(a, b); break;
-      case 2: r = __fmul_rn(a, b); break;
+      case 0: r = a + b; break;
+      case 1: r = a - b; break;
+      case 2: r = a * b; break;
       case 3: r = (float)((double)a / (double)b); break;
       default: r = a > b ? a : b; break;
     }
