@@ -36,6 +36,8 @@ DTYPE_CODES = {"f32": 1, "f16": 5, "bf16": 6}
 BINARY_KIND = {"add": 0, "sub": 1, "mul": 2, "truediv": 3, "max": 4}
 ENUM_LIMIT = 4_000_000
 MAX_GRID = 2048
+SCRATCH_BYTES = 32 << 20  # scratch of the allocation-free entry, per GPU
+MAX_DEVICES = 64
 
 
 @dataclass
@@ -309,11 +311,15 @@ class _Emitter:
         f = self.func
         L: list[str] = []
         L.append("#include <hip/hip_runtime.h>")
+        L.append("#include <cstdio>")
+        L.append("#include <mutex>")
         L.append('#include "kg_gfx950.h"')
+        L.append('#include "gfx950/kg_generated.h"')
         L.append('#include "gfx950/kg_tile.h"')
         L.append("")
         L.append("namespace {")
         L.append("using kg_tile::kg_floordiv; using kg_tile::kg_max; using kg_tile::kg_min; using kg_tile::kg_mod;")
+        L.append(f"constexpr int kMaxDevices = {MAX_DEVICES};")
         L.append("")
         L.append("struct KgArgs {")
         for p in f.params:
@@ -365,14 +371,49 @@ class _Emitter:
         L.append("  }")
         L.append("}")
         L.append("")
-        L.append("}  // namespace")
+        L.append("__global__ void kg_gfx950_clear_word(int* w) {")
+        L.append("  if (threadIdx.x == 0) *w = 0;")
+        L.append("}")
         L.append("")
         L += self.entry(function)
         return "\n".join(L) + "\n"
 
     def entry(self, function: str) -> list[str]:
         f = self.func
-        L = [f'extern "C" int kg_execute_entry(const KgArgSlot* s, unsigned long long n) {{',
+        L = ["}  // namespace", "",
+             "// Scratch of kg_execute_entry_noalloc: device memory the library never allocates.",
+             "// Every GPU holds its own copy until the process ends; every call on a GPU shares it",
+             "// (so calls that overlap on one GPU race), and it keeps the last call's contents.",
+             f"static __device__ __align__(256) char scratch[{SCRATCH_BYTES}];",
+             "",
+             "namespace {",
+             f"constexpr long long kScratchBytes = {SCRATCH_BYTES}LL;",
+             "std::mutex g_scratch_mutex;",
+             "char* g_scratch[kMaxDevices] = {};",
+             "",
+             "// This device's address of `scratch` (looked up once per device, with it current):",
+             "// the host-side name of a __device__ array is not a device address.",
+             "int scratch_of_current_device(char** out) {",
+             "  int dev = 0;",
+             "  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {",
+             "    (void)hipGetLastError();",
+             f'    return kg_gfx950_fail(-2, "{function}: no current device for the scratch");',
+             "  }",
+             "  std::lock_guard<std::mutex> lock(g_scratch_mutex);",
+             "  if (g_scratch[dev] == nullptr) {",
+             "    void* p = nullptr;",
+             "    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));",
+             "    if (e != hipSuccess || p == nullptr) {",
+             "      (void)hipGetLastError();",
+             f'      return kg_gfx950_fail(-2, "{function}: hipGetSymbolAddress(scratch) failed");',
+             "    }",
+             "    g_scratch[dev] = static_cast<char*>(p);",
+             "  }",
+             "  *out = g_scratch[dev];",
+             "  return 0;",
+             "}",
+             "",
+             "int run(const KgArgSlot* s, unsigned long long n, bool no_alloc) {",
              f'  if (s == nullptr) return kg_gfx950_fail(-1, "ordered_args is null");',
              f'  if (n != {len(f.params)}ULL) return kg_gfx950_fail(-1, "{function} expects {len(f.params)} slots");',
              "  KgArgs a{};"]
@@ -416,29 +457,49 @@ class _Emitter:
         else:
             L.append("  const long long total = 1;")
         L.append("  if (total <= 0) return kg_gfx950_finish_launch(\"" + function + "(empty)\");")
-        L.append(f"  const long long grid = total < {MAX_GRID} ? total : {MAX_GRID};")
+        L.append(f"  long long grid = total < {MAX_GRID} ? total : {MAX_GRID};")
         L += [
             "  hipStream_t stream = static_cast<hipStream_t>(kg_gfx950_launch_stream());",
-            "  const size_t bytes = (size_t)(grid * a.ws_per_block) + 256;",
             "  char* ws = nullptr;",
-            "  if (hipMallocAsync(reinterpret_cast<void**>(&ws), bytes, stream) != hipSuccess) {",
-            "    (void)hipGetLastError();",
-            f'    return kg_gfx950_fail(-2, "{function}: workspace allocation failed");',
+            "  if (no_alloc) {",
+            "    // fewer workgroups when the scratch cannot give each its slice (the loop is block-strided)",
+            "    if (a.ws_per_block > kScratchBytes - 256) {",
+            "      char msg[256];",
+            f'      snprintf(msg, sizeof(msg), "{function}: %lld bytes of workspace per workgroup exceed the %lld-byte '
+            f'scratch of the allocation-free entry", a.ws_per_block, kScratchBytes - 256);',
+            "      return kg_gfx950_fail(-3, msg);",
+            "    }",
+            "    const long long fit = (kScratchBytes - 256) / (a.ws_per_block > 0 ? a.ws_per_block : 1);",
+            "    if (grid > fit) grid = fit;",
+            "    if (scratch_of_current_device(&ws) != 0) return -2;",
+            "  } else {",
+            "    const size_t bytes = (size_t)(grid * a.ws_per_block) + 256;",
+            "    if (hipMallocAsync(reinterpret_cast<void**>(&ws), bytes, stream) != hipSuccess) {",
+            "      (void)hipGetLastError();",
+            f'      return kg_gfx950_fail(-2, "{function}: workspace allocation failed");',
+            "    }",
             "  }",
             "  a.err = reinterpret_cast<int*>(ws + grid * a.ws_per_block);",
             "  a.ws = ws;",
-            "  hipMemsetAsync(a.err, 0, sizeof(int), stream);",
+            "  // the error word starts at zero: cleared by a kernel (no memset node if a caller captures the stream)",
+            "  hipLaunchKernelGGL(kg_gfx950_clear_word, dim3(1), dim3(64), 0, stream, a.err);",
             "  hipLaunchKernelGGL(kg_gfx950_generated_kernel, dim3((unsigned)grid), dim3(256), 0, stream, a);",
             "  int err_word = 0;",
             "  const bool sync = kg_gfx950_launch_synchronous() != 0;",
-            "  if (sync) hipMemcpyAsync(&err_word, a.err, sizeof(int), hipMemcpyDeviceToHost, stream);",
-            "  hipFreeAsync(ws, stream);",
-            f'  const int rc = kg_gfx950_finish_launch("{function}(per-op)");',
+            "  if (sync) (void)hipMemcpyAsync(&err_word, a.err, sizeof(int), hipMemcpyDeviceToHost, stream);",
+            "  if (!no_alloc) (void)hipFreeAsync(ws, stream);",
+            f'  const int rc = kg_gfx950_finish_launch(no_alloc ? "{function}(per-op, no-alloc)" : "{function}(per-op)");',
             "  if (rc != 0) return rc;",
             f'  if (sync && err_word != 0) return kg_gfx950_fail(-1, "{function}: an operation addressed memory '
             f'outside its view or got inconsistent shapes (error word set)");',
             "  return 0;",
             "}",
+            "",
+            "}  // namespace",
+            "",
+            'extern "C" int kg_execute_entry(const KgArgSlot* s, unsigned long long n) { return run(s, n, false); }',
+            "",
+            'extern "C" int kg_execute_entry_noalloc(const KgArgSlot* s, unsigned long long n) { return run(s, n, true); }',
         ]
         return L
 

@@ -206,6 +206,11 @@ def test_real_hipcc_builds_generated_source(fuse):
         slots = (native.KgArgSlot * 3)()
         assert fn(slots, 3) == -1  # arity check in the generated entry, before any GPU work
         assert "expects 4 slots" in native.last_error()
+        if fuse == "false":  # include/gfx950/kg_generated.h: the allocation-free entry too
+            assert hasattr(lib, "kg_execute_entry_noalloc")
+            lib.kg_execute_entry_noalloc.restype = ctypes.c_int
+            lib.kg_execute_entry_noalloc.argtypes = fn.argtypes
+            assert lib.kg_execute_entry_noalloc(slots, 3) == -1
     finally:
         kernel.close()
 
