@@ -15,7 +15,9 @@ floats are passed as INT / FLOAT slots.
 lowers to an npu_demo cost function whose kinds are DMA1..DMA4, MAC, VECTOR1, VECTOR2;
 here the library's kg_gfx950_cost runs the fused kernel's validation and kernel choice and
 reports MAC, MFMA (wave-level matrix instructions of the chosen kernel), HBM_READ and
-HBM_WRITE (compulsory bytes). Kernels on the per-operation path have no cost model.
+HBM_WRITE (compulsory bytes), and ROOFLINE_NS is the time those imply at MI355X's peaks
+(the lower bound any run of the call meets). Kernels on the per-operation path have no
+cost model.
 """
 
 from __future__ import annotations
@@ -38,8 +40,23 @@ from ..pipeline import PassManager, get_pipeline
 from ..pipeline.gfx950_lowering import LoweredKernel
 
 ARITY_ERROR = "DslRunArityMismatch: real_args count must match the kernel's positional parameters"
-VALID_DSL_COST_KINDS = ("MAC", "MFMA", "HBM_READ", "HBM_WRITE")
-DSL_COST_KIND_ERROR = "DslCostRunInvalidCostKind: cost_kind must be one of [MAC, MFMA, HBM_READ, HBM_WRITE]"
+VALID_DSL_COST_KINDS = ("MAC", "MFMA", "HBM_READ", "HBM_WRITE", "ROOFLINE_NS")
+DSL_COST_KIND_ERROR = ("DslCostRunInvalidCostKind: cost_kind must be one of [MAC, MFMA, HBM_READ, HBM_WRITE, "
+                       "ROOFLINE_NS]")
+# MI355X: 256 CUs x 4 SIMDs at 2.4 GHz; a 32x32x16 bf16/f16 MFMA occupies a SIMD 32 cycles,
+# a 32x32x2 fp32 MFMA 64; HBM3E moves 8 TB/s (8000 bytes per ns).
+SIMDS, CLOCK_GHZ, HBM_BYTES_PER_NS = 1024, 2.4, 8000.0
+MFMA_CYCLES = {"f32": 64, "f16": 32, "bf16": 32}
+
+
+def roofline_ns(costs: dict, dtype: str) -> int:
+    """The time below which no kernel can finish the call: the larger of its matrix-core
+    time (MFMA instructions x cycles each, spread over every SIMD at the peak clock) and its
+    compulsory HBM traffic at peak bandwidth, in ns (rounded up)."""
+
+    mfma_ns = costs["MFMA"] * MFMA_CYCLES[dtype] / SIMDS / CLOCK_GHZ
+    hbm_ns = (costs["HBM_READ"] + costs["HBM_WRITE"]) / HBM_BYTES_PER_NS
+    return int(-(-max(mfma_ns, hbm_ns) // 1))
 DSL_COST_TARGET_ERROR = "DslCostRunInvalidTarget: dsl_cost_run only supports target 'gfx950'"
 DSL_COST_OUTPUT_ERROR = "DslCostRunInvalidOutput: cost query was rejected by the gfx950 library"
 _COMPILED: dict[str, CompiledKernel] = {}
@@ -209,4 +226,6 @@ def dsl_cost_run(func_obj: Callable, real_args: tuple | list, pipeline: str | Pa
         costs = native.cost(lowered.fused.family, slots)
     except native.NativeLibraryError as exc:
         raise _error(f"{DSL_COST_OUTPUT_ERROR}: {exc}") from exc
+    if cost_kind == "ROOFLINE_NS":
+        return roofline_ns(costs, lowered.func.param(lowered.fused.memory[0]).dtype)
     return costs[cost_kind]

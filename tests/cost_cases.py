@@ -61,7 +61,9 @@ def modelled(case) -> dict[str, int]:
     return native.cost(family, _slots(family, [native.TensorSpec(s, dtype) for s in shapes], scalars))
 
 
-def run(case, device: str = "cuda") -> None:
+def prepare(case, device: str = "cuda"):
+    """(entry name, slot args) of a case, with its tensors made on the host and copied."""
+
     import torch
 
     name, family, dtype, shapes, scalars = case
@@ -71,7 +73,12 @@ def run(case, device: str = "cuda") -> None:
     torch.cuda.synchronize()
     entry = {"matmul": "kg_gfx950_matmul_entry", "conv2d": "kg_gfx950_conv2d_entry",
              "flash_attention": "kg_gfx950_flash_attention_entry"}[family]
-    native.call_entry(entry, _slots(family, tensors, scalars))
+    return entry, _slots(family, tensors, scalars)
+
+
+def run(case, device: str = "cuda") -> None:
+    entry, args = prepare(case, device)
+    native.call_entry(entry, args)
 
 
 def main(argv: list[str] | None = None) -> int:

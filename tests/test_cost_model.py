@@ -207,3 +207,19 @@ def test_mfma_model_matches_hardware_counter():
     for case in CASES:
         kernel, counted, model_then = rows[case[0]]
         assert modelled(case)["MFMA"] == model_then == counted, case[0]
+
+
+def test_roofline_kind():
+    """ROOFLINE_NS: the larger of the MFMA time at the 2.4 GHz peak (32 cycles per 16-bit
+    32x32x16 MFMA, 64 per fp32 32x32x2, over 1024 SIMDs) and the compulsory bytes at 8 TB/s."""
+
+    b16 = T((4096, 4096), "bfloat16")
+    c2 = dsl_cost_run(matmul_inputs_dynamic_tile_dynamic_kernel, (b16, b16, b16, None, 64, 64, 64), PIPE, "ROOFLINE_NS")
+    assert c2 == -(-4194304 * 32 // (1024 * 2.4)) == 54614  # 2 x 4096^3 FLOP at 2516.6 TFLOP/s
+    x = T((32, 64, 56, 56), "float16")
+    w = T((64, 64, 3, 3), "float16")
+    conv = dsl_cost_run(conv2d_inputs_dynamic_tile_dynamic_kernel, (x, x, w, None) + (1,) * 8 + (8, 8, 8, 8, 8), PIPE,
+                        "ROOFLINE_NS")
+    mfma_ns = 258048 * 32 / 1024 / 2.4
+    bytes_ns = (2 * 32 * 64 * 56 * 56 * 2 + 64 * 64 * 9 * 2) / 8000
+    assert conv == int(-(-max(mfma_ns, bytes_ns) // 1))

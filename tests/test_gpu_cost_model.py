@@ -1,0 +1,56 @@
+"""The cost model against the GPU (the gfx950 analogue of dsl_cost_run,
+kernel_gen/tools/dsl_run.py:656-730): every case of tests/cost_cases.py (each kernel choice
+of the library) is run and timed with HIP events, and
+
+  - the modelled MFMA instructions carry at least the operation's FLOP (2 per MAC; 32768
+    per 32x32x16 16-bit MFMA, 4096 per 32x32x2 fp32 MFMA), exactly on exact-tile shapes;
+  - no case runs faster than its ROOFLINE_NS (matrix-core time of the modelled MFMAs at the
+    2.4 GHz peak clock, or compulsory HBM bytes at 8 TB/s), less 10 % for timer resolution;
+  - cases whose roofline is at least 20 us run within 4x of it (the stated band: these
+    kernels reach 25 % or more of the roofline; the counted instruction totals themselves
+    are pinned by profiles/mfma_instruction_counts.txt).
+"""
+
+from __future__ import annotations
+
+import pytest
+
+from kernelcode_generate_amd import native
+from kernelcode_generate_amd.tools import roofline_ns
+from tests.cost_cases import CASES, modelled, prepare
+
+pytestmark = pytest.mark.gpu
+FLOP_PER_MFMA = {"float32": 4096, "bfloat16": 32768, "float16": 32768}
+EXACT = {"gemm_bf16_4096", "gemm_bf16_c2s_8192x1024x4096", "gemm_f16_512x768x256", "gemm_f32_256",
+         "gemm_f32_splitk_512x512x4096", "gemm_f32_mfma_1024x256x1024", "fa_bf16_c4"}
+SHORT = {"float32": "f32", "bfloat16": "bf16", "float16": "f16"}
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_cost_model_against_the_gpu(device, case):
+    import torch
+
+    name, family, dtype = case[0], case[1], case[2]
+    model = modelled(case)
+    if model["MFMA"]:
+        assert model["MFMA"] * FLOP_PER_MFMA[dtype] >= 2 * model["MAC"], name
+        if name in EXACT:
+            assert model["MFMA"] * FLOP_PER_MFMA[dtype] == 2 * model["MAC"], name
+    roof = roofline_ns(model, SHORT[dtype])
+    print(f"[cost] {name}: roofline {roof} ns", flush=True)
+    entry, args = prepare(case)
+    native.call_entry(entry, args)  # warm
+    times = []
+    for _ in range(5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        native.call_entry(entry, args)
+        e1.record()
+        e1.synchronize()
+        times.append(e0.elapsed_time(e1) * 1e6)
+    measured = sorted(times)[len(times) // 2]
+    print(f"[cost] {name}: measured {measured:.0f} ns ({roof / measured:.2f} of the roofline)", flush=True)
+    assert measured >= 0.9 * roof, f"{name}: {measured:.0f} ns beats the modelled roofline {roof} ns"
+    if roof >= 20_000:
+        assert measured <= 4 * roof, f"{name}: {measured:.0f} ns is more than 4x the roofline {roof} ns"
+    assert native.last_error() == ""
