@@ -110,12 +110,21 @@ def read_traffic(path: Path):
     return float(m.group(1)) if m else None
 
 
+# "zeros": analysis mode (--only runs): the GEMM lines run on all-zero operands. The kernel,
+# its instruction stream and its memory traffic are unchanged; only the switching activity of
+# the data, and with it the power the part draws and the clock it holds, differ.
+GEMM_OPERANDS = ["random"]
+
+
 def gemm_workload(dev, m: int, n: int, k: int, seed: int):
     import torch
 
     g = torch.Generator(device=dev).manual_seed(seed)
     a = (torch.randn(m, k, generator=g, device=dev) * 0.02).to(torch.bfloat16)
     b = (torch.randn(k, n, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    if GEMM_OPERANDS[0] == "zeros":
+        a.zero_()
+        b.zero_()
     c = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
     return a, b, c
 
@@ -303,13 +312,14 @@ def c1(dev, add, steps):
 
 def c2(dev, add, steps):
     a, b, c = gemm_workload(dev, 4096, 4096, 4096, 20261202)
-    add("C2 bf16 matmul M=N=K=4096", 2 * 4096**3, PreparedCall("kg_gfx950_matmul_entry", (c, a, b, None)),
+    add("C2 bf16 matmul M=N=K=4096" + ("" if GEMM_OPERANDS[0] == "random" else " (zero operands)"), 2 * 4096**3, PreparedCall("kg_gfx950_matmul_entry", (c, a, b, None)),
         PEAK_BF16_TFLOPS, max(steps, 200))
 
 
 def c2s(dev, add, steps):
     a, b, c = gemm_workload(dev, 8192, 1024, 4096, 20261203)
-    add("C2' bf16 matmul M=8192 N=1024 K=4096", 2 * 8192 * 1024 * 4096,
+    add("C2' bf16 matmul M=8192 N=1024 K=4096" + ("" if GEMM_OPERANDS[0] == "random" else " (zero operands)"),
+        2 * 8192 * 1024 * 4096,
         PreparedCall("kg_gfx950_matmul_entry", (c, a, b, None)), PEAK_BF16_TFLOPS, max(steps, 200))
 
 
@@ -384,6 +394,8 @@ def main() -> int:
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--only", nargs="+", choices=PROFILE_KEYS,
                     help="profiling aid: run only these secondary workloads (no headline GEMM, no CPU baseline)")
+    ap.add_argument("--operands", choices=("random", "zeros"), default="random",
+                    help="with --only: run the GEMM lines on all-zero operands (power/clock analysis)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (reference point for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -394,6 +406,11 @@ def main() -> int:
             file=sys.stderr,
         )
         return 2
+
+    if args.operands != "random" and not args.only:
+        print("--operands zeros is an analysis mode for --only runs; the headline uses random operands", file=sys.stderr)
+        return 2
+    GEMM_OPERANDS[0] = args.operands
 
     import torch
 
