@@ -396,6 +396,9 @@ def main() -> int:
                     help="profiling aid: run only these secondary workloads (no headline GEMM, no CPU baseline)")
     ap.add_argument("--operands", choices=("random", "zeros"), default="random",
                     help="with --only: run the GEMM lines on all-zero operands (power/clock analysis)")
+    ap.add_argument("--mfma-ceiling", action="store_true",
+                    help="analysis mode: the sustained MFMA rate with no operand movement, random and zero bf16 "
+                         "operands (kg_gfx950_mfma_rate), as one JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (reference point for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -420,6 +423,19 @@ def main() -> int:
     native.load_library()
     stream = torch.cuda.current_stream()
     native.set_launch_mode(False, stream.cuda_stream)
+    if args.mfma_ceiling:
+        rates = {}
+        for zeros in (False, True):
+            r = native.mfma_rate("bf16", zeros)
+            key = "zero_operands" if zeros else "random_operands"
+            rates[key] = {"tflops": round(r["tflops"], 1), "clock_ghz": round(r["clock_ghz"], 3),
+                          "frac_of_peak": round(r["tflops"] / PEAK_BF16_TFLOPS, 4)}
+            log(f"[bench] mfma ceiling, bf16 {key}: {r['tflops']:.1f} TFLOP/s at {r['clock_ghz']:.3f} GHz")
+        print(json.dumps({"mfma_ceiling": rates, "peak": PEAK_BF16_TFLOPS,
+                          "kernel": "back-to-back v_mfma_f32_32x32x16_bf16 on register operands, 2048 workgroups x 4 waves"}),
+              flush=True)
+        native.set_launch_mode(True, None)
+        return 0
     if args.only:
         print(json.dumps({"secondary": secondary(dev, args.steps, args.warmup, args.only)}), flush=True)
         native.set_launch_mode(True, None)

@@ -139,6 +139,18 @@ const char* kg_gfx950_last_error(void);
 /* ABI revision of this library (bumped on any slot-contract change). */
 int kg_gfx950_abi_version(void);
 
+/*
+ * Measurement aid (no counterpart in the reference): the sustained rate of
+ * v_mfma_f32_32x32x16_{bf16,f16} with no operand movement. `workgroups` workgroups of 4 waves
+ * each load 8 operand registers once (N(0,1)*0.02 values, or zeros when zero_operands != 0)
+ * and issue `iterations` x 8 back-to-back MFMAs into 4 accumulators; after two untimed launches
+ * one launch is timed with HIP events. Writes the achieved TFLOP/s and the median clock the
+ * workgroups saw (s_memtime ticks per s_memrealtime tick x 100 MHz). Allocates and frees its
+ * own device buffers; synchronous on the null stream. 0, -1 (bad arguments) or -2 (HIP error).
+ */
+int kg_gfx950_mfma_rate(int dtype_code, int zero_operands, int iterations, int workgroups, double* tflops,
+                        double* clock_ghz);
+
 /* Operations and cost kinds of kg_gfx950_cost. */
 enum {
   KG_OP_MATMUL = 1,

@@ -11,6 +11,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <vector>
 
 #include "kg_gfx950.h"
 #include "kg_gfx950/common.h"
@@ -22,6 +23,7 @@
 #include "kg_gfx950/conv2d_igemm.h"
 #include "kg_gfx950/flash_attn_mfma.h"
 #include "kg_gfx950/flash_attn_f32.h"
+#include "kg_gfx950/mfma_rate.h"
 
 namespace {
 
@@ -731,5 +733,81 @@ int kg_gfx950_cost(int op, const KgArgSlot* ordered_args, unsigned long long arg
 }
 
 int kg_gfx950_abi_version(void) { return 1; }
+
+int kg_gfx950_mfma_rate(int dtype_code, int zero_operands, int iterations, int workgroups, double* tflops,
+                        double* clock_ghz) {
+  if (dtype_code != KG_DTYPE_BF16 && dtype_code != KG_DTYPE_F16)
+    return fail(kInvalid, "mfma_rate: dtype must be bf16 or f16, got %s", dtype_name(dtype_code));
+  if (iterations < 1 || iterations > (1 << 20) || workgroups < 1 || workgroups > (1 << 16))
+    return fail(kInvalid, "mfma_rate: iterations must be in [1, 2^20] and workgroups in [1, 65536]");
+  if (tflops == nullptr || clock_ghz == nullptr) return fail(kInvalid, "mfma_rate: null output");
+  // operands: N(0,1)*0.02 (Box-Muller on a fixed 64-bit LCG) rounded to the 16-bit format, or zeros
+  std::vector<uint16_t> host(kMfmaRateOperands * 8, 0);
+  if (!zero_operands) {
+    unsigned long long st = 0x9E3779B97F4A7C15ull;
+    auto uni = [&]() {
+      st = st * 6364136223846793005ull + 1442695040888963407ull;
+      return ((st >> 11) + 0.5) * (1.0 / 9007199254740992.0);
+    };
+    for (size_t i = 0; i < host.size(); ++i) {
+      const float v = (float)(0.02 * std::sqrt(-2.0 * std::log(uni())) * std::cos(6.283185307179586 * uni()));
+      uint32_t bits;
+      std::memcpy(&bits, &v, 4);
+      if (dtype_code == KG_DTYPE_BF16) {
+        host[i] = (uint16_t)((bits + 0x7fffu + ((bits >> 16) & 1u)) >> 16);
+      } else {
+        const _Float16 hv = (_Float16)v;
+        std::memcpy(&host[i], &hv, 2);
+      }
+    }
+  }
+  u32x4* d_ops = nullptr;
+  unsigned long long* d_times = nullptr;
+  float* d_sink = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  int rc = kOk;
+  auto check = [&](hipError_t e, const char* what) {
+    if (e != hipSuccess && rc == kOk) rc = fail(kHipFailure, "mfma_rate: %s: %s", what, hipGetErrorString(e));
+    return e == hipSuccess;
+  };
+  const size_t sink_n = (size_t)workgroups * kMfmaRateThreads;
+  if (check(hipMalloc(&d_ops, host.size() * 2), "hipMalloc") && check(hipMalloc(&d_times, (size_t)workgroups * 16), "hipMalloc") &&
+      check(hipMalloc(&d_sink, sink_n * 4), "hipMalloc") &&
+      check(hipMemcpy(d_ops, host.data(), host.size() * 2, hipMemcpyHostToDevice), "hipMemcpy") &&
+      check(hipEventCreate(&e0), "hipEventCreate") && check(hipEventCreate(&e1), "hipEventCreate")) {
+    auto launch = [&]() {
+      if (dtype_code == KG_DTYPE_BF16)
+        hipLaunchKernelGGL(mfma_rate_kernel<Bf16Tag>, dim3(workgroups), dim3(kMfmaRateThreads), 0, nullptr, d_ops, d_times,
+                           d_sink, iterations);
+      else
+        hipLaunchKernelGGL(mfma_rate_kernel<F16Tag>, dim3(workgroups), dim3(kMfmaRateThreads), 0, nullptr, d_ops, d_times,
+                           d_sink, iterations);
+      return hipGetLastError();
+    };
+    float ms = 0.f;
+    // two untimed launches (the clock settles under the load), then one timed
+    if (check(launch(), "launch") && check(launch(), "launch") && check(hipEventRecord(e0, nullptr), "hipEventRecord") &&
+        check(launch(), "launch") && check(hipEventRecord(e1, nullptr), "hipEventRecord") &&
+        check(hipEventSynchronize(e1), "hipEventSynchronize") && check(hipEventElapsedTime(&ms, e0, e1), "hipEventElapsedTime")) {
+      std::vector<unsigned long long> times((size_t)workgroups * 2);
+      if (check(hipMemcpy(times.data(), d_times, times.size() * 8, hipMemcpyDeviceToHost), "hipMemcpy")) {
+        std::vector<double> ghz;
+        for (int b = 0; b < workgroups; ++b)
+          if (times[2 * b + 1] > 0) ghz.push_back((double)times[2 * b] / (double)times[2 * b + 1] * 0.1);
+        std::sort(ghz.begin(), ghz.end());
+        *clock_ghz = ghz.empty() ? 0.0 : ghz[ghz.size() / 2];
+        const double flop = (double)workgroups * (kMfmaRateThreads / 64) * iterations * 8 * 32768.0;
+        *tflops = ms > 0.f ? flop / (ms * 1e-3) / 1e12 : 0.0;
+      }
+    }
+  }
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  if (d_ops) (void)hipFree(d_ops);
+  if (d_times) (void)hipFree(d_times);
+  if (d_sink) (void)hipFree(d_sink);
+  if (rc == kOk) g_last_error[0] = '\0';
+  return rc;
+}
 
 }  // extern "C"

@@ -49,6 +49,7 @@ CONTROL_SYMBOLS = (
     "kg_gfx950_launch_stream",
     "kg_gfx950_launch_synchronous",
     "kg_gfx950_finish_launch",
+    "kg_gfx950_mfma_rate",
 )
 
 # kg_gfx950_cost: op codes (KG_OP_*) and the order of its output array (KG_COST_*).
@@ -119,6 +120,9 @@ def load_library() -> ctypes.CDLL:
     lib.kg_gfx950_cost.argtypes = [ctypes.c_int, ctypes.POINTER(KgArgSlot), ctypes.c_ulonglong,
                                    ctypes.POINTER(ctypes.c_longlong)]
     lib.kg_gfx950_cost.restype = ctypes.c_int
+    lib.kg_gfx950_mfma_rate.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                        ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
+    lib.kg_gfx950_mfma_rate.restype = ctypes.c_int
     _LIBRARY = lib
     return lib
 
@@ -241,6 +245,19 @@ def set_launch_mode(synchronous: bool, stream: int | None = None) -> None:
     """synchronous=True: each entry waits for its kernel. False: enqueue on ``stream``."""
 
     load_library().kg_gfx950_set_launch_mode(1 if synchronous else 0, ctypes.c_void_p(stream or 0))
+
+
+def mfma_rate(dtype: str = "bf16", zero_operands: bool = False, iterations: int = 20000,
+              workgroups: int = 2048) -> dict[str, float]:
+    """Sustained v_mfma_f32_32x32x16 rate with no operand movement (kg_gfx950_mfma_rate)."""
+
+    code = {"bf16": DTYPE_CODES["bfloat16"], "f16": DTYPE_CODES["float16"]}[dtype]
+    tf, ghz = ctypes.c_double(0.0), ctypes.c_double(0.0)
+    rc = load_library().kg_gfx950_mfma_rate(code, int(bool(zero_operands)), int(iterations), int(workgroups),
+                                            ctypes.byref(tf), ctypes.byref(ghz))
+    if rc != 0:
+        raise NativeLibraryError(f"kg_gfx950_mfma_rate failed: {last_error()}", rc)
+    return {"tflops": tf.value, "clock_ghz": ghz.value}
 
 
 def matmul(out, lhs, rhs, bias=None, *tiles: int) -> None:

@@ -70,3 +70,17 @@ def test_wrong_slot_kind_is_rejected_without_gpu():
     arr, keep = native.marshal_slots((1, 2, 3, None))
     assert lib.kg_gfx950_matmul_entry(arr, 4) == -1
     assert "expected memory slot" in native.last_error()
+
+
+def test_mfma_rate_rejects_bad_arguments():
+    """kg_gfx950_mfma_rate validates before touching the GPU: no device is needed here."""
+    import ctypes
+
+    from kernelcode_generate_amd import native
+
+    lib = native.load_library()
+    tf, ghz = ctypes.c_double(0.0), ctypes.c_double(0.0)
+    assert lib.kg_gfx950_mfma_rate(1, 0, 10, 4, ctypes.byref(tf), ctypes.byref(ghz)) == -1  # fp32: not an MFMA 16-bit type
+    assert "bf16 or f16" in native.last_error()
+    assert lib.kg_gfx950_mfma_rate(6, 0, 0, 4, ctypes.byref(tf), ctypes.byref(ghz)) == -1
+    assert lib.kg_gfx950_mfma_rate(6, 0, 10, 1 << 17, ctypes.byref(tf), ctypes.byref(ghz)) == -1

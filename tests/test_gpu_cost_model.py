@@ -62,3 +62,14 @@ def test_cost_model_against_the_gpu(device, case):
     if roof >= 20_000:
         assert measured <= 4 * roof, f"{name}: {measured:.0f} ns is more than 4x the roofline {roof} ns"
     assert native.last_error() == ""
+
+
+@pytest.mark.gpu
+def test_mfma_rate_measures_the_matrix_cores(device):
+    """kg_gfx950_mfma_rate: a short run gives a rate below the nominal dense peak and above a
+    tenth of it, for both operand kinds, and a clock within the part's range."""
+    for zeros in (False, True):
+        r = native.mfma_rate("bf16", zeros, iterations=2000, workgroups=1024)
+        print(f"[mfma_rate] zeros={zeros}: {r['tflops']:.0f} TFLOP/s at {r['clock_ghz']:.2f} GHz", flush=True)
+        assert 0.1 * 2516.6 < r["tflops"] < 2516.6
+        assert 0.5 < r["clock_ghz"] < 2.6
