@@ -78,7 +78,8 @@ __host__ __device__ constexpr int v_mask(int key) {
 
 // Copy instruction p of wave w covers tile rows (w*PW + p)*RPP + lane/DCH. K keeps a
 // per-lane HBM offset for every p; V keeps the one of p = 0 and moves the wave-uniform base
-// by whole KiB, which needs the V masks of the rows to repeat.
+// by whole KiB, which needs the V masks of the rows to repeat (the tail tile uses the same
+// offsets).
 template <int D, int W>
 constexpr bool v_copy_masks_repeat() {
   constexpr int RB = 2 * D, PW = kBC * RB / 1024 / W, RPP = 1024 / RB, DCH = D / 8;
@@ -174,10 +175,13 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
   auto copy_piece = [&](const char* src, int t, uint32_t lds_buf, bool kV, int p) {
     const int n0 = t * kBC;
     const uint32_t m = lds_buf + (wave * PW + p) * 1024;
-    if (kMasked && n0 + kBC > s_kv) {  // tail tile: rows past s_kv repeat the last key (masked in S)
-      const int row = c_row0 + p * RPP;
-      const int mask = kV ? v_mask<D>(row) : k_mask<D>(row);
-      g2lds16_m(src + (long long)min(n0 + row, s_kv - 1) * RB + 16 * (c_slot ^ mask), m);
+    if constexpr (kMasked) {
+      // ragged S: every tile through a raw buffer resource that ends at row s_kv, so the rows
+      // of the tail tile past s_kv land zeros (their scores are masked in S: P is 0 there)
+      const char* base = src + (long long)n0 * RB + (kV ? p * 1024 : 0);
+      const long long left = (long long)(s_kv - n0) * RB - (kV ? p * 1024 : 0);
+      const uint32_t range = (uint32_t)max(0ll, min(left, (long long)TB));
+      buf2lds16_r(kV ? v_goff : k_goff[p], base, range, m);
     } else {
       const char* base = src + (long long)n0 * RB;
       if (kV) g2lds16_s(v_goff, base + p * 1024, m);
@@ -246,16 +250,26 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
     const int n0 = t * kBC;
     return (kMasked && n0 + kBC > s_kv) || (kCausal && n0 + kBC - 1 > wave_q_lo);
   };
+  // Ragged S: keys past key_lim_h + 16*half are dead, past s_kv or (causal) past the query;
+  // one limit per lane keeps the masked variants within their registers. Unmasked causal
+  // kernels compare each key with the query row.
+  const int key_lim_h = (kCausal ? min(q_row, s_kv - 1) : s_kv - 1) - 16 * half;
   auto apply_mask = [&](f32x16(&s)[2], int t) {
-    const int key0 = t * kBC + 16 * half;
+    if constexpr (kMasked) {
+      const int rel = key_lim_h - t * kBC;  // element i of block kb is dead if 32kb + i > rel
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int key = key0 + 32 * kb + i;
-        const bool dead = (kMasked && key >= s_kv) || (kCausal && key > q_row);
-        if (dead) s[kb][i] = -INFINITY;
-      }
+        for (int i = 0; i < 16; ++i)
+          if (32 * kb + i > rel) s[kb][i] = -INFINITY;
+    } else {
+      const int key0 = t * kBC + 16 * half;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (kCausal && key0 + 32 * kb + i > q_row) s[kb][i] = -INFINITY;
+    }
   };
   // max op k (0..15) over the 32 scores of a lane: v_maximum3_f32 chains
   auto max_op = [&](const f32x16(&s)[2], int k, float& mx) {
@@ -418,8 +432,14 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
   }
 
   const float inv = 1.f / halves_sum(l_run);
-  if (!kMasked || q_row < s_q) {
-    uint16_t* orow = Oh + (long long)q_row * D;
+  // masked variants take the output row and lane half from the lane id again: kept live
+  // across the loop they would take registers the loop needs (the compiler cannot tie
+  // __lane_id() to threadIdx.x)
+  const int lane_out = kMasked ? (int)__lane_id() : lane;
+  const int q_out = kMasked ? m0 + 32 * wave + (lane_out & 31) : q_row;
+  const int half_out = kMasked ? lane_out >> 5 : half;
+  if (!kMasked || q_out < s_q) {
+    uint16_t* orow = Oh + (long long)q_out * D;
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -428,7 +448,7 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
         u32x2 packed;
         packed[0] = H::pack2(o[db][4 * jj] * inv, o[db][4 * jj + 1] * inv);
         packed[1] = H::pack2(o[db][4 * jj + 2] * inv, o[db][4 * jj + 3] * inv);
-        st8(orow + 32 * db + 8 * jj + 4 * half, packed);
+        st8(orow + 32 * db + 8 * jj + 4 * half_out, packed);
       }
   }
 }

@@ -84,6 +84,25 @@ __device__ __forceinline__ void buf2lds16_s(uint32_t voff, const void* sbase, ui
       : "memory", "m0");
 }
 
+// Same copy through a raw buffer resource over [sbase, sbase + range) bytes (range a multiple
+// of 16, at most kBufRange): a lane whose voff lies at or past range reads nothing and lands
+// zeros in LDS.
+__device__ __forceinline__ void buf2lds16_r(uint32_t voff, const void* sbase, uint32_t range, uint32_t m0) {
+  const uint64_t p = (uint64_t)(uintptr_t)sbase;
+  u32x4 rsrc;
+  rsrc[0] = (uint32_t)p;
+  rsrc[1] = (uint32_t)(p >> 32);
+  rsrc[2] = range;
+  rsrc[3] = 0x00020000u;
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %0, %1, 0 offen lds"
+      :
+      : "v"(voff), "s"(rsrc), "s"(m0)
+      : "memory", "m0");
+}
+
 // LDS byte address of a shared-memory object (what M0 and ds_* addresses take).
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
