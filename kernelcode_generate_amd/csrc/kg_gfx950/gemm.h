@@ -33,6 +33,10 @@ namespace kg_gfx950 {
 //   epilogue stores only the rows and columns inside the matrix; the loop is unchanged.
 //   Host requirements: K % 8 == 0, N % 8 == 0, row strides multiples of 8 and at most
 //   2^22 elements, 16-byte aligned base pointers.
+//   Split-K (k_chunk > 0, for outputs of few tiles): workgroup row blockIdx.y runs the K range
+//   [y*k_chunk, min(K, (y+1)*k_chunk)) as a GEMM of its own and stores its fp32 sums to
+//   partial[y][M][N] (no bias); gemm_splitk_reduce_kernel adds the rows in y order, adds the
+//   bias and rounds once.
 namespace gemmp {
 constexpr int kBM = 256;  // largest tile height (kTM)
 constexpr int kBN = 256;
@@ -55,10 +59,18 @@ struct StageIdx {
 template <typename Tag, int kBias, int kTM, int kStages, bool kRagged>
 __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, uint16_t* __restrict__ C,
-    const void* __restrict__ bias, int M, int N, int K, long long lda, long long ldb, long long ldc) {
+    const void* __restrict__ bias, int M, int N, int K, long long lda, long long ldb, long long ldc,
+    float* __restrict__ partial, int k_chunk) {
   using namespace gemmp;
   using H = Half16<Tag>;
   static_assert(kTM == 256 || kTM == 128, "tile height");
+  if (k_chunk > 0) {  // split-K: this workgroup row's K range, as a GEMM of its own
+    const int k_begin = blockIdx.y * k_chunk;
+    A += k_begin;
+    B += (long long)k_begin * ldb;
+    K = min(k_chunk, K - k_begin);
+    partial += (long long)blockIdx.y * M * N;
+  }
   static_assert(kStages >= 2 && kStages <= 4, "ring depth");
   constexpr int MI = kTM / 64;              // 32-row fragments per wave
   constexpr int AP = kTM / 128;             // lhs copies per wave per slice
@@ -275,6 +287,10 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
         const int n = n0 + wn * 64 + j * 32 + 8 * q + 4 * frag_half;
         if (kRagged && (m >= M || n >= N)) continue;  // N % 8 == 0: n < N covers n .. n+3
         float v0 = acc[i][j][4 * q], v1 = acc[i][j][4 * q + 1], v2 = acc[i][j][4 * q + 2], v3 = acc[i][j][4 * q + 3];
+        if (k_chunk > 0) {
+          *reinterpret_cast<f32x4*>(partial + (long long)m * N + n) = f32x4{v0, v1, v2, v3};
+          continue;
+        }
         if constexpr (kBias == 1) {
           const float* bp = static_cast<const float*>(bias);
           v0 += bp[n];
@@ -295,6 +311,43 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
       }
     }
   }
+}
+
+// Sum of the split-K partial products: out[m][n] = round(sum_y partial[y][m][n] + bias[n]),
+// y in order; one thread per 4 consecutive columns of a row (N % 8 == 0), one wave per
+// workgroup so that small outputs still spread over every CU.
+constexpr int kSplitReduceThreads = 64;
+template <typename Tag, int kBias>
+__global__ __launch_bounds__(kSplitReduceThreads) void gemm_splitk_reduce_kernel(
+    const float* __restrict__ partial, int splits, uint16_t* __restrict__ C, const void* __restrict__ bias, int M, int N,
+    long long ldc) {
+  using H = Half16<Tag>;
+  const long long idx = (long long)blockIdx.x * kSplitReduceThreads + threadIdx.x;
+  const int nq = N >> 2;
+  if (idx >= (long long)M * nq) return;
+  const int m = (int)(idx / nq);
+  const int n = (int)(idx - (long long)m * nq) * 4;
+  const long long plane = (long long)M * N;
+  const float* p = partial + (long long)m * N + n;
+  f32x4 s = *reinterpret_cast<const f32x4*>(p);
+  for (int y = 1; y < splits; ++y) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(p + y * plane);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s[e] += v[e];
+  }
+  if constexpr (kBias == 1) {
+    const float* bp = static_cast<const float*>(bias);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s[e] += bp[n + e];
+  } else if constexpr (kBias == 2) {
+    const uint16_t* bp = static_cast<const uint16_t*>(bias);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s[e] += H::to_float(bp[n + e]);
+  }
+  u32x2 packed;
+  packed[0] = H::pack2(s[0], s[1]);
+  packed[1] = H::pack2(s[2], s[3]);
+  st8(C + (long long)m * ldc + n, packed);
 }
 
 // Generic path: any element type, any shape/strides (element strides), optional bias.

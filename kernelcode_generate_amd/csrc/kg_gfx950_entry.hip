@@ -11,6 +11,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <vector>
 
 #include "kg_gfx950.h"
@@ -246,6 +247,64 @@ bool pipe_aligned(long long M, long long N, long long K) {
 // 2^31 (the buffer range of the ragged copies; 255 rows x 2^23 bytes + 64).
 constexpr long long kMaxPipeLd = 1LL << 22;
 
+// Split-K for outputs of few tiles (skinny M or N: 16 x 4096 is 16 tiles of 128 x 256): the
+// K range is cut into chunks (multiples of the 32-deep slice, at least 256 deep) until the
+// grid covers the CUs, each workgroup row stores fp32 partial sums to a workspace, and a
+// second kernel adds them in chunk order. Returns the chunk count (1: no split). The decision
+// depends on the shape only, so every LDS ring depth gives the same bits.
+constexpr long long kSplitMaxTiles = 64;                 // split only below a quarter of the CUs
+constexpr long long kSplitMinChunk = 256;                // k per chunk, at least 8 slices
+constexpr long long kSplitMaxWorkspace = 64LL << 20;     // bytes of fp32 partials
+int pipe_splits(long long M, long long N, long long K, long long* chunk) {
+  const long long tiles = cdiv(M, pipe_tile_m(M, N)) * cdiv(N, gemmp::kBN);
+  *chunk = K;
+  if (tiles > kSplitMaxTiles || K < 2 * kSplitMinChunk) return 1;
+  long long splits = std::min(cdiv(kNumCUs, tiles), K / kSplitMinChunk);
+  splits = std::min(splits, kSplitMaxWorkspace / (M * N * 4));
+  if (splits < 2) return 1;
+  const long long c = cdiv(cdiv(K, splits), gemmp::kBK) * gemmp::kBK;
+  *chunk = c;
+  return (int)cdiv(K, c);
+}
+
+// Split-K workspaces, one per (device, stream) and kept for the life of the process: work
+// enqueued on one stream runs in order, so its calls can share one buffer, and calls on
+// different streams never do. A larger request replaces the buffer (the old one is released
+// in stream order, after the work already enqueued). An allocation per call
+// (hipMallocAsync/hipFreeAsync) cost about 60 us of host time per matmul.
+struct SplitWorkspace {
+  int device;
+  hipStream_t stream;
+  void* ptr;
+  size_t bytes;
+};
+std::mutex g_split_ws_mutex;
+std::vector<SplitWorkspace> g_split_ws;
+
+void* split_workspace(size_t bytes, hipStream_t stream) {
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> lock(g_split_ws_mutex);
+  SplitWorkspace* slot = nullptr;
+  for (auto& w : g_split_ws)
+    if (w.device == device && w.stream == stream) slot = &w;
+  if (slot != nullptr && slot->bytes >= bytes) return slot->ptr;
+  void* ptr = nullptr;
+  const size_t want = std::max(bytes, (size_t)(4u << 20));
+  if (hipMalloc(&ptr, want) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  if (slot != nullptr) {
+    (void)hipFreeAsync(slot->ptr, stream);
+    slot->ptr = ptr;
+    slot->bytes = want;
+  } else {
+    g_split_ws.push_back({device, stream, ptr, want});
+  }
+  return ptr;
+}
+
 template <typename Tag>
 int launch_gemm_mfma(const Mem& out, const Mem& lhs, const Mem& rhs, const Mem& bias, int M, int N, int K,
                      int stages) {
@@ -259,9 +318,17 @@ int launch_gemm_mfma(const Mem& out, const Mem& lhs, const Mem& rhs, const Mem& 
   const long long tm = pipe_tile_m(M, N);
   const bool ragged = !pipe_aligned(M, N, K);
   const int grid = (int)(cdiv(M, tm) * cdiv(N, gemmp::kBN));
-#define KG_GEMM_PIPE(BIAS, TM, ST, RAG)                                                                              \
-  hipLaunchKernelGGL((gemm_pipe_kernel<Tag, BIAS, TM, ST, RAG>), dim3(grid), dim3(gemmp::kThreads), 0, g_stream, A, B, \
-                     C, bp, M, N, K, lda, ldb, ldc)
+  long long chunk = K;
+  int splits = pipe_splits(M, N, K, &chunk);
+  float* partial = nullptr;
+  if (splits > 1) {
+    partial = static_cast<float*>(split_workspace((size_t)splits * M * N * sizeof(float), g_stream));
+    if (partial == nullptr) splits = 1;  // no workspace: the whole K range in one pass
+  }
+  const int k_chunk = splits > 1 ? (int)chunk : 0;
+#define KG_GEMM_PIPE(BIAS, TM, ST, RAG)                                                                  \
+  hipLaunchKernelGGL((gemm_pipe_kernel<Tag, BIAS, TM, ST, RAG>), dim3(grid, splits), dim3(gemmp::kThreads), 0, \
+                     g_stream, A, B, C, bp, M, N, K, lda, ldb, ldc, partial, k_chunk)
 #define KG_GEMM_PIPE_BIAS(TM, ST, RAG)               \
   if (bias_kind == 0) KG_GEMM_PIPE(0, TM, ST, RAG);   \
   else if (bias_kind == 1) KG_GEMM_PIPE(1, TM, ST, RAG); \
@@ -278,6 +345,19 @@ int launch_gemm_mfma(const Mem& out, const Mem& lhs, const Mem& rhs, const Mem& 
 #undef KG_GEMM_PIPE_DEPTH
 #undef KG_GEMM_PIPE_BIAS
 #undef KG_GEMM_PIPE
+  if (splits > 1) {
+    const int rgrid = (int)cdiv((long long)M * (N / 4), kSplitReduceThreads);
+    if (bias_kind == 0)
+      hipLaunchKernelGGL((gemm_splitk_reduce_kernel<Tag, 0>), dim3(rgrid), dim3(kSplitReduceThreads), 0, g_stream, partial, splits, C, bp,
+                         M, N, ldc);
+    else if (bias_kind == 1)
+      hipLaunchKernelGGL((gemm_splitk_reduce_kernel<Tag, 1>), dim3(rgrid), dim3(kSplitReduceThreads), 0, g_stream, partial, splits, C, bp,
+                         M, N, ldc);
+    else
+      hipLaunchKernelGGL((gemm_splitk_reduce_kernel<Tag, 2>), dim3(rgrid), dim3(kSplitReduceThreads), 0, g_stream, partial, splits, C, bp,
+                         M, N, ldc);
+    return finish_launch("matmul(mfma-pipe-splitk)");
+  }
   return finish_launch(ragged ? "matmul(mfma-pipe-ragged)" : "matmul(mfma-pipe)");
 }
 

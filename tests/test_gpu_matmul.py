@@ -130,6 +130,49 @@ def test_pipe_256_row_tiles_with_bias(device, oracle_mod, bias_kind):
 
 
 @pytest.mark.parametrize(
+    "shape,dtype_name,bias_kind,rows",
+    [
+        ((16, 4096, 4096), "bfloat16", "f32", None),  # 16 tiles: 16 K chunks of 256
+        ((128, 8192, 1024), "float16", "same", [(0, 16), (112, 128)]),  # 4 tiles: 32 chunks
+        ((3, 1000, 136), "bfloat16", "none", None),  # one ragged tile, last chunk 8 deep short of a slice
+        ((40, 2048, 520), "float16", "f32", None),  # 3 tiles, ragged N
+    ],
+    ids=["16x4096x4096", "128x8192x1024", "3x1000x136", "40x2048x520"],
+)
+def test_split_k_skinny(device, oracle_mod, shape, dtype_name, bias_kind, rows):
+    """Outputs of few tiles run the pipelined kernel split over K (fp32 partial sums in a
+    stream-ordered workspace, added in chunk order by a second kernel that also adds the bias
+    and rounds once). The output is a window of a NaN-filled buffer (extra rows and columns
+    must stay NaN); rows are checked against the oracle."""
+
+    import torch
+
+    dt = getattr(torch, dtype_name)
+    m, k, n = shape
+    rng = np.random.default_rng(m + 5 * k + 11 * n)
+    lt, lhs = round_to(rng.standard_normal((m, k), dtype=np.float32) * 0.1, dt)
+    rt, rhs = round_to(rng.standard_normal((k, n), dtype=np.float32) * 0.1, dt)
+    bias = bt = None
+    if bias_kind == "f32":
+        bias = bt = rng.standard_normal(n).astype(np.float32)
+    elif bias_kind == "same":
+        bt, bias = round_to(rng.standard_normal(n), dt)
+    big = torch.full((m + 2, n + 8), float("nan"), dtype=dt, device=device)
+    out = big[:m, :n]
+    print(f"[matmul] split-K M={m} K={k} N={n} {dtype_name} bias={bias_kind}", flush=True)
+    native.matmul(out, lt.to(device), rt.to(device), None if bt is None else torch.as_tensor(bt).to(device))
+    got = to_numpy(big)
+    assert np.isnan(got[m:]).all() and np.isnan(got[:, n:]).all(), "store outside the output window"
+    for r0, r1 in rows or [(0, m)]:
+        ref = oracle_mod.matmul_demo(lhs[r0:r1], rhs, bias, (64, 64, 64))
+        assert_h16_close(got[r0:r1, :n], ref, what=f"{shape} rows {r0}:{r1}")
+    # the same call again gives the same bits (chunks are added in a fixed order)
+    again = torch.full_like(out, float("nan"))
+    native.matmul(again, lt.to(device), rt.to(device), None if bt is None else torch.as_tensor(bt).to(device))
+    assert torch.equal(again, out.contiguous())
+
+
+@pytest.mark.parametrize(
     "shape,rows",
     [
         ((1000, 520, 1000), None),  # 128-row tiles, every edge ragged, 8-deep last K slice
