@@ -76,6 +76,9 @@ typedef struct KgArgSlot {
  * extension: INT memory_stage in {2, 3, 4}, the LDS ring depth of the pipelined 16-bit
  * kernel (the gfx950 reading of the reference's multi-buffer memory_stage,
  * kernel_gen/passes/memory/multi_buffer.py; default 4); other kernels ignore it.
+ * 16-bit outputs of at most 64 tiles of 128 x 256 with K >= 512 split K over workgroups and
+ * add the fp32 partial sums in a second kernel; the partials live in a workspace the library
+ * allocates once per (device, stream) on first use (hipMalloc, at most 64 MiB) and keeps.
  */
 int kg_gfx950_matmul_entry(const KgArgSlot* ordered_args, unsigned long long arg_count);
 
