@@ -480,6 +480,15 @@ def main() -> int:
         },
     }
     del a, b, c
+    # the part's sustained matrix-core rate on this data (random bf16, no operand movement):
+    # the power-limited ceiling the headline's fraction is read against
+    ceiling = native.mfma_rate("bf16", False)
+    result["roofline"]["mfma_ceiling"] = {
+        "tflops": round(ceiling["tflops"], 1), "clock_ghz": round(ceiling["clock_ghz"], 3),
+        "what": "back-to-back v_mfma_f32_32x32x16_bf16 on N(0,1)*0.02 register operands (kg_gfx950_mfma_rate)"}
+    result["roofline"]["frac_of_mfma_ceiling"] = round(achieved / ceiling["tflops"], 4)
+    log(f"[bench] mfma ceiling (random bf16 operands): {ceiling['tflops']:.1f} TFLOP/s at {ceiling['clock_ghz']:.3f} GHz; "
+        f"headline {achieved / ceiling['tflops']:.3f} of it")
     if args.copy_calibration:
         src = torch.empty(1 << 29, dtype=torch.bfloat16, device=dev).fill_(1.0)
         dst = torch.empty_like(src)
