@@ -88,13 +88,14 @@ def attention_f32_tolerance(q, k, v, scale=None, causal=False) -> np.ndarray:
     return 1e-5 + 1e-4 * np.abs(o) + e_max * dev + 4 * np.sqrt(s_kv) * 2.0 ** -24 * (p @ np.abs(v))
 
 
-def attention_h16_tolerance(q, k, v, scale=None, causal=False) -> np.ndarray:
+def attention_h16_tolerance(q, k, v, scale=None, causal=False, dtype_name="bfloat16") -> np.ndarray:
     """Per-element bar for the 16-bit attention kernels: the north-star 2e-2 |oracle| +
     1e-2 rms(oracle), plus the first-order effect of the one rounding the design adds on top
-    of the output's own: P is rounded to the 16-bit format (P_j (1 + d_j), |d_j| <= 2^-9 for
-    bf16, 2^-11 for f16, taken as 2^-9) before the P V product, and the row sum uses the same
-    rounded P, so O_i = sum_j w~_j V_j moves by exactly sum_j w_j (d_j - mean d) V_j =
-    sum_j w_j d_j (V_j - O_i) to first order: at most 2^-9 ((W |V|)_id + |O_id|). The rms
+    of the output's own: P is rounded to the 16-bit format (P_j (1 + d_j), |d_j| <= u, the
+    unit roundoff of round-to-nearest: 2^-8 for bf16's 8-bit significand, 2^-11 for f16's 11
+    bits) before the P V product, and the row sum uses the same rounded P, so
+    O_i = sum_j w~_j V_j moves by exactly sum_j w_j (d_j - mean d) V_j =
+    sum_j w_j d_j (V_j - O_i) to first order: at most u ((W |V|)_id + |O_id|). The rms
     term alone is too tight for short causal rows (row i averages i + 1 keys with large
     weights), where this term dominates. Float64 from the inputs."""
 
@@ -110,7 +111,8 @@ def attention_h16_tolerance(q, k, v, scale=None, causal=False) -> np.ndarray:
     w /= w.sum(-1, keepdims=True)
     o = w @ v
     rms = float(np.sqrt(np.mean(o * o))) if o.size else 0.0
-    return H16_ATOL_RMS * rms + H16_RTOL * np.abs(o) + 2.0 ** -9 * (w @ np.abs(v) + np.abs(o))
+    u = {"bfloat16": 2.0 ** -8, "float16": 2.0 ** -11}[dtype_name]
+    return H16_ATOL_RMS * rms + H16_RTOL * np.abs(o) + u * (w @ np.abs(v) + np.abs(o))
 
 
 def assert_within(out, ref, atol, what: str = "") -> None:

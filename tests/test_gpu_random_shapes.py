@@ -106,5 +106,5 @@ def test_random_attention(device, oracle_mod, b, h, s, d, causal, dtype_name):
     ref = oracle_mod.flash_attention_demo(q, k, v, 64, 64, scale=scale, causal=causal)
     got = to_numpy(out)
     assert np.isfinite(got).all()
-    assert_within(got, ref, attention_h16_tolerance(q, k, v, scale, causal),
+    assert_within(got, ref, attention_h16_tolerance(q, k, v, scale, causal, dtype_name),
                   what=f"attention {b}x{h}x{s}x{d} causal={causal} {dtype_name}")
