@@ -270,25 +270,40 @@ int pipe_splits(long long M, long long N, long long K, long long* chunk) {
 // Split-K workspaces, one per (device, stream) and kept for the life of the process: work
 // enqueued on one stream runs in order, so its calls can share one buffer, and calls on
 // different streams never do. A larger request replaces the buffer (the old one is released
-// in stream order, after the work already enqueued). An allocation per call
+// in stream order, after the work already enqueued). At most kSplitCachedStreams buffers are
+// kept per device: a call on another stream then takes the least recently used slot and
+// releases that slot's buffer with hipFree, which waits for the device's pending work (the
+// stream the buffer was used on may no longer exist). An allocation per call
 // (hipMallocAsync/hipFreeAsync) cost about 60 us of host time per matmul.
+constexpr int kSplitCachedStreams = 8;
 struct SplitWorkspace {
   int device;
   hipStream_t stream;
   void* ptr;
   size_t bytes;
+  unsigned long long last_use;
 };
 std::mutex g_split_ws_mutex;
 std::vector<SplitWorkspace> g_split_ws;
+unsigned long long g_split_ws_clock = 0;
 
 void* split_workspace(size_t bytes, hipStream_t stream) {
   int device = 0;
   if (hipGetDevice(&device) != hipSuccess) return nullptr;
   std::lock_guard<std::mutex> lock(g_split_ws_mutex);
   SplitWorkspace* slot = nullptr;
-  for (auto& w : g_split_ws)
-    if (w.device == device && w.stream == stream) slot = &w;
-  if (slot != nullptr && slot->bytes >= bytes) return slot->ptr;
+  SplitWorkspace* lru = nullptr;
+  int on_device = 0;
+  for (auto& w : g_split_ws) {
+    if (w.device != device) continue;
+    ++on_device;
+    if (w.stream == stream) slot = &w;
+    if (lru == nullptr || w.last_use < lru->last_use) lru = &w;
+  }
+  if (slot != nullptr && slot->bytes >= bytes) {
+    slot->last_use = ++g_split_ws_clock;
+    return slot->ptr;
+  }
   void* ptr = nullptr;
   const size_t want = std::max(bytes, (size_t)(4u << 20));
   if (hipMalloc(&ptr, want) != hipSuccess) {
@@ -297,11 +312,14 @@ void* split_workspace(size_t bytes, hipStream_t stream) {
   }
   if (slot != nullptr) {
     (void)hipFreeAsync(slot->ptr, stream);
-    slot->ptr = ptr;
-    slot->bytes = want;
+  } else if (on_device >= kSplitCachedStreams) {
+    (void)hipFree(lru->ptr);  // waits for the device's pending work
+    slot = lru;
   } else {
-    g_split_ws.push_back({device, stream, ptr, want});
+    g_split_ws.push_back({device, stream, nullptr, 0, 0});
+    slot = &g_split_ws.back();
   }
+  *slot = {device, stream, ptr, want, ++g_split_ws_clock};
   return ptr;
 }
 

@@ -172,6 +172,38 @@ def test_split_k_skinny(device, oracle_mod, shape, dtype_name, bias_kind, rows):
     assert torch.equal(again, out.contiguous())
 
 
+def test_split_k_on_many_streams(device, oracle_mod):
+    """Split-K matmuls enqueued on more streams than the library keeps workspaces for (8 per
+    device): the ninth and later streams take over the least recently used workspace, whose
+    buffer is released only after the device's pending work. Two rounds over 11 streams, each
+    call with its own inputs, every output checked against the oracle."""
+
+    import torch
+
+    m, k, n = 16, 2048, 512  # 2 output tiles, K split 8 ways
+    streams = [torch.cuda.Stream(device=device) for _ in range(11)]
+    cases = []
+    for rnd in range(2):
+        for i, stream in enumerate(streams):
+            rng = np.random.default_rng(1000 * rnd + i)
+            lt, lhs = round_to(rng.standard_normal((m, k), dtype=np.float32) * 0.1, torch.bfloat16)
+            rt, rhs = round_to(rng.standard_normal((k, n), dtype=np.float32) * 0.1, torch.bfloat16)
+            a, b = lt.to(device), rt.to(device)
+            out = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=device)
+            torch.cuda.synchronize()
+            print(f"[matmul] split-K round {rnd} stream {i}", flush=True)
+            native.set_launch_mode(False, stream.cuda_stream)
+            try:
+                native.matmul(out, a, b, None)
+            finally:
+                native.set_launch_mode(True, None)
+            cases.append((out, lhs, rhs, (rnd, i), (a, b)))  # inputs stay alive until the sync
+    torch.cuda.synchronize()
+    for out, lhs, rhs, tag, _ in cases:
+        ref = oracle_mod.matmul_demo(lhs, rhs, None, (64, 64, 64))
+        assert_h16_close(to_numpy(out), ref, what=f"split-K round/stream {tag}")
+
+
 @pytest.mark.parametrize(
     "shape,rows",
     [
