@@ -1,0 +1,336 @@
+// Implicit-GEMM conv2d on gfx950 MFMA for 16-bit NCHW convs of stride 1 and dilation 1
+// whose input and output rows split into whole pieces of G pixels (W % G == 0 and
+// Wo % G == 0, G = 8 or 4), with a KW = 3 window and left pad 1 or a KW = 1 window and
+// left pad 0 (any C, F, KH, top/bottom pads; C KH KW a multiple of 8). fp32 accumulation.
+//
+// GEMM view as in conv2d_igemm.h: Y[n][f][p] = sum_k W[f][k] Xcol[k][(n, p)] with k =
+// (c, kh, kw) in the weight's own order. What differs is how Xcol reaches LDS. With stride 1
+// the k-row (c, kh, kw) of G consecutive output pixels of one row is G consecutive input
+// pixels of one input row, shifted by kw - pl: so a thread that owns a (c, kh) run and a
+// G-pixel piece loads the aligned G-pixel pieces of input row ho - pt + kh that cover all
+// KW shifts (three for 3x3, one for 1x1), builds the KW shifted windows in registers
+// (v_alignbyte on compile-time offsets) and writes them as KW k-rows. Pieces outside the
+// row (the left/right padding) and rows outside the image load nothing and hold zeros; W %
+// G == 0 keeps every piece wholly inside or wholly outside. One load serves KW k-rows, so a
+// 32-deep K step takes one vector load per thread where the per-element gather took 16.
+//
+// Xcol sits in LDS k-major, [k-row][128 pixels] (256 bytes a row, 16-byte chunk c of row r
+// at c ^ 4(r & 3)), and the MFMA operand (8 consecutive k of one pixel) is read with two
+// ds_read_b64_tr_b16: within each 16-lane group, lane j addresses 4 consecutive pixels of
+// k-row j/4 and lane i receives k-rows 0..3 of pixel i; under the chunk swizzle the 32 lanes
+// served together hit 16 distinct chunks of one 256-byte bank cycle. Weights stay [f][k] rows
+// of one slice (16 KW values, 16-byte chunk loads), padded to an odd number of 16-byte
+// chunks per row so 16 consecutive rows at one chunk hit distinct banks.
+//
+// A workgroup (4 waves, 2 x 2) computes BM (64 or 128) filters x 128 output pixels and walks
+// K in slices of 16 KW k-rows (16 runs (c, kh) x KW taps): KW MFMA steps of 16 per slice,
+// two LDS stages, the next slice's loads in flight during the current slice's MFMAs. Each
+// lane ends with 4 consecutive output pixels of one filter (Wo % 4 == 0 keeps them in one
+// row of one image) and stores them as one 8-byte piece.
+#pragma once
+
+#include <type_traits>
+
+#include "common.h"
+#include "conv2d.h"
+#include "conv2d_igemm.h"
+#include "lds_dma.h"
+
+namespace kg_gfx950 {
+
+namespace convr {
+constexpr int kBN = 128;      // output pixels per tile
+constexpr int kThreads = 256;  // 4 waves, 2 x 2
+constexpr int kRuns = 16;      // (c, kh) runs per K slice
+
+struct Params {
+  int n, c, h, w, f, kh, ho, wo, pt;
+  int K;     // C KH KW
+  int runs;  // C KH
+  int P;     // Ho Wo
+  int NP;    // N Ho Wo
+  int bias_kind;  // 0 none, 1 fp32, 2 same 16-bit type
+  FastDiv div_kh, div_p, div_wo;
+};
+
+// byte offset of 16-byte chunk c of k-row r in an Xcol stage
+__host__ __device__ constexpr int xoff(int r, int c) { return r * 256 + ((c ^ (4 * (r & 3))) * 16); }
+
+template <int KW, int PL, int G>
+struct Geometry {
+  static_assert(G == 8 || G == 4, "pieces of 8 or 4 pixels");
+  static_assert(PL >= 0 && PL < G, "left pad within one piece");
+  static constexpr int kKR = 16 * KW;                    // k-rows per slice
+  static constexpr int kWPitch = 32 * KW + 16;           // weight row bytes in LDS: an odd number of chunks
+  static constexpr int kM0 = (G - PL) % G;               // first needed element within the first piece
+  static constexpr int kPieces = (kM0 + KW - 1 + G + G - 1) / G;  // aligned pieces covering all KW windows
+  static constexpr int kDw = G / 2;                      // dwords per piece
+  static constexpr int kGroups = kBN / G;                // pieces per k-row of a tile
+  static constexpr int kItems = kRuns * kGroups / kThreads;  // (run, piece) items per thread and slice
+};
+
+template <int BM, int KW, int PL, int G>
+constexpr int rowvec_stage_bytes() {
+  return Geometry<KW, PL, G>::kKR * 256 + BM * Geometry<KW, PL, G>::kWPitch;
+}
+}  // namespace convr
+
+template <typename Tag, int kMI, int KW, int PL, int G>
+__global__ __launch_bounds__(convr::kThreads) void conv2d_rowvec_kernel(const uint16_t* __restrict__ x,
+                                                                        const uint16_t* __restrict__ wt,
+                                                                        uint16_t* __restrict__ y,
+                                                                        const void* __restrict__ bias,
+                                                                        convr::Params s) {
+  using namespace convr;
+  using Geo = Geometry<KW, PL, G>;
+  using Hf = Half16<Tag>;
+  constexpr int BM = 64 * kMI;
+  constexpr int KR = Geo::kKR;
+  constexpr int kXBytes = KR * 256;
+  constexpr int kStage = rowvec_stage_bytes<BM, KW, PL, G>();
+  constexpr int kWChunks = BM * 2 * KW;  // 16-byte weight chunks per slice
+  constexpr int kWPerThread = (kWChunks + kThreads - 1) / kThreads;
+  using Piece = typename std::conditional<G == 8, u32x4, u32x2>::type;
+  __shared__ __attribute__((aligned(1024))) char lds[2 * kStage];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int tiles_m = (s.f + BM - 1) / BM;
+  const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int m0 = (logical % tiles_m) * BM;  // the filter tiles of one pixel tile are adjacent
+  const int n0 = (logical / tiles_m) * kBN;
+
+  // ---- this thread's output piece: pixels j0 .. j0+G-1 of one output row ----
+  const int g = tid % Geo::kGroups;
+  const int q0 = tid / Geo::kGroups;  // first run; item i takes run q0 + i * (16 / kItems)
+  const int j0 = n0 + G * g;
+  const bool piece_ok = j0 < s.NP;
+  const uint32_t jn = fdiv(piece_ok ? j0 : 0, s.div_p);
+  const uint32_t jp = (piece_ok ? j0 : 0) - jn * s.P;
+  const uint32_t jho = fdiv(jp, s.div_wo);
+  const int wo0 = (int)(jp - jho * s.wo);
+  const int hbase = (int)jho - s.pt;                   // input row of kh = 0
+  const int pc0 = (wo0 - PL + G) / G - 1;              // first aligned input piece (may be -1)
+  const int wpieces = s.w / G;
+  const long long hw = (long long)s.h * s.w;
+  const uint16_t* xn = x + (long long)jn * s.c * hw;
+
+  Piece raw[Geo::kItems][Geo::kPieces];
+  u32x4 rw[kWPerThread];
+  auto load_regs = [&](int kt) {
+#pragma unroll
+    for (int it = 0; it < Geo::kItems; ++it) {
+      const int run = kt * kRuns + q0 + it * (kRuns / Geo::kItems);
+      const uint32_t c = fdiv((uint32_t)run, s.div_kh);
+      const int hi = hbase + (run - (int)c * s.kh);
+      const bool row_ok = piece_ok && run < s.runs && (unsigned)hi < (unsigned)s.h;
+      const uint16_t* src = xn + (long long)c * hw + (long long)hi * s.w + G * pc0;
+#pragma unroll
+      for (int p = 0; p < Geo::kPieces; ++p) {
+        const bool ok = row_ok && (unsigned)(pc0 + p) < (unsigned)wpieces;
+        raw[it][p] = ok ? *reinterpret_cast<const Piece*>(src + G * p) : Piece{};
+      }
+    }
+    const int k0 = kt * KR;
+#pragma unroll
+    for (int i = 0; i < kWPerThread; ++i) {
+      const int ci = tid + kThreads * i;
+      const int row = ci / (2 * KW), kc = ci - row * (2 * KW);
+      const int f = m0 + row, k = k0 + 8 * kc;
+      rw[i] = (ci < kWChunks && f < s.f && k < s.K) ? ld16(wt + (long long)f * s.K + k) : u32x4{0, 0, 0, 0};
+    }
+  };
+  // window kw of item `it`: elements kM0 + kw .. + G-1 of its concatenated pieces
+  auto window = [&](int it, auto kw_tag) -> Piece {
+    constexpr int st = Geo::kM0 + decltype(kw_tag)::value;
+    Piece out;
+#pragma unroll
+    for (int d = 0; d < Geo::kDw; ++d) {
+      constexpr int kDw = Geo::kDw;
+      const int e = st + 2 * d;  // first element of output dword d
+      const int lo = e >> 1;
+      const uint32_t a = raw[it][lo / kDw][lo % kDw];
+      if ((st & 1) == 0) {
+        out[d] = a;
+      } else {
+        const int hi_ = lo + 1;
+        const uint32_t b = raw[it][hi_ / kDw][hi_ % kDw];
+        out[d] = __builtin_amdgcn_alignbyte(b, a, 2);
+      }
+    }
+    return out;
+  };
+  auto store_lds = [&](int buf) {
+    char* st = lds + buf * kStage;
+#pragma unroll
+    for (int it = 0; it < Geo::kItems; ++it) {
+      const int q = q0 + it * (kRuns / Geo::kItems);
+      auto put = [&](auto kw_tag) {
+        constexpr int kw = decltype(kw_tag)::value;
+        const int r = KW * q + kw;
+        const Piece v = window(it, kw_tag);
+        if constexpr (G == 8) {
+          *reinterpret_cast<u32x4*>(st + xoff(r, g)) = v;
+        } else {
+          *reinterpret_cast<u32x2*>(st + xoff(r, g >> 1) + 8 * (g & 1)) = v;
+        }
+      };
+      put(Int<0>{});
+      if constexpr (KW > 1) put(Int<1>{});
+      if constexpr (KW > 2) put(Int<2>{});
+    }
+#pragma unroll
+    for (int i = 0; i < kWPerThread; ++i) {
+      const int ci = tid + kThreads * i;
+      if (ci < kWChunks) {
+        const int row = ci / (2 * KW), kc = ci - row * (2 * KW);
+        *reinterpret_cast<u32x4*>(st + kXBytes + row * Geo::kWPitch + 16 * kc) = rw[i];
+      }
+    }
+  };
+
+  // ---- fragment addresses (bytes within a stage) ----
+  const int frag = lane & 31, h = lane >> 5;
+  const int lg = lane >> 4, j16 = lane & 15;
+  const int b_kofs = 8 * (lg >> 1) + (j16 >> 2);  // k-row of the first transposed read
+  int x_rd[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const int px = wn * 64 + 32 * b + 16 * (lg & 1) + 4 * (j16 & 3);
+    x_rd[b] = xoff(b_kofs, px >> 3) + 2 * (px & 7);  // +1024: k-rows +4; +4096: next K step
+  }
+  int w_rd[kMI];
+#pragma unroll
+  for (int i = 0; i < kMI; ++i) w_rd[i] = kXBytes + (wm * (BM / 2) + 32 * i + frag) * Geo::kWPitch + 16 * h;
+
+  f32x16 acc[kMI][2];
+#pragma unroll
+  for (int i = 0; i < kMI; ++i)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][b][e] = 0.f;
+
+  const int nk = (s.runs + kRuns - 1) / kRuns;
+  load_regs(0);
+  store_lds(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt + 1 < nk) load_regs(kt + 1);  // loads in flight during the MFMAs below
+    const char* st = lds + (kt & 1) * kStage;
+    const uint32_t sbase = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)st;
+#pragma unroll
+    for (int ks = 0; ks < KW; ++ks) {
+      u32x4 af[kMI], bf[2];
+#pragma unroll
+      for (int i = 0; i < kMI; ++i)
+        af[i] = *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(sbase + w_rd[i] + 32 * ks);
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) s16x4*)(uintptr_t)(sbase + x_rd[b] + 1024 * t + 4096 * ks));
+          const u32x2 w2 = __builtin_bit_cast(u32x2, v);
+          bf[b][2 * t] = w2[0];
+          bf[b][2 * t + 1] = w2[1];
+        }
+#pragma unroll
+      for (int i = 0; i < kMI; ++i)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) acc[i][b] = Hf::mfma32(bf[b], af[i], acc[i][b]);
+    }
+    if (kt + 1 < nk) store_lds((kt + 1) & 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: lane holds Y[f][j .. j+3], f = tile row wm*BM/2 + 32 i + lane % 32,
+  // j = tile pixel wn*64 + 32 b + 8 q + 4 (lane / 32); P % 4 == 0 keeps j .. j+3 in one image ----
+#pragma unroll
+  for (int i = 0; i < kMI; ++i) {
+    const int f = m0 + wm * (BM / 2) + 32 * i + frag;
+    if (f >= s.f) continue;
+    float bv = 0.f;
+    if (s.bias_kind == 1) bv = static_cast<const float*>(bias)[f];
+    if (s.bias_kind == 2) bv = Hf::to_float(static_cast<const uint16_t*>(bias)[f]);
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int j = n0 + wn * 64 + 32 * b + 8 * q + 4 * h;
+        if (j >= s.NP) continue;
+        const uint32_t n = fdiv(j, s.div_p);
+        const uint32_t p = j - n * s.P;
+        u32x2 packed;
+        packed[0] = Hf::pack2(acc[i][b][4 * q] + bv, acc[i][b][4 * q + 1] + bv);
+        packed[1] = Hf::pack2(acc[i][b][4 * q + 2] + bv, acc[i][b][4 * q + 3] + bv);
+        st8(y + ((long long)n * s.f + f) * s.P + p, packed);
+      }
+  }
+}
+
+// Pieces of G pixels: 8 when W and Wo are multiples of 8, else 4 when they are multiples of
+// 4, else 0 (the row-vector path does not apply).
+inline int conv_rowvec_piece(const ConvShape& s) {
+  if (s.w % 8 == 0 && s.wo % 8 == 0) return 8;
+  if (s.w % 4 == 0 && s.wo % 4 == 0) return 4;
+  return 0;
+}
+
+inline bool conv_rowvec_supported(const ConvShape& s) {
+  const long long K = (long long)s.c * s.kh * s.kw;
+  const bool window = (s.kw == 3 && s.pl == 1) || (s.kw == 1 && s.pl == 0);
+  return window && s.sh == 1 && s.sw == 1 && s.dh == 1 && s.dw == 1 && conv_rowvec_piece(s) != 0 && K % 8 == 0 &&
+         s.kh >= 1 && s.ho >= 1 && s.wo >= 1 && K < (1ll << 30) && (long long)s.n * s.ho * s.wo < (1ll << 31) &&
+         (long long)s.c * s.kh < (1ll << 30) && (long long)s.n * s.c * s.h * s.w < (1ll << 40);
+}
+
+// BM = 128 filters per tile when F > 64 and such tiles still give every CU of the MI355X
+// (256) two workgroups; else 64.
+inline int conv_rowvec_mi(const ConvShape& s) {
+  const long long cols = ((long long)s.n * s.ho * s.wo + convr::kBN - 1) / convr::kBN;
+  return s.f > 64 && ((s.f + 127) / 128) * cols >= 512 ? 2 : 1;
+}
+
+// MFMA instructions of one launch: per tile and slice, 4 waves x MI x 2 blocks x KW steps.
+inline long long conv_rowvec_mfma(const ConvShape& s) {
+  const long long mi = conv_rowvec_mi(s);
+  const long long tiles = ((s.f + 64 * mi - 1) / (64 * mi)) * (((long long)s.n * s.ho * s.wo + convr::kBN - 1) / convr::kBN);
+  const long long slices = ((long long)s.c * s.kh + convr::kRuns - 1) / convr::kRuns;
+  return tiles * slices * 4 * mi * 2 * s.kw;
+}
+
+template <typename Tag>
+hipError_t launch_conv2d_rowvec(const uint16_t* x, const uint16_t* w, uint16_t* y, const void* bias, int bias_kind,
+                                const ConvShape& s, hipStream_t stream) {
+  convr::Params p;
+  p.n = s.n; p.c = s.c; p.h = s.h; p.w = s.w; p.f = s.f; p.kh = s.kh; p.ho = s.ho; p.wo = s.wo; p.pt = s.pt;
+  p.K = s.c * s.kh * s.kw;
+  p.runs = s.c * s.kh;
+  p.P = s.ho * s.wo;
+  p.NP = s.n * p.P;
+  p.bias_kind = bias_kind;
+  p.div_kh = make_fast_div((uint32_t)s.kh);
+  p.div_p = make_fast_div((uint32_t)p.P);
+  p.div_wo = make_fast_div((uint32_t)s.wo);
+  const int mi = conv_rowvec_mi(s);
+  const int piece = conv_rowvec_piece(s);
+  const int grid = ((s.f + 64 * mi - 1) / (64 * mi)) * ((p.NP + convr::kBN - 1) / convr::kBN);
+#define KG_CONV_RV(MI, KW_, PL_, G_) \
+  hipLaunchKernelGGL((conv2d_rowvec_kernel<Tag, MI, KW_, PL_, G_>), dim3(grid), dim3(convr::kThreads), 0, stream, x, w, y, bias, p)
+#define KG_CONV_RV_G(KW_, PL_, G_) \
+  if (mi == 2) KG_CONV_RV(2, KW_, PL_, G_); \
+  else KG_CONV_RV(1, KW_, PL_, G_)
+  if (s.kw == 3) {
+    if (piece == 8) { KG_CONV_RV_G(3, 1, 8); } else { KG_CONV_RV_G(3, 1, 4); }
+  } else {
+    if (piece == 8) { KG_CONV_RV_G(1, 0, 8); } else { KG_CONV_RV_G(1, 0, 4); }
+  }
+#undef KG_CONV_RV_G
+#undef KG_CONV_RV
+  return hipGetLastError();
+}
+
+}  // namespace kg_gfx950

@@ -22,6 +22,7 @@
 #include "kg_gfx950/gemm_f32.h"
 #include "kg_gfx950/conv2d_mfma.h"
 #include "kg_gfx950/conv2d_igemm.h"
+#include "kg_gfx950/conv2d_rowvec.h"
 #include "kg_gfx950/flash_attn_mfma.h"
 #include "kg_gfx950/flash_attn_f32.h"
 #include "kg_gfx950/mfma_rate.h"
@@ -581,6 +582,8 @@ int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
     long long mfma = 0;
     if (out.dtype != KG_DTYPE_F32 && conv_mfma_supported(s)) {  // live waves x 252 MFMAs per 7-row block
       mfma = (long long)s.n * ((s.h + convk::kRows - 1) / convk::kRows) * (s.w > 32 ? 4 : 2) * 252;
+    } else if (out.dtype != KG_DTYPE_F32 && conv_rowvec_supported(s)) {
+      mfma = conv_rowvec_mfma(s);
     } else if (conv_igemm_supported(s)) {
       // implicit GEMM: per tile and 64-byte k slice, 4 waves x MI x 2 blocks x (2 MFMAs of
       // 32x32x16, or 8 of 32x32x2 for fp32)
@@ -611,6 +614,18 @@ int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
                                                bias_kind, s, g_stream);
     if (e != hipSuccess) return fail(kHipFailure, "conv2d(mfma): %s", hipGetErrorString(e));
     return finish_launch("conv2d(mfma)");
+  }
+  if (out.dtype != KG_DTYPE_F32 && conv_rowvec_supported(s) && aligned16(x.data) && aligned16(w.data) &&
+      aligned16(out.data)) {
+    const int bias_kind = !bias.present ? 0 : (bias.dtype == KG_DTYPE_F32 ? 1 : 2);
+    const uint16_t* xp = static_cast<const uint16_t*>(x.data);
+    const uint16_t* wp = static_cast<const uint16_t*>(w.data);
+    uint16_t* yp = static_cast<uint16_t*>(out.data);
+    const void* bp = bias.present ? bias.data : nullptr;
+    hipError_t e = out.dtype == KG_DTYPE_BF16 ? launch_conv2d_rowvec<Bf16Tag>(xp, wp, yp, bp, bias_kind, s, g_stream)
+                                              : launch_conv2d_rowvec<F16Tag>(xp, wp, yp, bp, bias_kind, s, g_stream);
+    if (e != hipSuccess) return fail(kHipFailure, "conv2d(rowvec): %s", hipGetErrorString(e));
+    return finish_launch("conv2d(rowvec)");
   }
   if (conv_igemm_supported(s) && aligned16(out.data)) {
     const int bias_kind = !bias.present ? 0 : (bias.dtype == KG_DTYPE_F32 ? 1 : 2);

@@ -172,7 +172,7 @@ def test_implicit_gemm_shapes(device, oracle_mod, dtype_name, xs, ws, stride, di
         ((1, 64, 12, 24), (64, 64, 3, 3), "f32"),  # MFMA: 7-row blocks with a 5-row tail, W <= 32
         ((3, 64, 20, 40), (64, 64, 3, 3), "h16"),  # MFMA: 6-row tail, second pixel block partly live
         ((1, 64, 1, 8), (64, 64, 3, 3), "f32"),  # MFMA: one row, one 8-column block
-        ((1, 64, 12, 20), (64, 64, 3, 3), "f32"),  # W % 8 != 0: implicit GEMM
+        ((1, 64, 12, 20), (64, 64, 3, 3), "f32"),  # W % 8 != 0: implicit GEMM on 4-pixel row pieces
         ((3, 16, 9, 13), (32, 16, 3, 3), "f32"),
         ((1, 8, 7, 7), (5, 8, 3, 3), None),
     ],
@@ -193,6 +193,64 @@ def test_16bit_3x3(device, oracle_mod, dtype_name, xs, ws, bias):
     ref = oracle_mod.conv2d_demo(x, w, b, (1, 1), (1, 1), (1, 1, 1, 1), (16, 16, 1, 8, 16))
     out = run(device, dt, xt, wt, bt, (1, 1), (1, 1), (1, 1, 1, 1))
     assert_h16_close(to_numpy(out), ref, what=f"{dtype_name} {xs} bias={bias}")
+
+
+def _rowvec_mfma(xs, ws, pad):
+    """MFMA instructions of the row-piece implicit GEMM (128-pixel tiles, 16-run K slices of
+    KW steps, 4 waves x MI x 2 blocks; MI = 2 for F > 64 with >= 512 workgroups)."""
+
+    n, c, h, w = xs
+    f, _, kh, kw = ws
+    ho, wo = out_hw(xs, ws, (1, 1), (1, 1), pad)
+    cols = -(-(n * ho * wo) // 128)
+    mi = 2 if f > 64 and -(-f // 128) * cols >= 512 else 1
+    return -(-f // (64 * mi)) * cols * -(-(c * kh) // 16) * 4 * mi * 2 * kw
+
+
+@pytest.mark.parametrize("dtype_name", ["float16", "bfloat16"])
+@pytest.mark.parametrize(
+    "xs,ws,pad,bias,images",
+    [
+        ((2, 48, 16, 64), (64, 48, 3, 3), (1, 1, 1, 1), "f32", None),  # 8-pixel pieces
+        ((2, 40, 12, 28), (80, 40, 3, 3), (1, 1, 1, 1), "same", None),  # 4-pixel pieces, F = 80, K slices ragged
+        ((1, 16, 9, 24), (32, 16, 5, 3), (2, 2, 1, 1), None, None),  # KH = 5
+        ((2, 24, 10, 16), (48, 24, 3, 3), (0, 2, 1, 1), "f32", None),  # asymmetric vertical pads
+        ((2, 32, 6, 28), (40, 32, 1, 1), (0, 0, 0, 4), "same", None),  # 1x1, right pad: Wo = 32 > W
+        ((16, 32, 64, 64), (128, 32, 3, 3), (1, 1, 1, 1), "f32", (0, 15)),  # 128-filter tiles
+    ],
+    ids=["p8", "p4_f80", "kh5", "pads_0_2", "1x1_rpad", "bm128"],
+)
+def test_row_piece_path(device, oracle_mod, dtype_name, xs, ws, pad, bias, images):
+    """16-bit convs of stride 1 whose rows split into whole 8- or 4-pixel pieces, with a 3-wide
+    window and left pad 1 or a 1-wide window and left pad 0: each thread loads aligned row
+    pieces once for all taps of a (c, kh) run and builds the shifted windows in registers.
+    The entry's cost query must count this kernel's MFMAs (so the case runs the row-piece
+    path); output against the oracle on the identically rounded inputs (`images`: the
+    images checked, the rest of the batch only runs)."""
+
+    import torch
+
+    dt = getattr(torch, dtype_name)
+    rng = np.random.default_rng(sum(xs) + sum(ws) + sum(pad))
+    xt, x = round_to(rng.standard_normal(xs), dt)
+    bound = np.sqrt(6.0 / (ws[1] * ws[2] * ws[3]))
+    wt, w = round_to(rng.uniform(-bound, bound, size=ws), dt)
+    b = bt = None
+    if bias == "f32":
+        b = bt = rng.normal(size=(ws[0],)).astype(np.float32)
+    elif bias == "same":
+        bt, b = round_to(rng.normal(size=(ws[0],)).astype(np.float32), dt)
+    ho, wo = out_hw(xs, ws, (1, 1), (1, 1), pad)
+    spec = [native.TensorSpec((xs[0], ws[0], ho, wo), dtype_name), native.TensorSpec(xs, dtype_name),
+            native.TensorSpec(ws, dtype_name),
+            None if bt is None else native.TensorSpec((ws[0],), "float32" if bias == "f32" else dtype_name),
+            1, 1, 1, 1, *pad]
+    assert native.cost("conv2d", spec)["MFMA"] == _rowvec_mfma(xs, ws, pad)
+    out = to_numpy(run(device, dt, xt, wt, bt, (1, 1), (1, 1), pad))
+    assert np.isfinite(out).all()
+    sel = slice(None) if images is None else list(images)
+    ref = oracle_mod.conv2d_demo(x[sel], w, b, (1, 1), (1, 1), pad, (16, 16, 1, 8, 16))
+    assert_h16_close(out[sel], ref, what=f"{dtype_name} {xs} {ws} p={pad} bias={bias}")
 
 
 def test_c3_full_size_fp16(device, oracle_mod):
