@@ -3,12 +3,14 @@ counter run can be laid beside the model:
 
     rocprofv3 --pmc SQ_INSTS_MFMA -d <dir> -- python3 -m tests.cost_cases
 
-Every case makes exactly one library kernel dispatch, in the order printed, and nothing
-else dispatches a kernel (inputs are generated on the host and copied), so dispatch i of the
-counter run is case i. Cases cover every kernel choice the model distinguishes: the
+Every case makes exactly one library kernel dispatch, in the order printed; inputs are
+generated on the host and copied, and the only other dispatches are the HIP runtime's own
+copy kernels (named __amd_rocclr_*) that some host-to-device copies use, so library
+dispatch i of the counter run is case i. Cases cover every kernel choice the model distinguishes: the
 pipelined MFMA GEMM with 256- and 128-row tiles and with ragged edges, the fp32 MFMA GEMM
 aligned and ragged, the fp32 split-K GEMM, the SIMT GEMM, the MFMA conv with four and with two live waves and a
-ragged last row block, the implicit-GEMM conv (16-bit and fp32), and the 16-bit and fp32 MFMA attention kernels for D=128 and D=64,
+ragged last row block, the implicit-GEMM conv (16-bit and fp32) and its 16-bit row-piece form
+(8- and 4-pixel pieces, 3x3 and 1x1), and the 16-bit and fp32 MFMA attention kernels for D=128 and D=64,
 causal and not, with ragged query and key tails.
 """
 
@@ -21,12 +23,13 @@ import sys
 from kernelcode_generate_amd import native
 
 # (name, family, dtype, shapes, scalars): shapes are (out, in0, in1[, in2]) in the slot
-# order of the family's entry; bias is always absent.
+# order of the family's entry; bias is always absent. No case takes the split-K matmul path
+# (at most 64 output tiles with K >= 512), which adds a second (reduce) dispatch.
 CASES = (
     ("gemm_bf16_4096", "matmul", "bfloat16", ((4096, 4096), (4096, 4096), (4096, 4096)), ()),
     ("gemm_bf16_c2s_8192x1024x4096", "matmul", "bfloat16", ((8192, 1024), (8192, 4096), (4096, 1024)), ()),
     ("gemm_f16_512x768x256", "matmul", "float16", ((512, 768), (512, 256), (256, 768)), ()),
-    ("gemm_bf16_ragged_1000x1000x520", "matmul", "bfloat16", ((1000, 1000), (1000, 520), (520, 1000)), ()),
+    ("gemm_bf16_ragged_1000x1000x488", "matmul", "bfloat16", ((1000, 1000), (1000, 488), (488, 1000)), ()),
     ("gemm_f32_256", "matmul", "float32", ((256, 256), (256, 256), (256, 256)), ()),
     ("gemm_f32_splitk_512x512x4096", "matmul", "float32", ((512, 512), (512, 4096), (4096, 512)), ()),
     ("gemm_f32_simt_250x250x250", "matmul", "float32", ((250, 250), (250, 250), (250, 250)), ()),
@@ -41,6 +44,10 @@ CASES = (
      (2, 2, 1, 1, 1, 1, 1, 1)),
     ("conv_f32_igemm_1x40x19x23_f96", "conv2d", "float32", ((1, 96, 18, 12), (1, 40, 19, 23), (96, 40, 3, 3)),
      (1, 2, 2, 1, 2, 1, 0, 3)),
+    ("conv_f16_rowvec_2x128x28x28", "conv2d", "float16", ((2, 128, 28, 28), (2, 128, 28, 28), (128, 128, 3, 3)),
+     (1, 1, 1, 1, 1, 1, 1, 1)),
+    ("conv_bf16_rowvec_1x1_2x64x16x32_f96", "conv2d", "bfloat16", ((2, 96, 16, 32), (2, 64, 16, 32), (96, 64, 1, 1)),
+     (1, 1, 1, 1, 0, 0, 0, 0)),
     ("fa_bf16_c4", "flash_attention", "bfloat16", ((4, 32, 2048, 128),) * 4, (128, 64, 0.088388, 0)),
     ("fa_bf16_causal_1x4x4096x128", "flash_attention", "bfloat16", ((1, 4, 4096, 128),) * 4, (128, 64, 0.088388, 1)),
     ("fa_f16_causal_1x2x1000x64", "flash_attention", "float16", ((1, 2, 1000, 64),) * 4, (128, 64, 0.125, 1)),
