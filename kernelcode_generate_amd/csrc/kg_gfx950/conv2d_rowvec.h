@@ -24,9 +24,10 @@
 //
 // A workgroup (4 waves, 2 x 2) computes BM (64 or 128) filters x 128 output pixels and walks
 // K in slices of 16 KW k-rows (16 runs (c, kh) x KW taps): KW MFMA steps of 16 per slice,
-// two LDS stages, the next slice's loads in flight during the current slice's MFMAs. Each
-// lane ends with 4 consecutive output pixels of one filter (Wo % 4 == 0 keeps them in one
-// row of one image) and stores them as one 8-byte piece.
+// two LDS stages and two register sets, so a slice's loads are issued two slices before its
+// MFMAs; register use is bounded for two waves per SIMD (unbounded, the 128-filter
+// instantiations took one wave per SIMD and ran 7-12 % slower on 3x3 shapes). Each lane ends with 4 consecutive output pixels of one filter (Wo % 4 == 0 keeps
+// them in one row of one image) and stores them as one 8-byte piece.
 #pragma once
 
 #include <type_traits>
@@ -76,7 +77,7 @@ constexpr int rowvec_stage_bytes() {
 }  // namespace convr
 
 template <typename Tag, int kMI, int KW, int PL, int G>
-__global__ __launch_bounds__(convr::kThreads) void conv2d_rowvec_kernel(const uint16_t* __restrict__ x,
+__global__ __launch_bounds__(convr::kThreads, 2) void conv2d_rowvec_kernel(const uint16_t* __restrict__ x,
                                                                         const uint16_t* __restrict__ wt,
                                                                         uint16_t* __restrict__ y,
                                                                         const void* __restrict__ bias,
@@ -117,9 +118,11 @@ __global__ __launch_bounds__(convr::kThreads) void conv2d_rowvec_kernel(const ui
   const long long hw = (long long)s.h * s.w;
   const uint16_t* xn = x + (long long)jn * s.c * hw;
 
-  Piece raw[Geo::kItems][Geo::kPieces];
-  u32x4 rw[kWPerThread];
-  auto load_regs = [&](int kt) {
+  // two register sets: slice s is loaded into set s & 1 two slices before its MFMAs
+  Piece raw[2][Geo::kItems][Geo::kPieces];
+  u32x4 rw[2][kWPerThread];
+  auto load_regs = [&](int kt, auto set_tag) {
+    constexpr int S = decltype(set_tag)::value;
 #pragma unroll
     for (int it = 0; it < Geo::kItems; ++it) {
       const int run = kt * kRuns + q0 + it * (kRuns / Geo::kItems);
@@ -130,7 +133,7 @@ __global__ __launch_bounds__(convr::kThreads) void conv2d_rowvec_kernel(const ui
 #pragma unroll
       for (int p = 0; p < Geo::kPieces; ++p) {
         const bool ok = row_ok && (unsigned)(pc0 + p) < (unsigned)wpieces;
-        raw[it][p] = ok ? *reinterpret_cast<const Piece*>(src + G * p) : Piece{};
+        raw[S][it][p] = ok ? *reinterpret_cast<const Piece*>(src + G * p) : Piece{};
       }
     }
     const int k0 = kt * KR;
@@ -139,11 +142,12 @@ __global__ __launch_bounds__(convr::kThreads) void conv2d_rowvec_kernel(const ui
       const int ci = tid + kThreads * i;
       const int row = ci / (2 * KW), kc = ci - row * (2 * KW);
       const int f = m0 + row, k = k0 + 8 * kc;
-      rw[i] = (ci < kWChunks && f < s.f && k < s.K) ? ld16(wt + (long long)f * s.K + k) : u32x4{0, 0, 0, 0};
+      rw[S][i] = (ci < kWChunks && f < s.f && k < s.K) ? ld16(wt + (long long)f * s.K + k) : u32x4{0, 0, 0, 0};
     }
   };
   // window kw of item `it`: elements kM0 + kw .. + G-1 of its concatenated pieces
-  auto window = [&](int it, auto kw_tag) -> Piece {
+  auto window = [&](int it, auto set_tag, auto kw_tag) -> Piece {
+    constexpr int S = decltype(set_tag)::value;
     constexpr int st = Geo::kM0 + decltype(kw_tag)::value;
     Piece out;
 #pragma unroll
@@ -151,18 +155,18 @@ __global__ __launch_bounds__(convr::kThreads) void conv2d_rowvec_kernel(const ui
       constexpr int kDw = Geo::kDw;
       const int e = st + 2 * d;  // first element of output dword d
       const int lo = e >> 1;
-      const uint32_t a = raw[it][lo / kDw][lo % kDw];
+      const uint32_t a = raw[S][it][lo / kDw][lo % kDw];
       if ((st & 1) == 0) {
         out[d] = a;
       } else {
         const int hi_ = lo + 1;
-        const uint32_t b = raw[it][hi_ / kDw][hi_ % kDw];
+        const uint32_t b = raw[S][it][hi_ / kDw][hi_ % kDw];
         out[d] = __builtin_amdgcn_alignbyte(b, a, 2);
       }
     }
     return out;
   };
-  auto store_lds = [&](int buf) {
+  auto store_lds = [&](int buf, auto set_tag) {
     char* st = lds + buf * kStage;
 #pragma unroll
     for (int it = 0; it < Geo::kItems; ++it) {
@@ -170,7 +174,7 @@ __global__ __launch_bounds__(convr::kThreads) void conv2d_rowvec_kernel(const ui
       auto put = [&](auto kw_tag) {
         constexpr int kw = decltype(kw_tag)::value;
         const int r = KW * q + kw;
-        const Piece v = window(it, kw_tag);
+        const Piece v = window(it, set_tag, kw_tag);
         if constexpr (G == 8) {
           *reinterpret_cast<u32x4*>(st + xoff(r, g)) = v;
         } else {
@@ -186,7 +190,7 @@ __global__ __launch_bounds__(convr::kThreads) void conv2d_rowvec_kernel(const ui
       const int ci = tid + kThreads * i;
       if (ci < kWChunks) {
         const int row = ci / (2 * KW), kc = ci - row * (2 * KW);
-        *reinterpret_cast<u32x4*>(st + kXBytes + row * Geo::kWPitch + 16 * kc) = rw[i];
+        *reinterpret_cast<u32x4*>(st + kXBytes + row * Geo::kWPitch + 16 * kc) = rw[decltype(set_tag)::value][i];
       }
     }
   };
@@ -214,12 +218,8 @@ __global__ __launch_bounds__(convr::kThreads) void conv2d_rowvec_kernel(const ui
       for (int e = 0; e < 16; ++e) acc[i][b][e] = 0.f;
 
   const int nk = (s.runs + kRuns - 1) / kRuns;
-  load_regs(0);
-  store_lds(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    if (kt + 1 < nk) load_regs(kt + 1);  // loads in flight during the MFMAs below
-    const char* st = lds + (kt & 1) * kStage;
+  auto compute = [&](int buf) {
+    const char* st = lds + buf * kStage;
     const uint32_t sbase = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)st;
 #pragma unroll
     for (int ks = 0; ks < KW; ++ks) {
@@ -242,8 +242,23 @@ __global__ __launch_bounds__(convr::kThreads) void conv2d_rowvec_kernel(const ui
 #pragma unroll
         for (int b = 0; b < 2; ++b) acc[i][b] = Hf::mfma32(bf[b], af[i], acc[i][b]);
     }
-    if (kt + 1 < nk) store_lds((kt + 1) & 1);
+  };
+  // slice kt: its MFMAs read LDS stage kt & 1; slice kt + 1 goes from register set
+  // (kt + 1) & 1 to the other stage; slice kt + 2 is loaded into set kt & 1 meanwhile.
+  auto step = [&](int kt, auto par_tag) {
+    constexpr int par = decltype(par_tag)::value;
+    if (kt + 2 < nk) load_regs(kt + 2, Int<par>{});
+    compute(par);
+    if (kt + 1 < nk) store_lds(par ^ 1, Int<par ^ 1>{});
     __syncthreads();
+  };
+  load_regs(0, Int<0>{});
+  store_lds(0, Int<0>{});
+  if (nk > 1) load_regs(1, Int<1>{});
+  __syncthreads();
+  for (int kt = 0; kt < nk; kt += 2) {
+    step(kt, Int<0>{});
+    if (kt + 1 < nk) step(kt + 1, Int<1>{});
   }
 
   // ---- epilogue: lane holds Y[f][j .. j+3], f = tile row wm*BM/2 + 32 i + lane % 32,
