@@ -1,15 +1,17 @@
-// Implicit-GEMM conv2d on gfx950 MFMA for 16-bit NCHW convs of stride 1 and dilation 1
-// whose input and output rows split into whole pieces of G pixels (W % G == 0 and
-// Wo % G == 0, G = 8 or 4), with a KW = 3 window and left pad 1 or a KW = 1 window and
-// left pad 0 (any C, F, KH, top/bottom pads; C KH KW a multiple of 8). fp32 accumulation.
+// Implicit-GEMM conv2d on gfx950 MFMA for 16-bit NCHW convs of stride S = 1 or 2 (both
+// directions) and dilation 1 whose input and output rows split into whole pieces of G
+// pixels (W % G == 0 and Wo % G == 0, G = 8 or 4), with a KW = 3 window and left pad 1 or a
+// KW = 1 window and left pad 0 (any C, F, KH, top/bottom pads; C KH KW a multiple of 8).
+// fp32 accumulation.
 //
 // GEMM view as in conv2d_igemm.h: Y[n][f][p] = sum_k W[f][k] Xcol[k][(n, p)] with k =
-// (c, kh, kw) in the weight's own order. What differs is how Xcol reaches LDS. With stride 1
-// the k-row (c, kh, kw) of G consecutive output pixels of one row is G consecutive input
-// pixels of one input row, shifted by kw - pl: so a thread that owns a (c, kh) run and a
-// G-pixel piece loads the aligned G-pixel pieces of input row ho - pt + kh that cover all
-// KW shifts (three for 3x3, one for 1x1), builds the KW shifted windows in registers
-// (v_alignbyte on compile-time offsets) and writes them as KW k-rows. Pieces outside the
+// (c, kh, kw) in the weight's own order. What differs is how Xcol reaches LDS. The k-row
+// (c, kh, kw) of G consecutive output pixels wo0 .. of one row is the input pixels
+// S wo0 - pl + kw + S u (u < G) of input row S ho - pt + kh: so a thread that owns a (c, kh)
+// run and a G-pixel output piece loads the aligned G-pixel input pieces of that row that
+// cover all KW windows (three for 3x3, two or one for 1x1), builds the KW windows in
+// registers (stride 1: v_alignbyte; stride 2: v_perm of every other 16-bit element; all
+// offsets compile-time) and writes them as KW k-rows. Pieces outside the
 // row (the left/right padding) and rows outside the image load nothing and hold zeros; W %
 // G == 0 keeps every piece wholly inside or wholly outside. One load serves KW k-rows, so a
 // 32-deep K step takes one vector load per thread where the per-element gather took 16.
@@ -57,38 +59,40 @@ struct Params {
 // byte offset of 16-byte chunk c of k-row r in an Xcol stage
 __host__ __device__ constexpr int xoff(int r, int c) { return r * 256 + ((c ^ (4 * (r & 3))) * 16); }
 
-template <int KW, int PL, int G>
+template <int KW, int PL, int G, int S>
 struct Geometry {
   static_assert(G == 8 || G == 4, "pieces of 8 or 4 pixels");
   static_assert(PL >= 0 && PL < G, "left pad within one piece");
+  static_assert(S == 1 || S == 2, "stride 1 or 2");
   static constexpr int kKR = 16 * KW;                    // k-rows per slice
   static constexpr int kWPitch = 32 * KW + 16;           // weight row bytes in LDS: an odd number of chunks
   static constexpr int kM0 = (G - PL) % G;               // first needed element within the first piece
-  static constexpr int kPieces = (kM0 + KW - 1 + G + G - 1) / G;  // aligned pieces covering all KW windows
+  static constexpr int kLast = kM0 + KW - 1 + S * (G - 1);  // last needed element
+  static constexpr int kPieces = kLast / G + 1;          // aligned pieces covering all KW windows
   static constexpr int kDw = G / 2;                      // dwords per piece
   static constexpr int kGroups = kBN / G;                // pieces per k-row of a tile
   static constexpr int kItems = kRuns * kGroups / kThreads;  // (run, piece) items per thread and slice
 };
 
-template <int BM, int KW, int PL, int G>
+template <int BM, int KW, int PL, int G, int S>
 constexpr int rowvec_stage_bytes() {
-  return Geometry<KW, PL, G>::kKR * 256 + BM * Geometry<KW, PL, G>::kWPitch;
+  return Geometry<KW, PL, G, S>::kKR * 256 + BM * Geometry<KW, PL, G, S>::kWPitch;
 }
 }  // namespace convr
 
-template <typename Tag, int kMI, int KW, int PL, int G>
+template <typename Tag, int kMI, int KW, int PL, int G, int S>
 __global__ __launch_bounds__(convr::kThreads, 2) void conv2d_rowvec_kernel(const uint16_t* __restrict__ x,
                                                                         const uint16_t* __restrict__ wt,
                                                                         uint16_t* __restrict__ y,
                                                                         const void* __restrict__ bias,
                                                                         convr::Params s) {
   using namespace convr;
-  using Geo = Geometry<KW, PL, G>;
+  using Geo = Geometry<KW, PL, G, S>;
   using Hf = Half16<Tag>;
   constexpr int BM = 64 * kMI;
   constexpr int KR = Geo::kKR;
   constexpr int kXBytes = KR * 256;
-  constexpr int kStage = rowvec_stage_bytes<BM, KW, PL, G>();
+  constexpr int kStage = rowvec_stage_bytes<BM, KW, PL, G, S>();
   constexpr int kWChunks = BM * 2 * KW;  // 16-byte weight chunks per slice
   constexpr int kWPerThread = (kWChunks + kThreads - 1) / kThreads;
   using Piece = typename std::conditional<G == 8, u32x4, u32x2>::type;
@@ -112,8 +116,8 @@ __global__ __launch_bounds__(convr::kThreads, 2) void conv2d_rowvec_kernel(const
   const uint32_t jp = (piece_ok ? j0 : 0) - jn * s.P;
   const uint32_t jho = fdiv(jp, s.div_wo);
   const int wo0 = (int)(jp - jho * s.wo);
-  const int hbase = (int)jho - s.pt;                   // input row of kh = 0
-  const int pc0 = (wo0 - PL + G) / G - 1;              // first aligned input piece (may be -1)
+  const int hbase = S * (int)jho - s.pt;               // input row of kh = 0
+  const int pc0 = (S * wo0 - PL + G) / G - 1;          // first aligned input piece (may be -1)
   const int wpieces = s.w / G;
   const long long hw = (long long)s.h * s.w;
   const uint16_t* xn = x + (long long)jn * s.c * hw;
@@ -122,7 +126,7 @@ __global__ __launch_bounds__(convr::kThreads, 2) void conv2d_rowvec_kernel(const
   Piece raw[2][Geo::kItems][Geo::kPieces];
   u32x4 rw[2][kWPerThread];
   auto load_regs = [&](int kt, auto set_tag) {
-    constexpr int S = decltype(set_tag)::value;
+    constexpr int SET = decltype(set_tag)::value;
 #pragma unroll
     for (int it = 0; it < Geo::kItems; ++it) {
       const int run = kt * kRuns + q0 + it * (kRuns / Geo::kItems);
@@ -133,7 +137,7 @@ __global__ __launch_bounds__(convr::kThreads, 2) void conv2d_rowvec_kernel(const
 #pragma unroll
       for (int p = 0; p < Geo::kPieces; ++p) {
         const bool ok = row_ok && (unsigned)(pc0 + p) < (unsigned)wpieces;
-        raw[S][it][p] = ok ? *reinterpret_cast<const Piece*>(src + G * p) : Piece{};
+        raw[SET][it][p] = ok ? *reinterpret_cast<const Piece*>(src + G * p) : Piece{};
       }
     }
     const int k0 = kt * KR;
@@ -142,26 +146,25 @@ __global__ __launch_bounds__(convr::kThreads, 2) void conv2d_rowvec_kernel(const
       const int ci = tid + kThreads * i;
       const int row = ci / (2 * KW), kc = ci - row * (2 * KW);
       const int f = m0 + row, k = k0 + 8 * kc;
-      rw[S][i] = (ci < kWChunks && f < s.f && k < s.K) ? ld16(wt + (long long)f * s.K + k) : u32x4{0, 0, 0, 0};
+      rw[SET][i] = (ci < kWChunks && f < s.f && k < s.K) ? ld16(wt + (long long)f * s.K + k) : u32x4{0, 0, 0, 0};
     }
   };
-  // window kw of item `it`: elements kM0 + kw .. + G-1 of its concatenated pieces
+  // window kw of item `it`: elements kM0 + kw + S u (u < G) of its concatenated pieces
   auto window = [&](int it, auto set_tag, auto kw_tag) -> Piece {
-    constexpr int S = decltype(set_tag)::value;
+    constexpr int SET = decltype(set_tag)::value;
     constexpr int st = Geo::kM0 + decltype(kw_tag)::value;
+    constexpr int kDw = Geo::kDw;
+    auto dw = [&](int i) -> uint32_t { return raw[SET][it][i / kDw][i % kDw]; };
     Piece out;
 #pragma unroll
-    for (int d = 0; d < Geo::kDw; ++d) {
-      constexpr int kDw = Geo::kDw;
-      const int e = st + 2 * d;  // first element of output dword d
-      const int lo = e >> 1;
-      const uint32_t a = raw[S][it][lo / kDw][lo % kDw];
-      if ((st & 1) == 0) {
-        out[d] = a;
+    for (int d = 0; d < kDw; ++d) {
+      const int e = st + 2 * S * d;  // element of output pixel 2d; pixel 2d+1 is element e + S
+      if constexpr (S == 1) {
+        if ((st & 1) == 0) out[d] = dw(e >> 1);
+        else out[d] = __builtin_amdgcn_alignbyte(dw((e >> 1) + 1), dw(e >> 1), 2);
       } else {
-        const int hi_ = lo + 1;
-        const uint32_t b = raw[S][it][hi_ / kDw][hi_ % kDw];
-        out[d] = __builtin_amdgcn_alignbyte(b, a, 2);
+        if ((st & 1) == 0) out[d] = lo_halves(dw(e >> 1), dw((e >> 1) + 1));
+        else out[d] = hi_halves(dw(e >> 1), dw((e >> 1) + 1));
       }
     }
     return out;
@@ -297,7 +300,8 @@ inline int conv_rowvec_piece(const ConvShape& s) {
 inline bool conv_rowvec_supported(const ConvShape& s) {
   const long long K = (long long)s.c * s.kh * s.kw;
   const bool window = (s.kw == 3 && s.pl == 1) || (s.kw == 1 && s.pl == 0);
-  return window && s.sh == 1 && s.sw == 1 && s.dh == 1 && s.dw == 1 && conv_rowvec_piece(s) != 0 && K % 8 == 0 &&
+  return window && (s.sh == 1 || s.sh == 2) && s.sw == s.sh && s.dh == 1 && s.dw == 1 && conv_rowvec_piece(s) != 0 &&
+         K % 8 == 0 &&
          s.kh >= 1 && s.ho >= 1 && s.wo >= 1 && K < (1ll << 30) && (long long)s.n * s.ho * s.wo < (1ll << 31) &&
          (long long)s.c * s.kh < (1ll << 30) && (long long)s.n * s.c * s.h * s.w < (1ll << 40);
 }
@@ -333,17 +337,21 @@ hipError_t launch_conv2d_rowvec(const uint16_t* x, const uint16_t* w, uint16_t* 
   const int mi = conv_rowvec_mi(s);
   const int piece = conv_rowvec_piece(s);
   const int grid = ((s.f + 64 * mi - 1) / (64 * mi)) * ((p.NP + convr::kBN - 1) / convr::kBN);
-#define KG_CONV_RV(MI, KW_, PL_, G_) \
-  hipLaunchKernelGGL((conv2d_rowvec_kernel<Tag, MI, KW_, PL_, G_>), dim3(grid), dim3(convr::kThreads), 0, stream, x, w, y, bias, p)
-#define KG_CONV_RV_G(KW_, PL_, G_) \
-  if (mi == 2) KG_CONV_RV(2, KW_, PL_, G_); \
-  else KG_CONV_RV(1, KW_, PL_, G_)
+#define KG_CONV_RV(MI, KW_, PL_, G_, S_)                                                                     \
+  hipLaunchKernelGGL((conv2d_rowvec_kernel<Tag, MI, KW_, PL_, G_, S_>), dim3(grid), dim3(convr::kThreads), 0, stream, x, \
+                     w, y, bias, p)
+#define KG_CONV_RV_MI(KW_, PL_, G_, S_) \
+  if (mi == 2) KG_CONV_RV(2, KW_, PL_, G_, S_); \
+  else KG_CONV_RV(1, KW_, PL_, G_, S_)
+#define KG_CONV_RV_G(KW_, PL_, S_) \
+  if (piece == 8) { KG_CONV_RV_MI(KW_, PL_, 8, S_); } else { KG_CONV_RV_MI(KW_, PL_, 4, S_); }
   if (s.kw == 3) {
-    if (piece == 8) { KG_CONV_RV_G(3, 1, 8); } else { KG_CONV_RV_G(3, 1, 4); }
+    if (s.sh == 1) { KG_CONV_RV_G(3, 1, 1) } else { KG_CONV_RV_G(3, 1, 2) }
   } else {
-    if (piece == 8) { KG_CONV_RV_G(1, 0, 8); } else { KG_CONV_RV_G(1, 0, 4); }
+    if (s.sh == 1) { KG_CONV_RV_G(1, 0, 1) } else { KG_CONV_RV_G(1, 0, 2) }
   }
 #undef KG_CONV_RV_G
+#undef KG_CONV_RV_MI
 #undef KG_CONV_RV
   return hipGetLastError();
 }

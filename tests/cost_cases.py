@@ -10,7 +10,7 @@ dispatch i of the counter run is case i. Cases cover every kernel choice the mod
 pipelined MFMA GEMM with 256- and 128-row tiles and with ragged edges, the fp32 MFMA GEMM
 aligned and ragged, the fp32 split-K GEMM, the SIMT GEMM, the MFMA conv with four and with two live waves and a
 ragged last row block, the implicit-GEMM conv (16-bit and fp32) and its 16-bit row-piece form
-(8- and 4-pixel pieces, 3x3 and 1x1), and the 16-bit and fp32 MFMA attention kernels for D=128 and D=64,
+(8- and 4-pixel pieces, 3x3 and 1x1, stride 1 and 2), and the 16-bit and fp32 MFMA attention kernels for D=128 and D=64,
 causal and not, with ragged query and key tails.
 """
 
@@ -40,7 +40,7 @@ CASES = (
      (1, 1, 1, 1, 1, 1, 1, 1)),
     ("conv_f16_2x64x12x24", "conv2d", "float16", ((2, 64, 12, 24), (2, 64, 12, 24), (64, 64, 3, 3)),
      (1, 1, 1, 1, 1, 1, 1, 1)),
-    ("conv_f16_igemm_2x64x56x56_s2", "conv2d", "float16", ((2, 64, 28, 28), (2, 64, 56, 56), (64, 64, 3, 3)),
+    ("conv_f16_igemm_2x64x50x50_s2", "conv2d", "float16", ((2, 64, 25, 25), (2, 64, 50, 50), (64, 64, 3, 3)),
      (2, 2, 1, 1, 1, 1, 1, 1)),
     ("conv_f32_igemm_1x40x19x23_f96", "conv2d", "float32", ((1, 96, 18, 12), (1, 40, 19, 23), (96, 40, 3, 3)),
      (1, 2, 2, 1, 2, 1, 0, 3)),
@@ -48,6 +48,8 @@ CASES = (
      (1, 1, 1, 1, 1, 1, 1, 1)),
     ("conv_bf16_rowvec_1x1_2x64x16x32_f96", "conv2d", "bfloat16", ((2, 96, 16, 32), (2, 64, 16, 32), (96, 64, 1, 1)),
      (1, 1, 1, 1, 0, 0, 0, 0)),
+    ("conv_f16_rowvec_s2_2x64x56x56", "conv2d", "float16", ((2, 128, 28, 28), (2, 64, 56, 56), (128, 64, 3, 3)),
+     (2, 2, 1, 1, 1, 1, 1, 1)),
     ("fa_bf16_c4", "flash_attention", "bfloat16", ((4, 32, 2048, 128),) * 4, (128, 64, 0.088388, 0)),
     ("fa_bf16_causal_1x4x4096x128", "flash_attention", "bfloat16", ((1, 4, 4096, 128),) * 4, (128, 64, 0.088388, 1)),
     ("fa_f16_causal_1x2x1000x64", "flash_attention", "float16", ((1, 2, 1000, 64),) * 4, (128, 64, 0.125, 1)),

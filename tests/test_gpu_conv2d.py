@@ -195,13 +195,13 @@ def test_16bit_3x3(device, oracle_mod, dtype_name, xs, ws, bias):
     assert_h16_close(to_numpy(out), ref, what=f"{dtype_name} {xs} bias={bias}")
 
 
-def _rowvec_mfma(xs, ws, pad):
+def _rowvec_mfma(xs, ws, stride, pad):
     """MFMA instructions of the row-piece implicit GEMM (128-pixel tiles, 16-run K slices of
     KW steps, 4 waves x MI x 2 blocks; MI = 2 for F > 64 with >= 512 workgroups)."""
 
     n, c, h, w = xs
     f, _, kh, kw = ws
-    ho, wo = out_hw(xs, ws, (1, 1), (1, 1), pad)
+    ho, wo = out_hw(xs, ws, stride, (1, 1), pad)
     cols = -(-(n * ho * wo) // 128)
     mi = 2 if f > 64 and -(-f // 128) * cols >= 512 else 1
     return -(-f // (64 * mi)) * cols * -(-(c * kh) // 16) * 4 * mi * 2 * kw
@@ -209,29 +209,34 @@ def _rowvec_mfma(xs, ws, pad):
 
 @pytest.mark.parametrize("dtype_name", ["float16", "bfloat16"])
 @pytest.mark.parametrize(
-    "xs,ws,pad,bias,images",
+    "xs,ws,stride,pad,bias,images",
     [
-        ((2, 48, 16, 64), (64, 48, 3, 3), (1, 1, 1, 1), "f32", None),  # 8-pixel pieces
-        ((2, 40, 12, 28), (80, 40, 3, 3), (1, 1, 1, 1), "same", None),  # 4-pixel pieces, F = 80, K slices ragged
-        ((1, 16, 9, 24), (32, 16, 5, 3), (2, 2, 1, 1), None, None),  # KH = 5
-        ((2, 24, 10, 16), (48, 24, 3, 3), (0, 2, 1, 1), "f32", None),  # asymmetric vertical pads
-        ((2, 32, 6, 28), (40, 32, 1, 1), (0, 0, 0, 4), "same", None),  # 1x1, right pad: Wo = 32 > W
-        ((16, 32, 64, 64), (128, 32, 3, 3), (1, 1, 1, 1), "f32", (0, 15)),  # 128-filter tiles
+        ((2, 48, 16, 64), (64, 48, 3, 3), 1, (1, 1, 1, 1), "f32", None),  # 8-pixel pieces
+        ((2, 40, 12, 28), (80, 40, 3, 3), 1, (1, 1, 1, 1), "same", None),  # 4-pixel pieces, F = 80, K slices ragged
+        ((1, 16, 9, 24), (32, 16, 5, 3), 1, (2, 2, 1, 1), None, None),  # KH = 5
+        ((2, 24, 10, 16), (48, 24, 3, 3), 1, (0, 2, 1, 1), "f32", None),  # asymmetric vertical pads
+        ((2, 32, 6, 28), (40, 32, 1, 1), 1, (0, 0, 0, 4), "same", None),  # 1x1, right pad: Wo = 32 > W
+        ((16, 32, 64, 64), (128, 32, 3, 3), 1, (1, 1, 1, 1), "f32", (0, 15)),  # 128-filter tiles
+        ((2, 64, 56, 56), (128, 64, 3, 3), 2, (1, 1, 1, 1), None, None),  # stride 2, Wo = 28: 4-pixel pieces
+        ((1, 24, 17, 32), (40, 24, 3, 3), 2, (1, 0, 1, 1), "f32", None),  # stride 2, odd H, 8-pixel pieces
+        ((2, 32, 32, 64), (64, 32, 1, 1), 2, (0, 0, 0, 0), "same", None),  # 1x1 stride 2
+        ((1, 16, 8, 40), (24, 16, 1, 1), 2, (0, 0, 0, 0), None, None),  # 1x1 stride 2, Wo = 20
     ],
-    ids=["p8", "p4_f80", "kh5", "pads_0_2", "1x1_rpad", "bm128"],
+    ids=["p8", "p4_f80", "kh5", "pads_0_2", "1x1_rpad", "bm128", "s2_p4", "s2_p8", "1x1_s2", "1x1_s2_p4"],
 )
-def test_row_piece_path(device, oracle_mod, dtype_name, xs, ws, pad, bias, images):
-    """16-bit convs of stride 1 whose rows split into whole 8- or 4-pixel pieces, with a 3-wide
-    window and left pad 1 or a 1-wide window and left pad 0: each thread loads aligned row
-    pieces once for all taps of a (c, kh) run and builds the shifted windows in registers.
-    The entry's cost query must count this kernel's MFMAs (so the case runs the row-piece
-    path); output against the oracle on the identically rounded inputs (`images`: the
-    images checked, the rest of the batch only runs)."""
+def test_row_piece_path(device, oracle_mod, dtype_name, xs, ws, stride, pad, bias, images):
+    """16-bit convs of stride 1 or 2 whose rows split into whole 8- or 4-pixel pieces, with a
+    3-wide window and left pad 1 or a 1-wide window and left pad 0: each thread loads aligned
+    row pieces once for all taps of a (c, kh) run and builds the windows in registers. The
+    entry's cost query must count this kernel's MFMAs (so the case runs the row-piece path);
+    output against the oracle on the identically rounded inputs (`images`: the images
+    checked, the rest of the batch only runs)."""
 
     import torch
 
     dt = getattr(torch, dtype_name)
-    rng = np.random.default_rng(sum(xs) + sum(ws) + sum(pad))
+    st = (stride, stride)
+    rng = np.random.default_rng(sum(xs) + sum(ws) + sum(pad) + stride)
     xt, x = round_to(rng.standard_normal(xs), dt)
     bound = np.sqrt(6.0 / (ws[1] * ws[2] * ws[3]))
     wt, w = round_to(rng.uniform(-bound, bound, size=ws), dt)
@@ -240,17 +245,17 @@ def test_row_piece_path(device, oracle_mod, dtype_name, xs, ws, pad, bias, image
         b = bt = rng.normal(size=(ws[0],)).astype(np.float32)
     elif bias == "same":
         bt, b = round_to(rng.normal(size=(ws[0],)).astype(np.float32), dt)
-    ho, wo = out_hw(xs, ws, (1, 1), (1, 1), pad)
+    ho, wo = out_hw(xs, ws, st, (1, 1), pad)
     spec = [native.TensorSpec((xs[0], ws[0], ho, wo), dtype_name), native.TensorSpec(xs, dtype_name),
             native.TensorSpec(ws, dtype_name),
             None if bt is None else native.TensorSpec((ws[0],), "float32" if bias == "f32" else dtype_name),
-            1, 1, 1, 1, *pad]
-    assert native.cost("conv2d", spec)["MFMA"] == _rowvec_mfma(xs, ws, pad)
-    out = to_numpy(run(device, dt, xt, wt, bt, (1, 1), (1, 1), pad))
+            stride, stride, 1, 1, *pad]
+    assert native.cost("conv2d", spec)["MFMA"] == _rowvec_mfma(xs, ws, st, pad)
+    out = to_numpy(run(device, dt, xt, wt, bt, st, (1, 1), pad))
     assert np.isfinite(out).all()
     sel = slice(None) if images is None else list(images)
-    ref = oracle_mod.conv2d_demo(x[sel], w, b, (1, 1), (1, 1), pad, (16, 16, 1, 8, 16))
-    assert_h16_close(out[sel], ref, what=f"{dtype_name} {xs} {ws} p={pad} bias={bias}")
+    ref = oracle_mod.conv2d_demo(x[sel], w, b, st, (1, 1), pad, (16, 16, 1, 8, 16))
+    assert_h16_close(out[sel], ref, what=f"{dtype_name} {xs} {ws} s={stride} p={pad} bias={bias}")
 
 
 def test_c3_full_size_fp16(device, oracle_mod):
