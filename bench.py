@@ -514,8 +514,9 @@ def main() -> int:
             for r in result["secondary"]:
                 if r["key"] in baselines:
                     r["cpu_baseline"] = baselines[r["key"]]
-                    log(f"[bench] cpu baseline {r['key']}: {baselines[r['key']]['value'] * 1e3:.3f} GFLOP/s "
-                        f"({baselines[r['key']]['sample_s'] if 'sample_s' in baselines[r['key']] else ''} s)")
+                    b = baselines[r["key"]]
+                    how = f"{b['sample_s']} s" if "sample_s" in b else b.get("note", "")
+                    log(f"[bench] cpu baseline {r['key']}: {b['value'] * 1e3:.3f} GFLOP/s ({how})")
     print(json.dumps(result), flush=True)
     return 0
 
