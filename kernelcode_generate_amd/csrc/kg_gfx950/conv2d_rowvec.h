@@ -1,8 +1,9 @@
-// Implicit-GEMM conv2d on gfx950 MFMA for 16-bit NCHW convs of stride S = 1 or 2 (both
-// directions) and dilation 1 whose input and output rows split into whole pieces of G
-// pixels (W % G == 0 and Wo % G == 0, G = 8 or 4), with a KW = 3 window and left pad 1 or a
-// KW = 1 window and left pad 0 (any C, F, KH, top/bottom pads; C KH KW a multiple of 8).
-// fp32 accumulation.
+// Implicit-GEMM conv2d on gfx950 MFMA for NCHW convs of stride S = 1 or 2 (both directions)
+// and dilation 1 whose input and output rows split into whole pieces of G pixels (W % G == 0
+// and Wo % G == 0; 16-bit: G = 8 or 4, fp32: G = 4), with a KW = 3 window and left pad 1 or
+// a KW = 1 window and left pad 0 (any C, F, KH, top/bottom pads; C KH KW a multiple of 8,
+// fp32: of 4). fp32 accumulation. The 16-bit kernel is described first; the fp32 one
+// (conv2d_rowvec_f32_kernel) differs in its MFMA and operand reads.
 //
 // GEMM view as in conv2d_igemm.h: Y[n][f][p] = sum_k W[f][k] Xcol[k][(n, p)] with k =
 // (c, kh, kw) in the weight's own order. What differs is how Xcol reaches LDS. The k-row
@@ -289,6 +290,199 @@ __global__ __launch_bounds__(convr::kThreads, 2) void conv2d_rowvec_kernel(const
   }
 }
 
+// fp32 form of the same scheme, on v_mfma_f32_32x32x2_f32 (one k per lane and operand):
+// 4-pixel (16-byte) pieces, K slices of 8 (c, kh) runs x KW taps (8 KW k-rows). Xcol rows
+// are 128 fp32 pixels padded to 544 bytes, so the two k-rows one operand read covers (4
+// apart, see below) fall 32 banks apart, and the MFMA operand is one ds_read_b32 per lane.
+// Weights are [f][8 KW k] rows read as 16-byte chunks of 4 k: lane half h of MFMA kk of
+// 8-k group g takes k = 8g + 4h + kk from its weight chunk, and the Xcol read takes the
+// same k-row, so both operands follow one (permuted) contraction order.
+namespace convr {
+constexpr int kRunsF32 = 8;        // (c, kh) runs per fp32 K slice
+constexpr int kXPitchF32 = 544;    // bytes per fp32 Xcol row: 512 + 32
+template <int KW, int PL, int S>
+struct GeometryF32 {
+  static constexpr int G = 4;
+  static_assert(PL >= 0 && PL < G, "left pad within one piece");
+  static_assert(S == 1 || S == 2, "stride 1 or 2");
+  static constexpr int kKR = kRunsF32 * KW;                 // k-rows per slice
+  static constexpr int kWPitch = 4 * kKR + 16;              // an odd number of 16-byte chunks
+  static constexpr int kM0 = (G - PL) % G;
+  static constexpr int kLast = kM0 + KW - 1 + S * (G - 1);
+  static constexpr int kPieces = kLast / G + 1;
+  static constexpr int kGroups = kBN / G;                   // 32 pieces per k-row of a tile
+  static_assert(kRunsF32 * kGroups == kThreads, "one (run, piece) item per thread and slice");
+};
+template <int BM, int KW, int PL, int S>
+constexpr int rowvec_f32_stage_bytes() {
+  return GeometryF32<KW, PL, S>::kKR * kXPitchF32 + BM * GeometryF32<KW, PL, S>::kWPitch;
+}
+}  // namespace convr
+
+template <int kMI, int KW, int PL, int S>
+__global__ __launch_bounds__(convr::kThreads, 2) void conv2d_rowvec_f32_kernel(const float* __restrict__ x,
+                                                                              const float* __restrict__ wt,
+                                                                              float* __restrict__ y,
+                                                                              const float* __restrict__ bias,
+                                                                              convr::Params s) {
+  using namespace convr;
+  using Geo = GeometryF32<KW, PL, S>;
+  constexpr int G = Geo::G;
+  constexpr int BM = 64 * kMI;
+  constexpr int KR = Geo::kKR;
+  constexpr int kXBytes = KR * kXPitchF32;
+  constexpr int kStage = rowvec_f32_stage_bytes<BM, KW, PL, S>();
+  constexpr int kWChunks = BM * (KR / 4);  // 16-byte weight chunks per slice
+  constexpr int kWPerThread = (kWChunks + kThreads - 1) / kThreads;
+  __shared__ __attribute__((aligned(1024))) char lds[2 * kStage];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int tiles_m = (s.f + BM - 1) / BM;
+  const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int m0 = (logical % tiles_m) * BM;
+  const int n0 = (logical / tiles_m) * kBN;
+
+  const int g = tid % Geo::kGroups;
+  const int q = tid / Geo::kGroups;  // this thread's run within a slice
+  const int j0 = n0 + G * g;
+  const bool piece_ok = j0 < s.NP;
+  const uint32_t jn = fdiv(piece_ok ? j0 : 0, s.div_p);
+  const uint32_t jp = (piece_ok ? j0 : 0) - jn * s.P;
+  const uint32_t jho = fdiv(jp, s.div_wo);
+  const int wo0 = (int)(jp - jho * s.wo);
+  const int hbase = S * (int)jho - s.pt;
+  const int pc0 = (S * wo0 - PL + G) / G - 1;
+  const int wpieces = s.w / G;
+  const long long hw = (long long)s.h * s.w;
+  const float* xn = x + (long long)jn * s.c * hw;
+
+  u32x4 raw[2][Geo::kPieces];
+  u32x4 rw[2][kWPerThread];
+  auto load_regs = [&](int kt, auto set_tag) {
+    constexpr int SET = decltype(set_tag)::value;
+    const int run = kt * kRunsF32 + q;
+    const uint32_t c = fdiv((uint32_t)run, s.div_kh);
+    const int hi = hbase + (run - (int)c * s.kh);
+    const bool row_ok = piece_ok && run < s.runs && (unsigned)hi < (unsigned)s.h;
+    const float* src = xn + (long long)c * hw + (long long)hi * s.w + G * pc0;
+#pragma unroll
+    for (int p = 0; p < Geo::kPieces; ++p) {
+      const bool ok = row_ok && (unsigned)(pc0 + p) < (unsigned)wpieces;
+      raw[SET][p] = ok ? ld16(src + G * p) : u32x4{0, 0, 0, 0};
+    }
+    const int k0 = kt * KR;
+#pragma unroll
+    for (int i = 0; i < kWPerThread; ++i) {
+      const int ci = tid + kThreads * i;
+      const int row = ci / (KR / 4), kc = ci - row * (KR / 4);
+      const int f = m0 + row, k = k0 + 4 * kc;
+      rw[SET][i] = (ci < kWChunks && f < s.f && k < s.K) ? ld16(wt + (long long)f * s.K + k) : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto store_lds = [&](int buf, auto set_tag) {
+    constexpr int SET = decltype(set_tag)::value;
+    char* st = lds + buf * kStage;
+    auto put = [&](auto kw_tag) {
+      constexpr int kw = decltype(kw_tag)::value;
+      constexpr int e0 = Geo::kM0 + kw;  // element of output pixel u: e0 + S u
+      u32x4 v;
+#pragma unroll
+      for (int u = 0; u < G; ++u) v[u] = raw[SET][(e0 + S * u) / G][(e0 + S * u) % G];
+      *reinterpret_cast<u32x4*>(st + (KW * q + kw) * kXPitchF32 + 16 * g) = v;
+    };
+    put(Int<0>{});
+    if constexpr (KW > 1) put(Int<1>{});
+    if constexpr (KW > 2) put(Int<2>{});
+#pragma unroll
+    for (int i = 0; i < kWPerThread; ++i) {
+      const int ci = tid + kThreads * i;
+      if (ci < kWChunks) {
+        const int row = ci / (KR / 4), kc = ci - row * (KR / 4);
+        *reinterpret_cast<u32x4*>(st + kXBytes + row * Geo::kWPitch + 16 * kc) = rw[SET][i];
+      }
+    }
+  };
+
+  const int frag = lane & 31, h = lane >> 5;
+  int x_rd[2];  // Xcol k-row 4h (+ 8 g + kk) at pixel wn*64 + 32 b + lane % 32
+#pragma unroll
+  for (int b = 0; b < 2; ++b) x_rd[b] = 4 * h * kXPitchF32 + 4 * (wn * 64 + 32 * b + frag);
+  int w_rd[kMI];  // weight chunk 2g + h of filter row wm*BM/2 + 32 i + lane % 32
+#pragma unroll
+  for (int i = 0; i < kMI; ++i) w_rd[i] = kXBytes + (wm * (BM / 2) + 32 * i + frag) * Geo::kWPitch + 16 * h;
+
+  f32x16 acc[kMI][2];
+#pragma unroll
+  for (int i = 0; i < kMI; ++i)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][b][e] = 0.f;
+
+  const int nk = (s.runs + kRunsF32 - 1) / kRunsF32;
+  auto compute = [&](int buf) {
+    const uint32_t sbase = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)(lds + buf * kStage);
+#pragma unroll
+    for (int g8 = 0; g8 < KR / 8; ++g8) {
+      f32x4 af[kMI];
+#pragma unroll
+      for (int i = 0; i < kMI; ++i)
+        af[i] = *(const __attribute__((address_space(3))) f32x4*)(uintptr_t)(sbase + w_rd[i] + 32 * g8);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        float bf[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          bf[b] = *(const __attribute__((address_space(3))) float*)(uintptr_t)(sbase + x_rd[b] +
+                                                                               (8 * g8 + kk) * kXPitchF32);
+#pragma unroll
+        for (int i = 0; i < kMI; ++i)
+#pragma unroll
+          for (int b = 0; b < 2; ++b)
+            acc[i][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(bf[b], af[i][kk], acc[i][b], 0, 0, 0);
+      }
+    }
+  };
+  auto step = [&](int kt, auto par_tag) {
+    constexpr int par = decltype(par_tag)::value;
+    if (kt + 2 < nk) load_regs(kt + 2, Int<par>{});
+    compute(par);
+    if (kt + 1 < nk) store_lds(par ^ 1, Int<par ^ 1>{});
+    __syncthreads();
+  };
+  load_regs(0, Int<0>{});
+  store_lds(0, Int<0>{});
+  if (nk > 1) load_regs(1, Int<1>{});
+  __syncthreads();
+  for (int kt = 0; kt < nk; kt += 2) {
+    step(kt, Int<0>{});
+    if (kt + 1 < nk) step(kt + 1, Int<1>{});
+  }
+
+  // ---- epilogue: lane holds Y[f][j .. j+3] as in the 16-bit kernel; one 16-byte store ----
+#pragma unroll
+  for (int i = 0; i < kMI; ++i) {
+    const int f = m0 + wm * (BM / 2) + 32 * i + frag;
+    if (f >= s.f) continue;
+    const float bv = s.bias_kind != 0 ? bias[f] : 0.f;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const int j = n0 + wn * 64 + 32 * b + 8 * qq + 4 * h;
+        if (j >= s.NP) continue;
+        const uint32_t n = fdiv(j, s.div_p);
+        const uint32_t p = j - n * s.P;
+        *reinterpret_cast<f32x4*>(y + ((long long)n * s.f + f) * s.P + p) =
+            f32x4{acc[i][b][4 * qq] + bv, acc[i][b][4 * qq + 1] + bv, acc[i][b][4 * qq + 2] + bv,
+                  acc[i][b][4 * qq + 3] + bv};
+      }
+  }
+}
+
 // Pieces of G pixels: 8 when W and Wo are multiples of 8, else 4 when they are multiples of
 // 4, else 0 (the row-vector path does not apply).
 inline int conv_rowvec_piece(const ConvShape& s) {
@@ -297,12 +491,13 @@ inline int conv_rowvec_piece(const ConvShape& s) {
   return 0;
 }
 
-inline bool conv_rowvec_supported(const ConvShape& s) {
+// f32: fp32 operands (4-pixel pieces only, K % 4 == 0); else 16-bit (K % 8 == 0).
+inline bool conv_rowvec_supported(const ConvShape& s, bool f32 = false) {
   const long long K = (long long)s.c * s.kh * s.kw;
   const bool window = (s.kw == 3 && s.pl == 1) || (s.kw == 1 && s.pl == 0);
-  return window && (s.sh == 1 || s.sh == 2) && s.sw == s.sh && s.dh == 1 && s.dw == 1 && conv_rowvec_piece(s) != 0 &&
-         K % 8 == 0 &&
-         s.kh >= 1 && s.ho >= 1 && s.wo >= 1 && K < (1ll << 30) && (long long)s.n * s.ho * s.wo < (1ll << 31) &&
+  const bool pieces = f32 ? (s.w % 4 == 0 && s.wo % 4 == 0 && K % 4 == 0) : (conv_rowvec_piece(s) != 0 && K % 8 == 0);
+  return window && pieces && (s.sh == 1 || s.sh == 2) && s.sw == s.sh && s.dh == 1 && s.dw == 1 && s.kh >= 1 &&
+         s.ho >= 1 && s.wo >= 1 && K < (1ll << 30) && (long long)s.n * s.ho * s.wo < (1ll << 31) &&
          (long long)s.c * s.kh < (1ll << 30) && (long long)s.n * s.c * s.h * s.w < (1ll << 40);
 }
 
@@ -313,17 +508,17 @@ inline int conv_rowvec_mi(const ConvShape& s) {
   return s.f > 64 && ((s.f + 127) / 128) * cols >= 512 ? 2 : 1;
 }
 
-// MFMA instructions of one launch: per tile and slice, 4 waves x MI x 2 blocks x KW steps.
-inline long long conv_rowvec_mfma(const ConvShape& s) {
+// MFMA instructions of one launch: per tile and slice, 4 waves x MI x 2 blocks x (16-bit:
+// KW steps of 32x32x16; fp32: 4 KW MFMAs of 32x32x2).
+inline long long conv_rowvec_mfma(const ConvShape& s, bool f32 = false) {
   const long long mi = conv_rowvec_mi(s);
   const long long tiles = ((s.f + 64 * mi - 1) / (64 * mi)) * (((long long)s.n * s.ho * s.wo + convr::kBN - 1) / convr::kBN);
-  const long long slices = ((long long)s.c * s.kh + convr::kRuns - 1) / convr::kRuns;
-  return tiles * slices * 4 * mi * 2 * s.kw;
+  const long long runs = f32 ? convr::kRunsF32 : convr::kRuns;
+  const long long slices = ((long long)s.c * s.kh + runs - 1) / runs;
+  return tiles * slices * 4 * mi * 2 * s.kw * (f32 ? 4 : 1);
 }
 
-template <typename Tag>
-hipError_t launch_conv2d_rowvec(const uint16_t* x, const uint16_t* w, uint16_t* y, const void* bias, int bias_kind,
-                                const ConvShape& s, hipStream_t stream) {
+inline convr::Params conv_rowvec_params(const ConvShape& s, int bias_kind) {
   convr::Params p;
   p.n = s.n; p.c = s.c; p.h = s.h; p.w = s.w; p.f = s.f; p.kh = s.kh; p.ho = s.ho; p.wo = s.wo; p.pt = s.pt;
   p.K = s.c * s.kh * s.kw;
@@ -334,6 +529,33 @@ hipError_t launch_conv2d_rowvec(const uint16_t* x, const uint16_t* w, uint16_t* 
   p.div_kh = make_fast_div((uint32_t)s.kh);
   p.div_p = make_fast_div((uint32_t)p.P);
   p.div_wo = make_fast_div((uint32_t)s.wo);
+  return p;
+}
+
+// fp32 operands; a bias (kind 1 or 2) is fp32 either way.
+inline hipError_t launch_conv2d_rowvec_f32(const float* x, const float* w, float* y, const float* bias, int bias_kind,
+                                           const ConvShape& s, hipStream_t stream) {
+  const convr::Params p = conv_rowvec_params(s, bias_kind);
+  const int mi = conv_rowvec_mi(s);
+  const int grid = ((s.f + 64 * mi - 1) / (64 * mi)) * ((p.NP + convr::kBN - 1) / convr::kBN);
+#define KG_CONV_RVF(MI, KW_, PL_, S_) \
+  hipLaunchKernelGGL((conv2d_rowvec_f32_kernel<MI, KW_, PL_, S_>), dim3(grid), dim3(convr::kThreads), 0, stream, x, w, y, bias, p)
+#define KG_CONV_RVF_MI(KW_, PL_, S_) \
+  if (mi == 2) { KG_CONV_RVF(2, KW_, PL_, S_); } else { KG_CONV_RVF(1, KW_, PL_, S_); }
+  if (s.kw == 3) {
+    if (s.sh == 1) { KG_CONV_RVF_MI(3, 1, 1) } else { KG_CONV_RVF_MI(3, 1, 2) }
+  } else {
+    if (s.sh == 1) { KG_CONV_RVF_MI(1, 0, 1) } else { KG_CONV_RVF_MI(1, 0, 2) }
+  }
+#undef KG_CONV_RVF_MI
+#undef KG_CONV_RVF
+  return hipGetLastError();
+}
+
+template <typename Tag>
+hipError_t launch_conv2d_rowvec(const uint16_t* x, const uint16_t* w, uint16_t* y, const void* bias, int bias_kind,
+                                const ConvShape& s, hipStream_t stream) {
+  const convr::Params p = conv_rowvec_params(s, bias_kind);
   const int mi = conv_rowvec_mi(s);
   const int piece = conv_rowvec_piece(s);
   const int grid = ((s.f + 64 * mi - 1) / (64 * mi)) * ((p.NP + convr::kBN - 1) / convr::kBN);

@@ -582,8 +582,8 @@ int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
     long long mfma = 0;
     if (out.dtype != KG_DTYPE_F32 && conv_mfma_supported(s)) {  // live waves x 252 MFMAs per 7-row block
       mfma = (long long)s.n * ((s.h + convk::kRows - 1) / convk::kRows) * (s.w > 32 ? 4 : 2) * 252;
-    } else if (out.dtype != KG_DTYPE_F32 && conv_rowvec_supported(s)) {
-      mfma = conv_rowvec_mfma(s);
+    } else if (conv_rowvec_supported(s, out.dtype == KG_DTYPE_F32)) {
+      mfma = conv_rowvec_mfma(s, out.dtype == KG_DTYPE_F32);
     } else if (conv_igemm_supported(s)) {
       // implicit GEMM: per tile and 64-byte k slice, 4 waves x MI x 2 blocks x (2 MFMAs of
       // 32x32x16, or 8 of 32x32x2 for fp32)
@@ -614,6 +614,15 @@ int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
                                                bias_kind, s, g_stream);
     if (e != hipSuccess) return fail(kHipFailure, "conv2d(mfma): %s", hipGetErrorString(e));
     return finish_launch("conv2d(mfma)");
+  }
+  if (out.dtype == KG_DTYPE_F32 && conv_rowvec_supported(s, true) && aligned16(x.data) && aligned16(w.data) &&
+      aligned16(out.data)) {
+    hipError_t e = launch_conv2d_rowvec_f32(static_cast<const float*>(x.data), static_cast<const float*>(w.data),
+                                            static_cast<float*>(out.data),
+                                            bias.present ? static_cast<const float*>(bias.data) : nullptr,
+                                            bias.present ? 1 : 0, s, g_stream);
+    if (e != hipSuccess) return fail(kHipFailure, "conv2d(rowvec f32): %s", hipGetErrorString(e));
+    return finish_launch("conv2d(rowvec f32)");
   }
   if (out.dtype != KG_DTYPE_F32 && conv_rowvec_supported(s) && aligned16(x.data) && aligned16(w.data) &&
       aligned16(out.data)) {

@@ -195,19 +195,21 @@ def test_16bit_3x3(device, oracle_mod, dtype_name, xs, ws, bias):
     assert_h16_close(to_numpy(out), ref, what=f"{dtype_name} {xs} bias={bias}")
 
 
-def _rowvec_mfma(xs, ws, stride, pad):
-    """MFMA instructions of the row-piece implicit GEMM (128-pixel tiles, 16-run K slices of
-    KW steps, 4 waves x MI x 2 blocks; MI = 2 for F > 64 with >= 512 workgroups)."""
+def _rowvec_mfma(xs, ws, stride, pad, f32=False):
+    """MFMA instructions of the row-piece implicit GEMM (128-pixel tiles, 4 waves x MI x 2
+    blocks, MI = 2 for F > 64 with >= 512 workgroups; 16-bit: 16-run K slices of KW
+    32x32x16 steps, fp32: 8-run slices of 4 KW 32x32x2 MFMAs)."""
 
     n, c, h, w = xs
     f, _, kh, kw = ws
     ho, wo = out_hw(xs, ws, stride, (1, 1), pad)
     cols = -(-(n * ho * wo) // 128)
     mi = 2 if f > 64 and -(-f // 128) * cols >= 512 else 1
-    return -(-f // (64 * mi)) * cols * -(-(c * kh) // 16) * 4 * mi * 2 * kw
+    runs, per = (8, 4) if f32 else (16, 1)
+    return -(-f // (64 * mi)) * cols * -(-(c * kh) // runs) * 4 * mi * 2 * kw * per
 
 
-@pytest.mark.parametrize("dtype_name", ["float16", "bfloat16"])
+@pytest.mark.parametrize("dtype_name", ["float16", "bfloat16", "float32"])
 @pytest.mark.parametrize(
     "xs,ws,stride,pad,bias,images",
     [
@@ -225,23 +227,31 @@ def _rowvec_mfma(xs, ws, stride, pad):
     ids=["p8", "p4_f80", "kh5", "pads_0_2", "1x1_rpad", "bm128", "s2_p4", "s2_p8", "1x1_s2", "1x1_s2_p4"],
 )
 def test_row_piece_path(device, oracle_mod, dtype_name, xs, ws, stride, pad, bias, images):
-    """16-bit convs of stride 1 or 2 whose rows split into whole 8- or 4-pixel pieces, with a
-    3-wide window and left pad 1 or a 1-wide window and left pad 0: each thread loads aligned
-    row pieces once for all taps of a (c, kh) run and builds the windows in registers. The
-    entry's cost query must count this kernel's MFMAs (so the case runs the row-piece path);
-    output against the oracle on the identically rounded inputs (`images`: the images
-    checked, the rest of the batch only runs)."""
+    """Convs of stride 1 or 2 whose rows split into whole 8- or 4-pixel pieces (fp32: 4), with
+    a 3-wide window and left pad 1 or a 1-wide window and left pad 0: each thread loads
+    aligned row pieces once for all taps of a (c, kh) run and builds the windows in
+    registers. The entry's cost query must count this kernel's MFMAs (so the case runs the
+    row-piece path); output against the oracle on the identically rounded inputs (`images`:
+    the images checked, the rest of the batch only runs). fp32 bar: rtol 1e-4 / atol 1e-5
+    plus 4 sqrt(K) 2^-24 (|W| * |X|), the summation-order bound used for the implicit GEMM."""
 
     import torch
 
     dt = getattr(torch, dtype_name)
+    f32 = dt == torch.float32
     st = (stride, stride)
     rng = np.random.default_rng(sum(xs) + sum(ws) + sum(pad) + stride)
-    xt, x = round_to(rng.standard_normal(xs), dt)
-    bound = np.sqrt(6.0 / (ws[1] * ws[2] * ws[3]))
-    wt, w = round_to(rng.uniform(-bound, bound, size=ws), dt)
+    k = ws[1] * ws[2] * ws[3]
+    bound = np.sqrt(6.0 / k)
+    if f32:
+        x = rng.standard_normal(xs).astype(np.float32)
+        w = rng.uniform(-bound, bound, size=ws).astype(np.float32)
+        xt, wt = torch.from_numpy(x), torch.from_numpy(w)
+    else:
+        xt, x = round_to(rng.standard_normal(xs), dt)
+        wt, w = round_to(rng.uniform(-bound, bound, size=ws), dt)
     b = bt = None
-    if bias == "f32":
+    if bias == "f32" or (bias == "same" and f32):
         b = bt = rng.normal(size=(ws[0],)).astype(np.float32)
     elif bias == "same":
         bt, b = round_to(rng.normal(size=(ws[0],)).astype(np.float32), dt)
@@ -250,12 +260,20 @@ def test_row_piece_path(device, oracle_mod, dtype_name, xs, ws, stride, pad, bia
             native.TensorSpec(ws, dtype_name),
             None if bt is None else native.TensorSpec((ws[0],), "float32" if bias == "f32" else dtype_name),
             stride, stride, 1, 1, *pad]
-    assert native.cost("conv2d", spec)["MFMA"] == _rowvec_mfma(xs, ws, st, pad)
+    assert native.cost("conv2d", spec)["MFMA"] == _rowvec_mfma(xs, ws, st, pad, f32)
     out = to_numpy(run(device, dt, xt, wt, bt, st, (1, 1), pad))
     assert np.isfinite(out).all()
     sel = slice(None) if images is None else list(images)
-    ref = oracle_mod.conv2d_demo(x[sel], w, b, st, (1, 1), pad, (16, 16, 1, 8, 16))
-    assert_h16_close(out[sel], ref, what=f"{dtype_name} {xs} {ws} s={stride} p={pad} bias={bias}")
+    tiles = (16, 16, 1, 8, 16)
+    ref = oracle_mod.conv2d_demo(x[sel], w, b, st, (1, 1), pad, tiles)
+    what = f"{dtype_name} {xs} {ws} s={stride} p={pad} bias={bias}"
+    if f32:
+        terms = oracle_mod.conv2d_demo(np.abs(x[sel]), np.abs(w), None, st, (1, 1), pad, tiles).astype(np.float64)
+        tol = 1e-4 * np.abs(ref) + 1e-5 + 4 * np.sqrt(k) * 2.0 ** -24 * terms
+        err = np.abs(out[sel].astype(np.float64) - ref)
+        assert (err <= tol).all(), f"{what}: max err/tol {np.max(err / tol):.3g}"
+    else:
+        assert_h16_close(out[sel], ref, what=what)
 
 
 def test_c3_full_size_fp16(device, oracle_mod):
