@@ -9,8 +9,8 @@ copy kernels (named __amd_rocclr_*) that some host-to-device copies use, so libr
 dispatch i of the counter run is case i. Cases cover every kernel choice the model distinguishes: the
 pipelined MFMA GEMM with 256- and 128-row tiles and with ragged edges, the fp32 MFMA GEMM
 aligned and ragged, the fp32 split-K GEMM, the SIMT GEMM, the MFMA conv with four and with two live waves and a
-ragged last row block, the implicit-GEMM conv (16-bit and fp32) and its 16-bit row-piece form
-(8- and 4-pixel pieces, 3x3 and 1x1, stride 1 and 2), and the 16-bit and fp32 MFMA attention kernels for D=128 and D=64,
+ragged last row block, the implicit-GEMM conv (16-bit and fp32) and its row-piece form
+(16-bit 8- and 4-pixel pieces, 3x3 and 1x1, stride 1 and 2; fp32), and the 16-bit and fp32 MFMA attention kernels for D=128 and D=64,
 causal and not, with ragged query and key tails.
 """
 
@@ -50,6 +50,8 @@ CASES = (
      (1, 1, 1, 1, 0, 0, 0, 0)),
     ("conv_f16_rowvec_s2_2x64x56x56", "conv2d", "float16", ((2, 128, 28, 28), (2, 64, 56, 56), (128, 64, 3, 3)),
      (2, 2, 1, 1, 1, 1, 1, 1)),
+    ("conv_f32_rowvec_2x64x28x28_f96", "conv2d", "float32", ((2, 96, 28, 28), (2, 64, 28, 28), (96, 64, 3, 3)),
+     (1, 1, 1, 1, 1, 1, 1, 1)),
     ("fa_bf16_c4", "flash_attention", "bfloat16", ((4, 32, 2048, 128),) * 4, (128, 64, 0.088388, 0)),
     ("fa_bf16_causal_1x4x4096x128", "flash_attention", "bfloat16", ((1, 4, 4096, 128),) * 4, (128, 64, 0.088388, 1)),
     ("fa_f16_causal_1x2x1000x64", "flash_attention", "float16", ((1, 2, 1000, 64),) * 4, (128, 64, 0.125, 1)),
