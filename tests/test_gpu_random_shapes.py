@@ -1,6 +1,7 @@
-"""Seeded random shapes through the 16-bit matmul, 3x3 conv and attention entries against the
-CPU oracle: many small and ragged shapes in one place, including matmuls that take the split-K
-path (outputs of at most 64 tiles with K >= 512), strided output windows and every bias form."""
+"""Seeded random shapes through the 16-bit matmul, the conv (3x3 row-block kernel and the
+row-piece implicit GEMM, 16-bit and fp32) and attention entries against the CPU oracle: many
+small and ragged shapes in one place, including matmuls that take the split-K path (outputs of
+at most 64 tiles with K >= 512), strided output windows and every bias form."""
 
 from __future__ import annotations
 
@@ -79,6 +80,82 @@ def test_random_conv3x3(device, oracle_mod, n, h, w, dtype_name, bias_kind):
                   (1, 1), (1, 1), (1, 1, 1, 1))
     ref = oracle_mod.conv2d_demo(x, wgt, bias, (1, 1), (1, 1), (1, 1, 1, 1), (16, 16, 1, 8, 16))
     assert_h16_close(to_numpy(out), ref, what=f"conv {n}x64x{h}x{w} {dtype_name} bias={bias_kind}")
+
+
+def _rowvec_cases(n_cases=16, seed=20261206):
+    """Random convs the row-piece kernels take: stride 1 or 2, 3x3 (left pad 1) or 1x1 (pad 0),
+    W a multiple of 8 or 4 with a matching Wo, random C, F, H, vertical pads, dtype."""
+
+    rng = np.random.default_rng(seed)
+    cases = []
+    while len(cases) < n_cases:
+        i = len(cases)
+        k = [3, 1][i % 2]
+        stride = int(rng.integers(1, 3))
+        c = 8 * int(rng.integers(1, 13))
+        f = int(rng.integers(1, 150))
+        h = int(rng.integers(1, 24))
+        w = 4 * int(rng.integers(1, 25))
+        pt, pb = (int(rng.integers(0, 3)), int(rng.integers(0, 3))) if k == 3 else (0, 0)
+        pads = (pt, pb, 1, 1) if k == 3 else (0, 0, 0, 0)
+        ho = (h + pt + pb - k) // stride + 1
+        wo = (w + pads[2] + pads[3] - k) // stride + 1
+        if ho < 1 or wo < 1 or wo % 4:
+            continue
+        dt = ["float16", "bfloat16", "float32"][i % 3]
+        cases.append((int(rng.integers(1, 4)), c, h, w, f, k, stride, pads, dt, ["none", "f32", "same"][i % 3]))
+    return cases
+
+
+@pytest.mark.parametrize("n,c,h,w,f,k,stride,pads,dtype_name,bias_kind", _rowvec_cases())
+def test_random_row_piece_conv(device, oracle_mod, n, c, h, w, f, k, stride, pads, dtype_name, bias_kind):
+    """The row-piece implicit GEMM (8- or 4-pixel row pieces shared by all taps) on random
+    shapes; the fp32 bar adds the summation-order bound 4 sqrt(K) 2^-24 (|W| * |X|)."""
+
+    import torch
+
+    dt = getattr(torch, dtype_name)
+    f32 = dt == torch.float32
+    rng = np.random.default_rng(n * 7 + c * 11 + h * 13 + w * 17 + f * 19 + k + stride)
+    kk = c * k * k
+    bound = np.sqrt(6.0 / kk)
+    if f32:
+        x = rng.standard_normal((n, c, h, w)).astype(np.float32)
+        wgt = rng.uniform(-bound, bound, size=(f, c, k, k)).astype(np.float32)
+        xt, wt = torch.from_numpy(x), torch.from_numpy(wgt)
+    else:
+        xt, x = round_to(rng.standard_normal((n, c, h, w), dtype=np.float32), dt)
+        wt, wgt = round_to(rng.uniform(-bound, bound, size=(f, c, k, k)).astype(np.float32), dt)
+    bias = bt = None
+    if bias_kind == "f32" or (bias_kind == "same" and f32):
+        bias = bt = rng.standard_normal(f).astype(np.float32)
+    elif bias_kind == "same":
+        bt, bias = round_to(rng.standard_normal(f), dt)
+    ho = (h + pads[0] + pads[1] - k) // stride + 1
+    wo = (w + pads[2] + pads[3] - k) // stride + 1
+    out = torch.full((n, f, ho, wo), float("nan"), dtype=dt, device=device)
+    st = (stride, stride)
+    spec = [native.TensorSpec(tuple(out.shape), dtype_name), native.TensorSpec(tuple(xt.shape), dtype_name),
+            native.TensorSpec(tuple(wt.shape), dtype_name), None, stride, stride, 1, 1, *pads]
+    runs, per = (8, 4) if f32 else (16, 1)
+    cols = -(-(n * ho * wo) // 128)
+    mi = 2 if f > 64 and -(-f // 128) * cols >= 512 else 1
+    assert native.cost("conv2d", spec)["MFMA"] == -(-f // (64 * mi)) * cols * -(-(c * k) // runs) * 8 * mi * k * per
+    print(f"[random] row-piece conv N={n} C={c} H={h} W={w} F={f} {k}x{k} s{stride} p={pads} {dtype_name} "
+          f"bias={bias_kind}", flush=True)
+    native.conv2d(out, xt.to(device), wt.to(device), None if bt is None else torch.as_tensor(bt).to(device),
+                  st, (1, 1), pads)
+    got = to_numpy(out)
+    tiles = (16, 16, 1, 8, 16)
+    ref = oracle_mod.conv2d_demo(x, wgt, bias, st, (1, 1), pads, tiles)
+    what = f"row-piece conv {n}x{c}x{h}x{w} F={f} {k}x{k} s{stride} p={pads} {dtype_name} bias={bias_kind}"
+    if f32:
+        terms = oracle_mod.conv2d_demo(np.abs(x), np.abs(wgt), None, st, (1, 1), pads, tiles).astype(np.float64)
+        tol = 1e-4 * np.abs(ref) + 1e-5 + 4 * np.sqrt(kk) * 2.0 ** -24 * terms
+        err = np.abs(got.astype(np.float64) - ref)
+        assert (err <= tol).all(), f"{what}: max err/tol {np.max(err / tol):.3g}"
+    else:
+        assert_h16_close(got, ref, what=what)
 
 
 def _fa_cases(n_cases=10, seed=20261205):
