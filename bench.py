@@ -35,6 +35,7 @@ import json
 import math
 import os
 import re
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -399,6 +400,9 @@ def main() -> int:
     ap.add_argument("--mfma-ceiling", action="store_true",
                     help="analysis mode: the sustained MFMA rate with no operand movement, random and zero bf16 "
                          "operands (kg_gfx950_mfma_rate), as one JSON line")
+    ap.add_argument("--vs-library", action="store_true",
+                    help="analysis mode: the C2 GEMM and torch.matmul (hipBLASLt) on the same operands, timed in "
+                         "alternating blocks in one process, as one JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (reference point for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -434,6 +438,24 @@ def main() -> int:
         print(json.dumps({"mfma_ceiling": rates, "peak": PEAK_BF16_TFLOPS,
                           "kernel": "back-to-back v_mfma_f32_32x32x16_bf16 on register operands, 2048 workgroups x 4 waves"}),
               flush=True)
+        native.set_launch_mode(True, None)
+        return 0
+    if args.vs_library:
+        a, b, c = gemm_workload(dev, 4096, 4096, 4096, 20261202)
+        flop = 2.0 * 4096 ** 3
+        calls = {"ours": PreparedCall("kg_gfx950_matmul_entry", (c, a, b, None)),
+                 "hipblaslt": lambda: torch.matmul(a, b, out=c)}
+        rates = {name: [] for name in calls}
+        torch.cuda.synchronize()
+        for rnd in range(3):  # alternating blocks: both see the same clock and temperature drift
+            for name, fn in calls.items():
+                _, ev_ms, _ = time_steps(fn, args.steps, 20, SECONDARY_WARMUP_S)
+                rates[name].append(flop / (ev_ms * 1e-3) / 1e12)
+                log(f"[bench] round {rnd} {name}: {ev_ms * 1e3:.1f} us {rates[name][-1]:.1f} TFLOP/s")
+        print(json.dumps({"vs_library": {name: {"tflops_median": round(statistics.median(v), 1),
+                                                 "tflops_rounds": [round(x, 1) for x in v]}
+                                          for name, v in rates.items()},
+                          "workload": "bf16 4096^3, A,B ~ N(0,1)*0.02", "peak": PEAK_BF16_TFLOPS}), flush=True)
         native.set_launch_mode(True, None)
         return 0
     if args.only:
