@@ -409,7 +409,7 @@ def main() -> int:
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(
             "bench.py measures one MI355X: the gfx950 hot-path kernels are single-GPU and this build has no "
-            "multi-GPU path (sharding is described in DESIGN.md). Run with --gpus 1.",
+            "multi-GPU path. Run with --gpus 1.",
             file=sys.stderr,
         )
         return 2
