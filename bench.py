@@ -429,14 +429,16 @@ def main() -> int:
     native.set_launch_mode(False, stream.cuda_stream)
     if args.mfma_ceiling:
         rates = {}
-        for zeros in (False, True):
-            r = native.mfma_rate("bf16", zeros)
-            key = "zero_operands" if zeros else "random_operands"
-            rates[key] = {"tflops": round(r["tflops"], 1), "clock_ghz": round(r["clock_ghz"], 3),
-                          "frac_of_peak": round(r["tflops"] / PEAK_BF16_TFLOPS, 4)}
-            log(f"[bench] mfma ceiling, bf16 {key}: {r['tflops']:.1f} TFLOP/s at {r['clock_ghz']:.3f} GHz")
+        for shape, mfma_m in (("16x16x32", 16), ("32x32x16", 32)):
+            for zeros in (False, True):
+                r = native.mfma_rate("bf16", zeros, mfma_m=mfma_m)
+                key = f"{shape}_{'zero' if zeros else 'random'}_operands"
+                rates[key] = {"tflops": round(r["tflops"], 1), "clock_ghz": round(r["clock_ghz"], 3),
+                              "frac_of_peak": round(r["tflops"] / PEAK_BF16_TFLOPS, 4)}
+                log(f"[bench] mfma ceiling, bf16 {key}: {r['tflops']:.1f} TFLOP/s at {r['clock_ghz']:.3f} GHz")
         print(json.dumps({"mfma_ceiling": rates, "peak": PEAK_BF16_TFLOPS,
-                          "kernel": "back-to-back v_mfma_f32_32x32x16_bf16 on register operands, 2048 workgroups x 4 waves"}),
+                          "kernel": "back-to-back v_mfma_f32_{16x16x32,32x32x16}_bf16 on register operands, "
+                                    "2048 workgroups x 4 waves"}),
               flush=True)
         native.set_launch_mode(True, None)
         return 0
@@ -488,7 +490,7 @@ def main() -> int:
         "data": "synthetic: A,B ~ N(0,1)*0.02 (seeded torch generator on the device), resident in HBM",
         "config": {
             "workload": "bf16 matmul M=N=K=4096, row-major A[M,K] B[K,N], fp32 accumulate, bf16 out (BASELINE configs[1])",
-            "M": m, "N": n, "K": k, "kernel": "gemm_pipe_kernel 256x256 tiles, 8 waves, 4-stage HBM->LDS ring, v_mfma_f32_32x32x16_bf16",
+            "M": m, "N": n, "K": k, "kernel": "gemm_pipe_kernel 256x256 tiles, 8 waves, 4-stage HBM->LDS ring, v_mfma_f32_16x16x32_bf16",
         },
         "roofline": {
             "bound": "mfma",
@@ -504,10 +506,11 @@ def main() -> int:
     del a, b, c
     # the part's sustained matrix-core rate on this data (random bf16, no operand movement):
     # the power-limited ceiling the headline's fraction is read against
-    ceiling = native.mfma_rate("bf16", False)
+    ceiling = native.mfma_rate("bf16", False, mfma_m=16)
     result["roofline"]["mfma_ceiling"] = {
         "tflops": round(ceiling["tflops"], 1), "clock_ghz": round(ceiling["clock_ghz"], 3),
-        "what": "back-to-back v_mfma_f32_32x32x16_bf16 on N(0,1)*0.02 register operands (kg_gfx950_mfma_rate)"}
+        "what": "back-to-back v_mfma_f32_16x16x32_bf16 (the headline kernel's instruction) on N(0,1)*0.02 "
+                "register operands (kg_gfx950_mfma_rate)"}
     result["roofline"]["frac_of_mfma_ceiling"] = round(achieved / ceiling["tflops"], 4)
     log(f"[bench] mfma ceiling (random bf16 operands): {ceiling['tflops']:.1f} TFLOP/s at {ceiling['clock_ghz']:.3f} GHz; "
         f"headline {achieved / ceiling['tflops']:.3f} of it")

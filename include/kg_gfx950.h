@@ -144,15 +144,16 @@ int kg_gfx950_abi_version(void);
 
 /*
  * Measurement aid (no counterpart in the reference): the sustained rate of
- * v_mfma_f32_32x32x16_{bf16,f16} with no operand movement. `workgroups` workgroups of 4 waves
- * each load 8 operand registers once (N(0,1)*0.02 values, or zeros when zero_operands != 0)
- * and issue `iterations` x 8 back-to-back MFMAs into 4 accumulators; after two untimed launches
- * one launch is timed with HIP events. Writes the achieved TFLOP/s and the median clock the
- * workgroups saw (s_memtime ticks per s_memrealtime tick x 100 MHz). Allocates and frees its
- * own device buffers; synchronous on the null stream. 0, -1 (bad arguments) or -2 (HIP error).
+ * v_mfma_f32_32x32x16_{bf16,f16} (mfma_m = 32) or v_mfma_f32_16x16x32_{bf16,f16} (mfma_m = 16)
+ * with no operand movement. `workgroups` workgroups of 4 waves each load 8 operand registers
+ * once (N(0,1)*0.02 values, or zeros when zero_operands != 0) and issue `iterations` x 8
+ * back-to-back MFMAs into 8 accumulators; after two untimed launches one launch is timed with
+ * HIP events. Writes the achieved TFLOP/s and the median clock the workgroups saw (s_memtime
+ * ticks per s_memrealtime tick x 100 MHz). Allocates and frees its own device buffers;
+ * synchronous on the null stream. 0, -1 (bad arguments) or -2 (HIP error).
  */
-int kg_gfx950_mfma_rate(int dtype_code, int zero_operands, int iterations, int workgroups, double* tflops,
-                        double* clock_ghz);
+int kg_gfx950_mfma_rate(int dtype_code, int mfma_m, int zero_operands, int iterations, int workgroups,
+                        double* tflops, double* clock_ghz);
 
 /* Operations and cost kinds of kg_gfx950_cost. */
 enum {
@@ -165,7 +166,8 @@ enum {
   KG_COST_MFMA = 1,      /* wave-level MFMA instructions the chosen kernel issues (0 on SIMT paths) */
   KG_COST_HBM_READ = 2,  /* compulsory bytes read: every input element once */
   KG_COST_HBM_WRITE = 3, /* compulsory bytes written: every output element once */
-  KG_COST_KINDS = 4
+  KG_COST_MFMA_CYCLES = 4, /* SIMD cycles those MFMA instructions occupy (shapes differ per kernel) */
+  KG_COST_KINDS = 5
 };
 
 /*

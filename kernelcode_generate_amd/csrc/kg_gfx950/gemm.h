@@ -1,9 +1,10 @@
 // GEMM kernels for the matmul demos: out[M,N] = lhs[M,K] @ rhs[K,N] (+ bias[N]),
 // row-major, fp32 accumulation.
 //
-// gemm_pipe_kernel: bf16/f16 operands on gfx950 MFMA (v_mfma_f32_32x32x16_{bf16,f16}; the
-//   32x32x16 form is the one that reaches full matrix-core rate on gfx950, the 16x16x32
-//   form issues at half of it), any M, N % 8 == 0, K % 8 == 0.
+// gemm_pipe_kernel: bf16/f16 operands on gfx950 MFMA (v_mfma_f32_16x16x32_{bf16,f16}: the
+//   same FLOP per cycle as 32x32x16 at half the cycles per instruction; in this kernel, which
+//   runs at the part's power limit, it does the same work for less energy and so holds a
+//   higher clock), any M, N % 8 == 0, K % 8 == 0.
 //
 // gemm_simt_kernel: any dtype (f32/bf16/f16), any shape and stride; 64x64 LDS tiles,
 //   4x4 outputs per thread, fp32 FMA accumulation in k order.
@@ -15,7 +16,7 @@
 namespace kg_gfx950 {
 
 // gemm_pipe_kernel: kTM x 256 tiles (kTM = 256, or 128 when 256-row tiles would leave CUs idle) computed by
-//   8 waves (2 x 4 waves of kTM/2 x 64, two per SIMD) with 32x32x16 MFMAs. Both operands
+//   8 waves (2 x 4 waves of kTM/2 x 64, two per SIMD) with 16x16x32 MFMAs. Both operands
 //   are copied HBM -> LDS by global_load_lds_dwordx4 (no registers, no VALU work) through a
 //   kStages-deep ring of 32-deep K slices (kStages x (kTM/16 + 16) KiB; 4 by default, 2 or
 //   3 on request), so loads are issued kStages - 1 slices ahead of their use; every wave issues kTM/128 + 2 of a slice's copies (1 KiB
@@ -24,10 +25,12 @@ namespace kg_gfx950 {
 //   stay [k][n] as in HBM and the MFMA operand (8 consecutive k of one n) is read with two
 //   ds_read_b64_tr_b16: within each 16-lane group, lane j addresses 4 consecutive n of
 //   k-row j/4 and lane i receives k-rows 0..3 of column i. Chunk swizzles: lhs
-//   p = c ^ ((row >> 2) & 3), rhs p = c ^ 4(k & 3) -- the fragment reads hit distinct
-//   banks of the 64-bank LDS. Fragments are double-buffered in registers: while the MFMAs
-//   of one 16-deep half of a slice run, the other half (or the next slice's first half) is
-//   being read, and the per-slice barrier sits between the two halves.
+//   p = c ^ ((row >> 2) & 3), rhs p = c ^ (4(k & 3) ^ 2((k >> 3) & 1)) -- the fragment
+//   reads hit distinct banks of the 64-bank LDS. Each MFMA takes a whole 32-deep slice of a
+//   16 x 16 block; a wave's kTM/32 lhs blocks are split in two halves: while the MFMAs of
+//   the first half run, the second half's lhs fragments are read; while those of the second
+//   run, the next slice's rhs and first-half lhs fragments are read (two register sets,
+//   alternating by slice), and the per-slice barrier sits between the two halves.
 //   kRagged (M % kTM, N % 256 or K % 32 non-zero): the copies go through buffer loads whose
 //   out-of-range lanes land zeros in LDS (edge rows, edge column chunks, k >= K), and the
 //   epilogue stores only the rows and columns inside the matrix; the loop is unchanged.
@@ -47,7 +50,7 @@ constexpr int kBVecs = kBK * kBN / 8;  // 1024 u32x4 per rhs stage
 // LDS has 64 banks of 4 bytes: ds_read_b128 serves 16 lanes per cycle, 64-bit reads 32.
 // The swizzles are XOR masks, so the same mask maps an LDS slot back to its HBM chunk.
 __device__ __forceinline__ int a_mask(int row) { return (row >> 2) & 3; }
-__device__ __forceinline__ int b_mask(int k) { return 4 * (k & 3); }
+__device__ __forceinline__ int b_mask(int k) { return (4 * (k & 3)) ^ (2 * ((k >> 3) & 1)); }
 __device__ __forceinline__ int a_slot(int row, int c) { return row * 4 + (c ^ a_mask(row)); }
 __device__ __forceinline__ int b_slot(int k, int c) { return k * 32 + (c ^ b_mask(k)); }
 template <int S>
@@ -72,12 +75,14 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
     partial += (long long)blockIdx.y * M * N;
   }
   static_assert(kStages >= 2 && kStages <= 4, "ring depth");
-  constexpr int MI = kTM / 64;              // 32-row fragments per wave
+  constexpr int MB = kTM / 32;              // 16-row lhs blocks per wave
+  constexpr int MH = MB / 2;                // of them in each half slice
   constexpr int AP = kTM / 128;             // lhs copies per wave per slice
   constexpr int kPieces = AP + 2;           // copies per wave per slice: AP lhs, 2 rhs
-  constexpr int NR = MI + 4;                // fragment reads per half slice: MI lhs, 4 rhs
-  constexpr int NM = 2 * MI;                // MFMAs per half slice
-  constexpr int NSTEP = NM > NR ? NM : NR;  // interleave steps per half slice
+  constexpr int NRX = 4 + MH;               // read steps of a slice's set X: 4 rhs blocks, MH lhs blocks
+  constexpr int NM = 4 * MH;                // MFMAs per half slice: MH lhs blocks x 4 rhs blocks
+  constexpr int NS0 = NM > MH ? NM : MH;    // interleave steps of half 0 (MH lhs reads)
+  constexpr int NS1 = NM > NRX ? NM : NRX;  // interleave steps of half 1 (the next slice's first set)
   constexpr int kAVecs = kTM * kBK / 8;     // u32x4 per lhs stage
   __shared__ u32x4 lds_a[kStages][kAVecs];
   __shared__ u32x4 lds_b[kStages][kBVecs];
@@ -153,49 +158,52 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
     }
   };
 
-  // ---- fragment reads ----
-  // lhs block i is 32 rows below block 0 (same mask): +2048 bytes; rhs k-rows +4 (t) and
-  // +16 (ks) keep the mask: +2048 / +8192 bytes. Per-lane byte addresses, LDS base included.
-  const int frag_row = lane & 31;
-  const int frag_half = lane >> 5;
-  const int g = lane >> 4;
-  const int j16 = lane & 15;
-  const int b_nofs = 16 * (g & 1) + 4 * (j16 & 3);
-  const int b_kofs = 8 * (g >> 1) + (j16 >> 2);
-  uint32_t a_rd[2], b_rd[2];
+  // ---- fragment reads (v_mfma_f32_16x16x32: 16-row lhs blocks x 16-column rhs blocks, the
+  // whole 32-deep slice in one step) ----
+  // lhs block ib: rows wm*kTM/2 + 16 ib + lane%16, 16-byte chunk lane/16 (8 k): one
+  // ds_read_b128; block ib+1 is 16 rows on (same mask): +1024 bytes. rhs block nb: columns
+  // wn*64 + 16 nb + lane%16, k-rows 8*(lane/16) + 0..7 in two ds_read_b64_tr_b16 (k-rows +4:
+  // +2048 bytes, same mask). Per-lane byte addresses, LDS base included.
+  const int l16 = lane & 15;
+  const int lg = lane >> 4;
+  const uint32_t a_rd = lds_a0 + a_slot(wm * (kTM / 2) + l16, lg) * 16;
+  uint32_t b_rd[4];
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) a_rd[ks] = lds_a0 + a_slot(wm * (kTM / 2) + frag_row, 2 * ks + frag_half) * 16;
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int n = wn * 64 + j * 32 + b_nofs;
-    b_rd[j] = lds_b0 + b_slot(b_kofs, n >> 3) * 16 + (n & 7) * 2;
+  for (int nb = 0; nb < 4; ++nb) {
+    const int n = wn * 64 + nb * 16 + 4 * (l16 & 3);
+    b_rd[nb] = lds_b0 + b_slot(8 * lg + (l16 >> 2), n >> 3) * 16 + (n & 7) * 2;
   }
 
-  struct Frag {
-    u32x4 a[MI];
-    u32x4 b[2];
+  // A slice's fragments come in two sets: X (the 4 rhs blocks and lhs blocks 0..MH-1, read
+  // before the slice) and Y (lhs blocks MH..MB-1, read during its first half).
+  struct FragX {
+    u32x4 b[4];
+    u32x4 a[MH];
   };
-  // read #r (0..NR-1) of a fragment set: MI lhs b128 reads, then 4 rhs transposed reads
-  auto read_piece = [&](int s, int ks, Frag& f, int r) {
-    if (r < MI) {
-      f.a[r] = *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(a_rd[ks] + s * kAStage + r * 2048);
-    } else {
-      const int j = (r - MI) >> 1, t = (r - MI) & 1;
-      const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) s16x4*)(uintptr_t)(b_rd[j] + s * kBStage + t * 2048 + ks * 8192));
-      const u32x2 w = __builtin_bit_cast(u32x2, v);
-      f.b[j][2 * t] = w[0];
-      f.b[j][2 * t + 1] = w[1];
-    }
+  auto read_b = [&](int s, u32x4& f, int nb) {
+    const uint32_t ad = b_rd[nb] + s * kBStage;
+    const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(uintptr_t)ad);
+    const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4*)(uintptr_t)(ad + 2048));
+    const u32x2 w0 = __builtin_bit_cast(u32x2, v0), w1 = __builtin_bit_cast(u32x2, v1);
+    f = u32x4{w0[0], w0[1], w1[0], w1[1]};
+  };
+  auto read_a = [&](int s, int ib) -> u32x4 {
+    return *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(a_rd + s * kAStage + ib * 1024);
+  };
+  // read step r (0..NRX-1) of set X: the rhs blocks first (two transposed reads each), then lhs
+  auto read_x = [&](int s, FragX& f, int r) {
+    if (r < 4) read_b(s, f.b[r], r);
+    else f.a[r - 4] = read_a(s, r - 4);
   };
 
-  f32x16 acc[MI][2];
+  f32x4 acc[MB][4];
 #pragma unroll
-  for (int i = 0; i < MI; ++i)
+  for (int i = 0; i < MB; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+      for (int e = 0; e < 4; ++e) acc[i][j][e] = 0.f;
 
   const int ktiles = kRagged ? (K + kBK - 1) / kBK : K / kBK;
 #pragma unroll
@@ -210,21 +218,26 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
     else if (younger == 1) wait_and_barrier<kPieces>();
     else wait_and_barrier<0>();
   }
-  Frag f0, f1;
+  FragX fr[2];   // set X of slice kt is fr[kt & 1]; the next slice's is read into the other
+  u32x4 fy[MH];  // this slice's set Y
 #pragma unroll
-  for (int r = 0; r < NR; ++r) read_piece(0, 0, f0, r);
+  for (int r = 0; r < NRX; ++r) read_x(0, fr[0], r);
 
-  // One 32-deep slice in stage S: MFMAs of half 0 with the reads of half 1 slotted in
-  // between, barrier, MFMAs of half 1 with the next slice's first reads and this stage's
-  // refill copies slotted in between. kSteady: more slices follow and a refill is due.
-  auto slice = [&](int kt, auto stage_tag, auto steady_tag) {
+  // One 32-deep slice in stage S: the MFMAs of lhs blocks 0..MH-1 with the reads of set Y
+  // slotted in between, barrier, the MFMAs of blocks MH..MB-1 with the next slice's set X
+  // and this stage's refill copies slotted in between. kSteady: more slices follow and a
+  // refill is due.
+  auto slice = [&](int kt, auto stage_tag, auto par_tag, auto steady_tag) {
     constexpr int S = decltype(stage_tag)::value;
+    constexpr int P = decltype(par_tag)::value;
     constexpr bool kSteady = decltype(steady_tag)::value != 0;
+    FragX& fx = fr[P];
+    FragX& fn = fr[P ^ 1];
 #pragma unroll
-    for (int idx = 0; idx < NSTEP; ++idx) {
-      const int i = idx >> 1, j = idx & 1;
-      if (idx < NM) acc[i][j] = H::mfma32(f0.b[j], f0.a[i], acc[i][j]);
-      if (idx < NR) read_piece(S, 1, f1, idx);
+    for (int idx = 0; idx < NS0; ++idx) {
+      const int i = idx >> 2, j = idx & 3;
+      if (idx < NM) acc[i][j] = H::mfma16(fx.b[j], fx.a[i], acc[i][j]);
+      if (idx < MH) fy[idx] = read_a(S, MH + idx);
       __builtin_amdgcn_sched_barrier(0);
     }
     const bool more = kSteady || kt + 1 < ktiles;
@@ -239,10 +252,10 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
     }
     if (kSteady) {
 #pragma unroll
-      for (int idx = 0; idx < NSTEP; ++idx) {
-        const int i = idx >> 1, j = idx & 1;
-        if (idx < NM) acc[i][j] = H::mfma32(f1.b[j], f1.a[i], acc[i][j]);
-        if (idx < NR) read_piece((S + 1) % kStages, 0, f0, idx);
+      for (int idx = 0; idx < NS1; ++idx) {
+        const int i = idx >> 2, j = idx & 3;
+        if (idx < NM) acc[MH + i][j] = H::mfma16(fx.b[j], fy[i], acc[MH + i][j]);
+        if (idx < NRX) read_x((S + 1) % kStages, fn, idx);
         if ((idx & 1) && (idx >> 1) < kPieces) issue_piece(kt + kStages, S, idx >> 1);
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -252,41 +265,51 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
         for (int piece = 0; piece < kPieces; ++piece) issue_piece(kt + kStages, S, piece);
       if (more)
 #pragma unroll
-        for (int r = 0; r < NR; ++r) read_piece((S + 1) % kStages, 0, f0, r);
+        for (int r = 0; r < NRX; ++r) read_x((S + 1) % kStages, fn, r);
 #pragma unroll
       for (int idx = 0; idx < NM; ++idx) {
-        const int i = idx >> 1, j = idx & 1;
-        acc[i][j] = H::mfma32(f1.b[j], f1.a[i], acc[i][j]);
+        const int i = idx >> 2, j = idx & 3;
+        acc[MH + i][j] = H::mfma16(fx.b[j], fy[i], acc[MH + i][j]);
       }
     }
   };
 
+  // Slices are unrolled U at a time so that each one's stage (kt % kStages) and register set
+  // (kt & 1) are compile-time constants.
+  constexpr int U = kStages % 2 == 0 ? kStages : 2 * kStages;
+  auto unrolled = [&](int kt0, auto steady_tag) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      // u as a constant: one slice per case
+      if (kt0 + u < ktiles || decltype(steady_tag)::value) {
+        if (u == 0) slice(kt0 + 0, StageIdx<0 % kStages>{}, StageIdx<0>{}, steady_tag);
+        if (u == 1) slice(kt0 + 1, StageIdx<1 % kStages>{}, StageIdx<1>{}, steady_tag);
+        if constexpr (U > 2) {
+          if (u == 2) slice(kt0 + 2, StageIdx<2 % kStages>{}, StageIdx<0>{}, steady_tag);
+          if (u == 3) slice(kt0 + 3, StageIdx<3 % kStages>{}, StageIdx<1>{}, steady_tag);
+        }
+        if constexpr (U > 4) {
+          if (u == 4) slice(kt0 + 4, StageIdx<4 % kStages>{}, StageIdx<0>{}, steady_tag);
+          if (u == 5) slice(kt0 + 5, StageIdx<5 % kStages>{}, StageIdx<1>{}, steady_tag);
+        }
+      }
+    }
+  };
   int kt = 0;
-  for (; kt + 2 * kStages <= ktiles; kt += kStages) {  // every slice refills its stage
-    slice(kt, StageIdx<0>{}, StageIdx<1>{});
-    slice(kt + 1, StageIdx<1>{}, StageIdx<1>{});
-    if constexpr (kStages > 2) slice(kt + 2, StageIdx<2 % kStages>{}, StageIdx<1>{});
-    if constexpr (kStages > 3) slice(kt + 3, StageIdx<3 % kStages>{}, StageIdx<1>{});
-  }
-  for (; kt < ktiles; kt += kStages) {
-    slice(kt, StageIdx<0>{}, StageIdx<0>{});
-    if (kt + 1 < ktiles) slice(kt + 1, StageIdx<1>{}, StageIdx<0>{});
-    if constexpr (kStages > 2)
-      if (kt + 2 < ktiles) slice(kt + 2, StageIdx<2 % kStages>{}, StageIdx<0>{});
-    if constexpr (kStages > 3)
-      if (kt + 3 < ktiles) slice(kt + 3, StageIdx<3 % kStages>{}, StageIdx<0>{});
-  }
+  for (; kt + U + kStages <= ktiles; kt += U) unrolled(kt, StageIdx<1>{});  // every slice refills its stage
+  for (; kt < ktiles; kt += U) unrolled(kt, StageIdx<0>{});
 
+  // Epilogue: lane l holds C[m][n .. n+3] of block (ib, nb): m = row block + l % 16, n = column
+  // block + 4 (l / 16).
 #pragma unroll
-  for (int i = 0; i < MI; ++i) {
-    const int m = m0 + wm * (kTM / 2) + i * 32 + frag_row;
+  for (int i = 0; i < MB; ++i) {
+    const int m = m0 + wm * (kTM / 2) + i * 16 + l16;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int n = n0 + wn * 64 + j * 32 + 8 * q + 4 * frag_half;
+    for (int j = 0; j < 4; ++j) {
+      {
+        const int n = n0 + wn * 64 + j * 16 + 4 * lg;
         if (kRagged && (m >= M || n >= N)) continue;  // N % 8 == 0: n < N covers n .. n+3
-        float v0 = acc[i][j][4 * q], v1 = acc[i][j][4 * q + 1], v2 = acc[i][j][4 * q + 2], v3 = acc[i][j][4 * q + 3];
+        float v0 = acc[i][j][0], v1 = acc[i][j][1], v2 = acc[i][j][2], v3 = acc[i][j][3];
         if (k_chunk > 0) {
           *reinterpret_cast<f32x4*>(partial + (long long)m * N + n) = f32x4{v0, v1, v2, v3};
           continue;

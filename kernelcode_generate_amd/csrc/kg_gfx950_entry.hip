@@ -192,11 +192,14 @@ int read_float(const KgArgSlot* slots, int idx, const char* name, double* out) {
 // (cost queries model device buffers, which are always 256-byte aligned)
 bool aligned16(const void* p) { return g_cost != nullptr || ((uintptr_t)p & 15u) == 0; }
 
-int record_cost(long long mac, long long mfma, long long read, long long write) {
+// mfma_cycles: SIMD cycles one of the kernel's MFMA instructions occupies (32 for
+// 32x32x16, 16 for 16x16x32, 64 for the fp32 32x32x2).
+int record_cost(long long mac, long long mfma, long long mfma_cycles, long long read, long long write) {
   g_cost->v[KG_COST_MAC] = mac;
   g_cost->v[KG_COST_MFMA] = mfma;
   g_cost->v[KG_COST_HBM_READ] = read;
   g_cost->v[KG_COST_HBM_WRITE] = write;
+  g_cost->v[KG_COST_MFMA_CYCLES] = mfma * mfma_cycles;
   return kOk;
 }
 long long esize(int dtype) { return dtype == KG_DTYPE_F32 ? 4 : 2; }
@@ -475,20 +478,22 @@ int matmul_impl(const KgArgSlot* args, unsigned long long n) {
                            rhs.stride[0] <= kMaxPipeLd && aligned16(lhs.data) && aligned16(rhs.data) &&
                            aligned16(out.data) && (!bias.present || bias.stride[0] == 1) && gemm_f32_mfma_pays(M, N, K);
   if (g_cost) {
-    long long mfma = 0;
+    long long mfma = 0, cyc = 64;
     if (f32_mfma_ok)  // 4 waves x 2 x 2 blocks x 8 k-steps (32x32x2) per 16-deep slice of a 128 x 128 tile
       mfma = cdiv(M, gemmf::kTile) * cdiv(N, gemmf::kTile) * cdiv(K, gemmf::kBK) * 128;
     else if (out.dtype == KG_DTYPE_F32 && gemm_f32_splitk_ok(out, lhs, rhs, M, N, K) &&
              (!bias.present || bias.stride[0] == 1))  // 8 MFMAs (32x32x2) per 32 x 32 block and 16-deep slice
       mfma = (M / 32) * (N / 32) * (K / 16) * 8;
     if (mfma_ok && M > 0 && N > 0) {
-      // 8 waves x tm/16 MFMAs (32x32x16) per 32-deep slice of a tm x 256 tile; ragged edges
+      // 8 waves x tm/8 MFMAs (16x16x32) per 32-deep slice of a tm x 256 tile; ragged edges
       // are covered by whole tiles and slices
       const long long tm = pipe_tile_m(M, N);
-      mfma = cdiv(M, tm) * cdiv(N, gemmp::kBN) * cdiv(K, gemmp::kBK) * (tm / 2);
+      mfma = cdiv(M, tm) * cdiv(N, gemmp::kBN) * cdiv(K, gemmp::kBK) * tm;
+      cyc = 16;
     }
     const long long es = esize(out.dtype);
-    return record_cost(M * N * K, mfma, (M * K + K * N) * es + (bias.present ? N * esize(bias.dtype) : 0), M * N * es);
+    return record_cost(M * N * K, mfma, cyc, (M * K + K * N) * es + (bias.present ? N * esize(bias.dtype) : 0),
+                       M * N * es);
   }
   if (M == 0 || N == 0) return finish_launch("matmul(empty)");
 
@@ -593,7 +598,7 @@ int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
       mfma = tiles * cdiv(K, bk) * 4 * mi * 2 * per;
     }
     const long long es = esize(out.dtype);
-    return record_cost(out.numel() * w.shape[1] * w.shape[2] * w.shape[3], mfma,
+    return record_cost(out.numel() * w.shape[1] * w.shape[2] * w.shape[3], mfma, out.dtype == KG_DTYPE_F32 ? 64 : 32,
                        (x.numel() + w.numel()) * es + (bias.present ? bias.shape[0] * esize(bias.dtype) : 0),
                        out.numel() * es);
   }
@@ -762,7 +767,8 @@ int flash_attention_impl(const KgArgSlot* args, unsigned long long n) {
       mfma = B_H * waves_tiles * s.d;
     }
     const long long es = esize(out.dtype);
-    return record_cost(2 * B_H * pairs * D, mfma, (q.numel() + k.numel() + v.numel()) * es, out.numel() * es);
+    return record_cost(2 * B_H * pairs * D, mfma, out.dtype == KG_DTYPE_F32 ? 64 : 32,
+                       (q.numel() + k.numel() + v.numel()) * es, out.numel() * es);
   }
 
   if ((out.dtype == KG_DTYPE_BF16 || out.dtype == KG_DTYPE_F16) && fa_mfma_supported(s) && aligned16(q.data) &&
@@ -856,10 +862,12 @@ int kg_gfx950_cost(int op, const KgArgSlot* ordered_args, unsigned long long arg
 
 int kg_gfx950_abi_version(void) { return 1; }
 
-int kg_gfx950_mfma_rate(int dtype_code, int zero_operands, int iterations, int workgroups, double* tflops,
+int kg_gfx950_mfma_rate(int dtype_code, int mfma_m, int zero_operands, int iterations, int workgroups, double* tflops,
                         double* clock_ghz) {
   if (dtype_code != KG_DTYPE_BF16 && dtype_code != KG_DTYPE_F16)
     return fail(kInvalid, "mfma_rate: dtype must be bf16 or f16, got %s", dtype_name(dtype_code));
+  if (mfma_m != 32 && mfma_m != 16)
+    return fail(kInvalid, "mfma_rate: mfma_m must be 32 (32x32x16) or 16 (16x16x32), got %d", mfma_m);
   if (iterations < 1 || iterations > (1 << 20) || workgroups < 1 || workgroups > (1 << 16))
     return fail(kInvalid, "mfma_rate: iterations must be in [1, 2^20] and workgroups in [1, 65536]");
   if (tflops == nullptr || clock_ghz == nullptr) return fail(kInvalid, "mfma_rate: null output");
@@ -898,12 +906,11 @@ int kg_gfx950_mfma_rate(int dtype_code, int zero_operands, int iterations, int w
       check(hipMemcpy(d_ops, host.data(), host.size() * 2, hipMemcpyHostToDevice), "hipMemcpy") &&
       check(hipEventCreate(&e0), "hipEventCreate") && check(hipEventCreate(&e1), "hipEventCreate")) {
     auto launch = [&]() {
-      if (dtype_code == KG_DTYPE_BF16)
-        hipLaunchKernelGGL(mfma_rate_kernel<Bf16Tag>, dim3(workgroups), dim3(kMfmaRateThreads), 0, nullptr, d_ops, d_times,
-                           d_sink, iterations);
-      else
-        hipLaunchKernelGGL(mfma_rate_kernel<F16Tag>, dim3(workgroups), dim3(kMfmaRateThreads), 0, nullptr, d_ops, d_times,
-                           d_sink, iterations);
+      const bool bf = dtype_code == KG_DTYPE_BF16;
+      auto kernel = mfma_m == 32 ? (bf ? mfma_rate_kernel<Bf16Tag, 32> : mfma_rate_kernel<F16Tag, 32>)
+                                 : (bf ? mfma_rate_kernel<Bf16Tag, 16> : mfma_rate_kernel<F16Tag, 16>);
+      hipLaunchKernelGGL(kernel, dim3(workgroups), dim3(kMfmaRateThreads), 0, nullptr, d_ops, d_times, d_sink,
+                         iterations);
       return hipGetLastError();
     };
     float ms = 0.f;
@@ -918,7 +925,8 @@ int kg_gfx950_mfma_rate(int dtype_code, int zero_operands, int iterations, int w
           if (times[2 * b + 1] > 0) ghz.push_back((double)times[2 * b] / (double)times[2 * b + 1] * 0.1);
         std::sort(ghz.begin(), ghz.end());
         *clock_ghz = ghz.empty() ? 0.0 : ghz[ghz.size() / 2];
-        const double flop = (double)workgroups * (kMfmaRateThreads / 64) * iterations * 8 * 32768.0;
+        const double flop_per_mfma = mfma_m == 32 ? 32768.0 : 16384.0;
+        const double flop = (double)workgroups * (kMfmaRateThreads / 64) * iterations * 8 * flop_per_mfma;
         *tflops = ms > 0.f ? flop / (ms * 1e-3) / 1e12 : 0.0;
       }
     }

@@ -54,7 +54,7 @@ CONTROL_SYMBOLS = (
 
 # kg_gfx950_cost: op codes (KG_OP_*) and the order of its output array (KG_COST_*).
 COST_OPS = {"matmul": 1, "conv2d": 2, "flash_attention": 3}
-COST_KINDS = ("MAC", "MFMA", "HBM_READ", "HBM_WRITE")
+COST_KINDS = ("MAC", "MFMA", "HBM_READ", "HBM_WRITE", "MFMA_CYCLES")
 
 
 class KgArgSlot(ctypes.Structure):
@@ -120,7 +120,7 @@ def load_library() -> ctypes.CDLL:
     lib.kg_gfx950_cost.argtypes = [ctypes.c_int, ctypes.POINTER(KgArgSlot), ctypes.c_ulonglong,
                                    ctypes.POINTER(ctypes.c_longlong)]
     lib.kg_gfx950_cost.restype = ctypes.c_int
-    lib.kg_gfx950_mfma_rate.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+    lib.kg_gfx950_mfma_rate.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                         ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
     lib.kg_gfx950_mfma_rate.restype = ctypes.c_int
     _LIBRARY = lib
@@ -248,13 +248,14 @@ def set_launch_mode(synchronous: bool, stream: int | None = None) -> None:
 
 
 def mfma_rate(dtype: str = "bf16", zero_operands: bool = False, iterations: int = 20000,
-              workgroups: int = 2048) -> dict[str, float]:
-    """Sustained v_mfma_f32_32x32x16 rate with no operand movement (kg_gfx950_mfma_rate)."""
+              workgroups: int = 2048, mfma_m: int = 16) -> dict[str, float]:
+    """Sustained rate of v_mfma_f32_16x16x32 (mfma_m=16) or v_mfma_f32_32x32x16 (mfma_m=32)
+    with no operand movement (kg_gfx950_mfma_rate)."""
 
     code = {"bf16": DTYPE_CODES["bfloat16"], "f16": DTYPE_CODES["float16"]}[dtype]
     tf, ghz = ctypes.c_double(0.0), ctypes.c_double(0.0)
-    rc = load_library().kg_gfx950_mfma_rate(code, int(bool(zero_operands)), int(iterations), int(workgroups),
-                                            ctypes.byref(tf), ctypes.byref(ghz))
+    rc = load_library().kg_gfx950_mfma_rate(code, int(mfma_m), int(bool(zero_operands)), int(iterations),
+                                            int(workgroups), ctypes.byref(tf), ctypes.byref(ghz))
     if rc != 0:
         raise NativeLibraryError(f"kg_gfx950_mfma_rate failed: {last_error()}", rc)
     return {"tflops": tf.value, "clock_ghz": ghz.value}

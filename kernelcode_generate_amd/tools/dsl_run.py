@@ -40,21 +40,22 @@ from ..pipeline import PassManager, get_pipeline
 from ..pipeline.gfx950_lowering import LoweredKernel
 
 ARITY_ERROR = "DslRunArityMismatch: real_args count must match the kernel's positional parameters"
-VALID_DSL_COST_KINDS = ("MAC", "MFMA", "HBM_READ", "HBM_WRITE", "ROOFLINE_NS")
+VALID_DSL_COST_KINDS = ("MAC", "MFMA", "HBM_READ", "HBM_WRITE", "MFMA_CYCLES", "ROOFLINE_NS")
 DSL_COST_KIND_ERROR = ("DslCostRunInvalidCostKind: cost_kind must be one of [MAC, MFMA, HBM_READ, HBM_WRITE, "
-                       "ROOFLINE_NS]")
-# MI355X: 256 CUs x 4 SIMDs at 2.4 GHz; a 32x32x16 bf16/f16 MFMA occupies a SIMD 32 cycles,
-# a 32x32x2 fp32 MFMA 64; HBM3E moves 8 TB/s (8000 bytes per ns).
+                       "MFMA_CYCLES, ROOFLINE_NS]")
+# MI355X: 256 CUs x 4 SIMDs at 2.4 GHz (the library reports the SIMD cycles its MFMAs occupy:
+# 16 per 16x16x32 and 32 per 32x32x16 bf16/f16 MFMA, 64 per 32x32x2 fp32 MFMA); HBM3E moves
+# 8 TB/s (8000 bytes per ns).
 SIMDS, CLOCK_GHZ, HBM_BYTES_PER_NS = 1024, 2.4, 8000.0
-MFMA_CYCLES = {"f32": 64, "f16": 32, "bf16": 32}
 
 
-def roofline_ns(costs: dict, dtype: str) -> int:
+def roofline_ns(costs: dict) -> int:
     """The time below which no kernel can finish the call: the larger of its matrix-core
-    time (MFMA instructions x cycles each, spread over every SIMD at the peak clock) and its
-    compulsory HBM traffic at peak bandwidth, in ns (rounded up)."""
+    time (the chosen kernel's MFMA instructions x the cycles each occupies, spread over every
+    SIMD at the peak clock) and its compulsory HBM traffic at peak bandwidth, in ns (rounded
+    up)."""
 
-    mfma_ns = costs["MFMA"] * MFMA_CYCLES[dtype] / SIMDS / CLOCK_GHZ
+    mfma_ns = costs["MFMA_CYCLES"] / SIMDS / CLOCK_GHZ
     hbm_ns = (costs["HBM_READ"] + costs["HBM_WRITE"]) / HBM_BYTES_PER_NS
     return int(-(-max(mfma_ns, hbm_ns) // 1))
 DSL_COST_TARGET_ERROR = "DslCostRunInvalidTarget: dsl_cost_run only supports target 'gfx950'"
@@ -227,5 +228,5 @@ def dsl_cost_run(func_obj: Callable, real_args: tuple | list, pipeline: str | Pa
     except native.NativeLibraryError as exc:
         raise _error(f"{DSL_COST_OUTPUT_ERROR}: {exc}") from exc
     if cost_kind == "ROOFLINE_NS":
-        return roofline_ns(costs, lowered.func.param(lowered.fused.memory[0]).dtype)
+        return roofline_ns(costs)
     return costs[cost_kind]

@@ -80,7 +80,9 @@ def test_mfma_rate_rejects_bad_arguments():
 
     lib = native.load_library()
     tf, ghz = ctypes.c_double(0.0), ctypes.c_double(0.0)
-    assert lib.kg_gfx950_mfma_rate(1, 0, 10, 4, ctypes.byref(tf), ctypes.byref(ghz)) == -1  # fp32: not an MFMA 16-bit type
+    assert lib.kg_gfx950_mfma_rate(1, 16, 0, 10, 4, ctypes.byref(tf), ctypes.byref(ghz)) == -1  # fp32: not 16-bit
     assert "bf16 or f16" in native.last_error()
-    assert lib.kg_gfx950_mfma_rate(6, 0, 0, 4, ctypes.byref(tf), ctypes.byref(ghz)) == -1
-    assert lib.kg_gfx950_mfma_rate(6, 0, 10, 1 << 17, ctypes.byref(tf), ctypes.byref(ghz)) == -1
+    assert lib.kg_gfx950_mfma_rate(6, 8, 0, 10, 4, ctypes.byref(tf), ctypes.byref(ghz)) == -1
+    assert "mfma_m" in native.last_error()
+    assert lib.kg_gfx950_mfma_rate(6, 32, 0, 0, 4, ctypes.byref(tf), ctypes.byref(ghz)) == -1
+    assert lib.kg_gfx950_mfma_rate(6, 16, 0, 10, 1 << 17, ctypes.byref(tf), ctypes.byref(ghz)) == -1

@@ -5,9 +5,11 @@ result).
 
 MAC and byte counts are pinned by brute force (an oracle run gives the output shape; a
 mask count gives the causal pairs); MFMA counts are pinned by the MAC content of one
-32x32x16 MFMA (16384 MACs) on exact-tile shapes, and by the hardware counter
+MFMA (16x16x32: 8192 MACs in the pipelined GEMM; 32x32x16: 16384 in the conv and attention
+kernels; fp32 32x32x2: 2048) on exact-tile shapes, and by the hardware counter
 SQ_INSTS_MFMA on every kernel choice (profiles/mfma_instruction_counts.txt, made by
-tests/cost_cases.py under rocprofv3 --pmc).
+tests/cost_cases.py under rocprofv3 --pmc). MFMA_CYCLES is the MFMA count times 16, 32 or
+64 by the same shapes.
 """
 
 from __future__ import annotations
@@ -37,7 +39,8 @@ from tests.cost_cases import CASES, modelled
 
 T = native.TensorSpec
 PIPE = "gfx950-lowering"
-MFMA_MACS = 32 * 32 * 16
+MFMA_MACS = 32 * 32 * 16  # conv and attention kernels
+GEMM_MFMA_MACS = 16 * 16 * 32  # pipelined 16-bit GEMM
 PROFILE = Path(__file__).resolve().parents[1] / "profiles" / "mfma_instruction_counts.txt"
 
 
@@ -111,9 +114,11 @@ def test_matmul_counts(dtype, mnk):
     elif k % 8 or n % 8:
         assert c["MFMA"] == 0  # SIMT path
     elif m % 256 == 0 and n % 256 == 0 and k % 64 == 0:
-        assert c["MFMA"] * MFMA_MACS == c["MAC"]  # exact tiles: no wasted MFMA work
+        assert c["MFMA"] * GEMM_MFMA_MACS == c["MAC"]  # exact tiles: no wasted MFMA work
     else:
-        assert c["MFMA"] * MFMA_MACS >= c["MAC"]
+        assert c["MFMA"] * GEMM_MFMA_MACS >= c["MAC"]
+    # 1024 16-bit or 64 fp32 FLOP per SIMD cycle, whichever MFMA shape the kernel uses
+    assert c["MFMA_CYCLES"] == c["MFMA"] * (64 if dtype == "float32" else 16)
 
 
 def test_matmul_static_demo_uses_baked_tiles():
@@ -160,6 +165,7 @@ def test_conv_mfma_path():
     assert c["MAC"] == 32 * 64 * 56 * 56 * 64 * 9
     # 56 columns fill 64 MFMA columns (two 32-wide waves): MFMA work is MAC * 64/56
     assert c["MFMA"] * MFMA_MACS * 56 == c["MAC"] * 64
+    assert c["MFMA_CYCLES"] == 32 * c["MFMA"]
 
 
 @pytest.mark.parametrize("causal", [False, True])
@@ -177,7 +183,7 @@ def test_attention_macs_count_mask(shape, causal):
 def test_attention_mfma_exact_tiles():
     shape = (4, 32, 2048, 128)
     c = costs(flash_attention_scaled_kernel, (T(shape, "bfloat16"),) * 4 + (128, 64, 0.088))
-    assert c["MFMA"] * MFMA_MACS == c["MAC"]
+    assert c["MFMA"] * MFMA_MACS == c["MAC"] and c["MFMA_CYCLES"] == 32 * c["MFMA"]
     static = costs(flash_attention_inputs_static_tile_static_kernel, (T(shape, "bfloat16"),) * 4)
     assert static["MAC"] == c["MAC"] and static["MFMA"] == c["MFMA"]
 
@@ -210,12 +216,13 @@ def test_mfma_model_matches_hardware_counter():
 
 
 def test_roofline_kind():
-    """ROOFLINE_NS: the larger of the MFMA time at the 2.4 GHz peak (32 cycles per 16-bit
-    32x32x16 MFMA, 64 per fp32 32x32x2, over 1024 SIMDs) and the compulsory bytes at 8 TB/s."""
+    """ROOFLINE_NS: the larger of the MFMA time at the 2.4 GHz peak (16 cycles per 16-bit
+    16x16x32 MFMA, 32 per 32x32x16, 64 per fp32 32x32x2, over 1024 SIMDs) and the compulsory
+    bytes at 8 TB/s."""
 
     b16 = T((4096, 4096), "bfloat16")
     c2 = dsl_cost_run(matmul_inputs_dynamic_tile_dynamic_kernel, (b16, b16, b16, None, 64, 64, 64), PIPE, "ROOFLINE_NS")
-    assert c2 == -(-4194304 * 32 // (1024 * 2.4)) == 54614  # 2 x 4096^3 FLOP at 2516.6 TFLOP/s
+    assert c2 == -(-8388608 * 16 // (1024 * 2.4)) == 54614  # 2 x 4096^3 FLOP at 2516.6 TFLOP/s
     x = T((32, 64, 56, 56), "float16")
     w = T((64, 64, 3, 3), "float16")
     conv = dsl_cost_run(conv2d_inputs_dynamic_tile_dynamic_kernel, (x, x, w, None) + (1,) * 8 + (8, 8, 8, 8, 8), PIPE,

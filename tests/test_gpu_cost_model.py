@@ -2,8 +2,9 @@
 kernel_gen/tools/dsl_run.py:656-730): every case of tests/cost_cases.py (each kernel choice
 of the library) is run and timed with HIP events, and
 
-  - the modelled MFMA instructions carry at least the operation's FLOP (2 per MAC; 32768
-    per 32x32x16 16-bit MFMA, 4096 per 32x32x2 fp32 MFMA), exactly on exact-tile shapes;
+  - the modelled MFMA cycles carry at least the operation's FLOP (2 per MAC; a SIMD does
+    1024 16-bit MFMA FLOP per cycle in either shape, 32x32x16 or 16x16x32, and 64 fp32 FLOP
+    per cycle of 32x32x2), exactly on exact-tile shapes;
   - no case runs faster than its ROOFLINE_NS (matrix-core time of the modelled MFMAs at the
     2.4 GHz peak clock, or compulsory HBM bytes at 8 TB/s), less 10 % for timer resolution;
   - cases whose roofline is at least 20 us run within 4x of it (the stated band: these
@@ -20,10 +21,9 @@ from kernelcode_generate_amd.tools import roofline_ns
 from tests.cost_cases import CASES, modelled, prepare
 
 pytestmark = pytest.mark.gpu
-FLOP_PER_MFMA = {"float32": 4096, "bfloat16": 32768, "float16": 32768}
+FLOP_PER_MFMA_CYCLE = {"float32": 64, "bfloat16": 1024, "float16": 1024}
 EXACT = {"gemm_bf16_4096", "gemm_bf16_c2s_8192x1024x4096", "gemm_f16_512x768x256", "gemm_f32_256",
          "gemm_f32_splitk_512x512x4096", "gemm_f32_mfma_1024x256x1024", "fa_bf16_c4"}
-SHORT = {"float32": "f32", "bfloat16": "bf16", "float16": "f16"}
 
 
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
@@ -33,10 +33,10 @@ def test_cost_model_against_the_gpu(device, case):
     name, family, dtype = case[0], case[1], case[2]
     model = modelled(case)
     if model["MFMA"]:
-        assert model["MFMA"] * FLOP_PER_MFMA[dtype] >= 2 * model["MAC"], name
+        assert model["MFMA_CYCLES"] * FLOP_PER_MFMA_CYCLE[dtype] >= 2 * model["MAC"], name
         if name in EXACT:
-            assert model["MFMA"] * FLOP_PER_MFMA[dtype] == 2 * model["MAC"], name
-    roof = roofline_ns(model, SHORT[dtype])
+            assert model["MFMA_CYCLES"] * FLOP_PER_MFMA_CYCLE[dtype] == 2 * model["MAC"], name
+    roof = roofline_ns(model)
     print(f"[cost] {name}: roofline {roof} ns", flush=True)
     entry, args = prepare(case)
     native.call_entry(entry, args)  # warm
@@ -67,9 +67,11 @@ def test_cost_model_against_the_gpu(device, case):
 @pytest.mark.gpu
 def test_mfma_rate_measures_the_matrix_cores(device):
     """kg_gfx950_mfma_rate: a short run gives a rate below the nominal dense peak and above a
-    tenth of it, for both operand kinds, and a clock within the part's range."""
-    for zeros in (False, True):
-        r = native.mfma_rate("bf16", zeros, iterations=2000, workgroups=1024)
-        print(f"[mfma_rate] zeros={zeros}: {r['tflops']:.0f} TFLOP/s at {r['clock_ghz']:.2f} GHz", flush=True)
-        assert 0.1 * 2516.6 < r["tflops"] < 2516.6
-        assert 0.5 < r["clock_ghz"] < 2.6
+    tenth of it, for both MFMA shapes and both operand kinds, and a clock within the part's range."""
+    for mfma_m in (16, 32):
+        for zeros in (False, True):
+            r = native.mfma_rate("bf16", zeros, iterations=2000, workgroups=1024, mfma_m=mfma_m)
+            print(f"[mfma_rate] m={mfma_m} zeros={zeros}: {r['tflops']:.0f} TFLOP/s at {r['clock_ghz']:.2f} GHz",
+                  flush=True)
+            assert 0.1 * 2516.6 < r["tflops"] < 2516.6
+            assert 0.5 < r["clock_ghz"] < 2.6
