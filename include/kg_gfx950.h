@@ -139,7 +139,9 @@ int kg_gfx950_finish_launch(const char* what);
 /* Text of the last failure on the calling thread ("" if none). */
 const char* kg_gfx950_last_error(void);
 
-/* ABI revision of this library (bumped on any slot-contract change). */
+/* ABI revision of this library (bumped on any change of a declaration here or of the slot
+ * contract). 2: kg_gfx950_cost writes five kinds (KG_COST_MFMA_CYCLES added);
+ * kg_gfx950_mfma_rate takes the MFMA shape. */
 int kg_gfx950_abi_version(void);
 
 /*

@@ -8,17 +8,22 @@
 // ids are dealt to the 8 XCDs round-robin; they are remapped so that each XCD runs the query
 // blocks of the same (b,h) together and its L2 serves their K/V.
 //
-// Per wave and key tile the kernel computes S^T = K Q^T with v_mfma_f32_32x32x16 (operand A
-// = 32 keys x 16 d from LDS, operand B = Q^T kept in registers for the whole kernel). In
-// the 32x32 MFMA result lane l holds column l%32 (one query) and rows {8j + 4(l/32) + r};
-// the K rows are read in the permuted order pi(8j + 4h + r) = 16h + 4j + r, so lane l ends
-// up with the scores of ITS query against 16 CONSECUTIVE keys (16h .. 16h+15 of the
-// 32-key block). Row max/sum are lane-local plus one exchange with lane l^32
-// (v_permlane32_swap), and P (rounded to 16 bits) is already laid out as the B operand of
-// O^T += V^T P^T: lane half h supplies keys 16h+8t .. 16h+8t+7 of MFMA t. The V^T operand
-// (8 consecutive keys of one d per lane) comes from the key-major V tile through two
-// ds_read_b64_tr_b16: within each 16-lane group, lane j addresses 4 consecutive d of key
-// row j/4 and lane i receives key rows 0..3 of column i.
+// Matrix cores: v_mfma_f32_16x16x32 (16x16 blocks, 32-deep contraction; the same FLOP per
+// cycle as 32x32x16, and under the part's power limit it holds a higher clock). A wave's 32
+// queries are two query blocks qb (16 each), a key tile four key blocks kb (16 keys).
+//   S^T = K Q^T: operand A = 16 keys x 32 d of K from LDS (lane l: key l%16, d 8(l/16)..+7),
+//     operand B = Q^T kept in registers for the whole kernel (lane l: query l%16 of qb, the
+//     same d). Each K fragment feeds the MFMAs of both query blocks. Lane l ends up with
+//     S[query l%16 of qb][keys 16kb + 4(l/16) + 0..3] for every (qb, kb): 16 scores of each
+//     of its two queries, so row max and sum combine the four lanes l%16 + 16r (three
+//     v_permlane{16,32}_swap for both queries together).
+//   O^T += V^T P^T over 32-key chunks c: the contraction index k = 8r + j of lane row r stands
+//     for key 32c + 4r + j (j < 4) and 32c + 16 + 4r + j - 4 (j >= 4), exactly the keys whose
+//     scores lane row r holds, so P (rounded to 16 bits) feeds operand B from its own
+//     registers; operand A (lane l: d 16db + l%16, those 8 keys) is two ds_read_b64_tr_b16
+//     from the key-major V tile: within each 16-lane group, lane j addresses 4 consecutive d
+//     of key row j/4 and lane i receives key rows 0..3 of column i. Each V fragment feeds
+//     both query blocks.
 //
 // Softmax works in base 2: p = exp2(s * scale*log2(e) - m) with m tracked in the same
 // units (v_exp_f32). The running max is raised only when a tile's max exceeds it by more
@@ -62,36 +67,36 @@ struct Cfg {
 // Running-max slack (log2 units): P <= 2^8 between rescales.
 constexpr float kRescaleSlack = 8.0f;
 
-// Row of the K tile that MFMA row r reads (see header comment).
-__host__ __device__ constexpr int key_perm(int r) { return 16 * ((r >> 2) & 1) + 4 * (r >> 3) + (r & 3); }
-// The 16 lanes of one b128 read cycle read keys pi(0..15) = {0-3, 16-19, 4-7, 20-23} (+8)
-// at the same chunk; D=128 rows are 256 bytes (one bank row), D=64 rows 128 bytes.
+// K fragment reads: the 16 lanes of a b128 read cycle read key rows 16kb + 0..15 at the same
+// chunk. D=128 rows are 256 bytes (one bank row): slot c ^ (r & 15) puts them in 16 distinct
+// chunks. D=64 rows are 128 bytes (two per bank row): rows of one parity need distinct
+// chunks, c ^ ((r >> 1) & 7).
 template <int D>
 __host__ __device__ constexpr int k_mask(int key) {
-  return D == 128 ? ((key & 7) | ((key >> 1) & 8)) : (((key >> 1) & 3) | ((key >> 2) & 4));
+  return D == 128 ? (key & 15) : ((key >> 1) & 7);
 }
-// Transposed reads: the 32 lanes of a cycle read 4 key rows x two 32-byte pieces.
+// V^T reads: the 32 lanes of a 64-bit read cycle read key rows 8i + 0..7, 32 contiguous bytes
+// (chunks 2db, 2db+1) each. D=128: slot c ^ 2(r & 7) gives the 8 rows 8 distinct chunk
+// pairs; D=64: rows of one parity (4 of them) distinct pairs, c ^ 2((r >> 1) & 3).
 template <int D>
 __host__ __device__ constexpr int v_mask(int key) {
-  return D == 128 ? 4 * (key & 3) : 4 * ((key >> 1) & 1);
+  return D == 128 ? 2 * (key & 7) : 2 * ((key >> 1) & 3);
 }
 
-// Copy instruction p of wave w covers tile rows (w*PW + p)*RPP + lane/DCH. K keeps a
-// per-lane HBM offset for every p; V keeps the one of p = 0 and moves the wave-uniform base
-// by whole KiB, which needs the V masks of the rows to repeat (the tail tile uses the same
-// offsets).
+// The copy rows of one lane (kWaves * RPP apart, RPP = 1024 / (2D) rows per KiB) share
+// their K and V masks.
 template <int D, int W>
-constexpr bool v_copy_masks_repeat() {
-  constexpr int RB = 2 * D, PW = kBC * RB / 1024 / W, RPP = 1024 / RB, DCH = D / 8;
+constexpr bool copy_masks_repeat() {
+  constexpr int RPP = 1024 / (2 * D), PW = 64 * 2 * D / 1024 / W;
   for (int w = 0; w < W; ++w)
     for (int lane = 0; lane < 64; ++lane)
       for (int p = 0; p < PW; ++p) {
-        const int row = (w * PW + p) * RPP + lane / DCH;
-        if (v_mask<D>(row) != v_mask<D>((w * PW) * RPP + lane / DCH)) return false;
+        const int r0 = w * RPP + lane / (D / 8), r = r0 + W * p * RPP;
+        if (k_mask<D>(r) != k_mask<D>(r0) || v_mask<D>(r) != v_mask<D>(r0)) return false;
       }
   return true;
 }
-static_assert(v_copy_masks_repeat<128, 8>() && v_copy_masks_repeat<128, 4>() && v_copy_masks_repeat<64, 4>(),
+static_assert(copy_masks_repeat<128, 8>() && copy_masks_repeat<128, 4>() && copy_masks_repeat<64, 4>(),
               "copy offsets");
 
 // Bijection of workgroup ids: XCD x (ids with id % 8 == x) gets one contiguous range.
@@ -104,6 +109,29 @@ __device__ __forceinline__ int xcd_block(int pid, int total) {
 
 __device__ __forceinline__ float max3f(float a, float b, float c) {
   return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
+}
+
+// a and b combined over the four 16-lane rows (lanes with the same lane % 16), both results
+// in every lane. v_permlane16_swap(x, y) swaps the odd rows of x with the even rows of y:
+// it returns [x0 y0 x2 y2] and [x1 y1 x3 y3]; v_permlane32_swap(x, y) swaps the high half of
+// x with the low half of y: with x = y it returns [x0 x1 x0 x1] and [x2 x3 x2 x3].
+template <bool kMax>
+__device__ __forceinline__ void rows4_combine(float& a, float& b) {
+  auto op = [](float x, float y) { return kMax ? __builtin_elementwise_maximum(x, y) : x + y; };
+  auto f = [](uint32_t u) { return __builtin_bit_cast(float, u); };
+  const auto r1 = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                                                   false, false);
+  const uint32_t r10 = r1[0], r11 = r1[1];
+  const float m = op(f(r10), f(r11));  // rows: a01 b01 a23 b23
+  const uint32_t um = __builtin_bit_cast(uint32_t, m);
+  const auto r2 = __builtin_amdgcn_permlane32_swap(um, um, false, false);
+  const uint32_t r20 = r2[0], r21 = r2[1];
+  const float t = op(f(r20), f(r21));  // rows: A B A B
+  const uint32_t ut = __builtin_bit_cast(uint32_t, t);
+  const auto r3 = __builtin_amdgcn_permlane16_swap(ut, ut, false, false);
+  const uint32_t r30 = r3[0], r31 = r3[1];
+  a = f(r30);
+  b = f(r31);
 }
 
 }  // namespace fa
@@ -121,21 +149,24 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
   constexpr int RB = 2 * D;          // bytes per K/V row
   constexpr int TB = kBC * RB;       // bytes per K or V tile
   constexpr int DCH = D / 8;         // 16-byte chunks per row
-  constexpr int NKK = D / 16;        // S^T MFMAs per 32-key block
-  constexpr int NDB = D / 32;        // 32-row d blocks of O^T
-  constexpr int NS = 2 * NKK;        // S^T MFMAs per tile
-  constexpr int NP = 4 * NDB;        // PV MFMAs per tile
+  constexpr int NDS = D / 32;        // 32-deep d steps of S^T
+  constexpr int NKF = 4 * NDS;       // K fragments per tile: 4 key blocks x NDS
+  constexpr int NS = 2 * NKF;        // S^T MFMAs per tile (both query blocks per fragment)
+  constexpr int NDB = D / 16;        // 16-row d blocks of O^T
+  constexpr int NVF = 2 * NDB;       // V^T fragments per tile: 2 key chunks x NDB
+  constexpr int NP = 2 * NVF;        // PV MFMAs per tile
   constexpr int PW = TB / 1024 / kWaves;  // copy instructions per wave, tile and operand
   static_assert(PW >= 1 && 2 * PW <= NS, "copy slots");
   constexpr int RPP = 1024 / RB;     // rows per copy instruction
+  constexpr int kKAhead = 3;         // K fragments read ahead of their MFMAs
 
   __shared__ __attribute__((aligned(1024))) u32x4 lds[4 * TB / 16];  // K0 K1 V0 V1
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int half = lane >> 5;
-  const int ql = lane & 31;
+  const int l16 = lane & 15;
+  const int lr = lane >> 4;  // lane row (16 lanes)
 
   const int nmb = (s_q + kBM - 1) / kBM;
   const int lin = xcd_block(blockIdx.x, nmb * bh_count);
@@ -149,43 +180,44 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
   const char* Vb = reinterpret_cast<const char*>(V + kv_base);
   uint16_t* Oh = O + (long long)bh * s_q * D;
 
-  const int q_row = m0 + 32 * wave + ql;
-  u32x4 qf[NKK];
+  const int wave_q_lo = m0 + 32 * wave;
+  const int q_row0 = wave_q_lo + l16;  // query of block qb: q_row0 + 16 qb
+  u32x4 qf[2][NDS];
 #pragma unroll
-  for (int kk = 0; kk < NKK; ++kk)
-    qf[kk] = (!kMasked || q_row < s_q) ? ld16(Qh + (long long)q_row * D + 16 * kk + 8 * half) : u32x4{0, 0, 0, 0};
+  for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+    for (int s = 0; s < NDS; ++s) {
+      const int q = q_row0 + 16 * qb;
+      qf[qb][s] = (!kMasked || q < s_q) ? ld16(Qh + (long long)q * D + 32 * s + 8 * lr) : u32x4{0, 0, 0, 0};
+    }
 
   const int n_end = kCausal ? min(s_kv, m0 + kBM) : s_kv;
   const int ntiles = (n_end + kBC - 1) / kBC;
-  const int wave_q_lo = m0 + 32 * wave;
 
   // ---- HBM -> LDS copies: K tile t into K buffer b (LDS bytes b*TB), V into 2*TB + b*TB ----
+  // Copy instruction p of wave w covers the KiB (w + kWaves*p) of the tile: rows
+  // (w + kWaves*p)*RPP + lane/DCH, LDS slot lane%DCH. The rows of one lane's copies lie
+  // kWaves*RPP (at least 32) rows apart, so they share their K and V masks: one per-lane
+  // offset each, and p moves the wave-uniform source base by whole KiB.
   const uint32_t lds0 = lds_addr(&lds[0]);
-  const int c_row0 = wave * PW * RPP + lane / DCH;
+  const int c_row0 = wave * RPP + lane / DCH;
   const int c_slot = lane % DCH;
-  uint32_t k_goff[PW];
-#pragma unroll
-  for (int p = 0; p < PW; ++p) {
-    const int row = c_row0 + p * RPP;
-    k_goff[p] = (uint32_t)(row * RB + 16 * (c_slot ^ k_mask<D>(row)));
-  }
+  const uint32_t k_goff = (uint32_t)(c_row0 * RB + 16 * (c_slot ^ k_mask<D>(c_row0)));
   const uint32_t v_goff = (uint32_t)(c_row0 * RB + 16 * (c_slot ^ v_mask<D>(c_row0)));
 
   // Copy instruction p (< PW) of tile t of K (kV false) or V into the LDS buffer at lds_buf.
   auto copy_piece = [&](const char* src, int t, uint32_t lds_buf, bool kV, int p) {
     const int n0 = t * kBC;
-    const uint32_t m = lds_buf + (wave * PW + p) * 1024;
+    const uint32_t m = lds_buf + (wave + kWaves * p) * 1024;
+    const char* base = src + (long long)n0 * RB + kWaves * p * 1024;
     if constexpr (kMasked) {
       // ragged S: every tile through a raw buffer resource that ends at row s_kv, so the rows
       // of the tail tile past s_kv land zeros (their scores are masked in S: P is 0 there)
-      const char* base = src + (long long)n0 * RB + (kV ? p * 1024 : 0);
-      const long long left = (long long)(s_kv - n0) * RB - (kV ? p * 1024 : 0);
+      const long long left = (long long)(s_kv - n0) * RB - kWaves * p * 1024;
       const uint32_t range = (uint32_t)max(0ll, min(left, (long long)TB));
-      buf2lds16_r(kV ? v_goff : k_goff[p], base, range, m);
+      buf2lds16_r(kV ? v_goff : k_goff, base, range, m);
     } else {
-      const char* base = src + (long long)n0 * RB;
-      if (kV) g2lds16_s(v_goff, base + p * 1024, m);
-      else g2lds16_s(k_goff[p], base, m);
+      g2lds16_s(kV ? v_goff : k_goff, base, m);
     }
   };
   auto copy_k = [&](int t, int buf) {
@@ -198,145 +230,178 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
   };
 
   // ---- fragment reads ----
-  // K: MFMA step i (block kb = i&1, d step kk = i>>1) reads key key_perm(ql) + 32kb, chunk
-  // 2kk + half; k_mask(key + 32) == k_mask(key), so kb is an immediate offset.
-  uint32_t k_rd[NKK];
+  // K fragment f = kb*NDS + s: key row 16kb + l16, chunk 4s + lr; k_mask(16kb + l16) ==
+  // k_mask(l16), so kb is an immediate offset.
+  uint32_t k_rd[NDS];
   {
-    const int key = key_perm(ql);
-    const int km = k_mask<D>(key);
+    const int km = k_mask<D>(l16);
 #pragma unroll
-    for (int kk = 0; kk < NKK; ++kk) k_rd[kk] = lds0 + key * RB + 16 * ((2 * kk + half) ^ km);
+    for (int s = 0; s < NDS; ++s) k_rd[s] = lds0 + l16 * RB + 16 * ((4 * s + lr) ^ km);
   }
-  // V^T: PV MFMA i = (2kb + t)*NDB + db; lane group g = lane/16 reads key rows
-  // 32kb + 16*half + 8t + {0..3} (then +4) and d columns 32db + 16(g&1) .. +15. v_mask of
-  // those rows equals that of row 16*half + (j>>2), so kb and t are immediate offsets.
+  // V^T fragment f = c*NDB + db: lane row lr reads key rows 32c + 4lr + {0..3} (then +16) and
+  // d columns 16db .. 16db+15, lane j of the row addressing row j/4 and d 4(j%4) .. +3.
+  // v_mask of those rows equals that of row 4lr + j/4, so c and the +16 are immediate offsets.
   uint32_t v_rd[NDB];
   {
-    const int g = lane >> 4, jj = lane & 15;
-    const int row = 16 * half + (jj >> 2);
+    const int row = 4 * lr + (l16 >> 2);
     const int vm = v_mask<D>(row);
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
-      const int c16 = 4 * db + 2 * (g & 1) + ((jj & 3) >> 1);
-      v_rd[db] = lds0 + 2 * TB + row * RB + 16 * (c16 ^ vm) + 8 * (jj & 1);
+      const int c16 = 2 * db + ((l16 & 3) >> 1);
+      v_rd[db] = lds0 + 2 * TB + row * RB + 16 * (c16 ^ vm) + 8 * (l16 & 1);
     }
   }
-  auto read_k = [&](int buf, int i) -> u32x4 {
-    return *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(k_rd[i >> 1] + buf * TB + (i & 1) * 32 * RB);
+  auto read_k = [&](int buf, int f) -> u32x4 {
+    const int kb = f / NDS, s = f % NDS;
+    return *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(k_rd[s] + buf * TB + kb * 16 * RB);
   };
-  auto read_v = [&](int buf, int i) -> u32x4 {
-    const int grp = i / NDB, db = i % NDB;
-    const uint32_t a = v_rd[db] + buf * TB + (32 * (grp >> 1) + 8 * (grp & 1)) * RB;
+  auto read_v = [&](int buf, int f) -> u32x4 {
+    const int c = f / NDB, db = f % NDB;
+    const uint32_t a = v_rd[db] + buf * TB + 32 * c * RB;
     const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(uintptr_t)a);
     const s16x4 hi =
-        __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(uintptr_t)(a + 4 * RB));
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(uintptr_t)(a + 16 * RB));
     const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
     return u32x4{l2[0], l2[1], h2[0], h2[1]};
   };
 
-  // ---- softmax state ----
-  f32x16 o[NDB];
+  // ---- softmax state (per query block) ----
+  f32x4 o[NDB][2];
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
-  float m_run = -INFINITY;  // max used by exp2 (log2 units)
-  float l_run = 0.f;        // this lane's share of the row sum
-  float m_cur = -INFINITY;  // max of the S tile about to be exponentiated (log2 units)
-  u32x4 pp[4];              // P of group 2kb + t (keys 32kb + 16*half + 8t + 0..7)
-  const f32x16 zero16 = {};
+    for (int qb = 0; qb < 2; ++qb) o[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run[2] = {-INFINITY, -INFINITY};  // max used by exp2 (log2 units)
+  float l_run[2] = {0.f, 0.f};              // this lane's share of the row sums
+  float m_cur[2] = {-INFINITY, -INFINITY};  // max of the S tile about to be exponentiated
+  u32x4 pp[2][2];                           // P of chunk c, query block qb (keys as above)
+  const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+  using Scores = f32x4[2][4];               // [qb][kb], lane holds keys 16kb + 4lr + 0..3
 
   auto need_mask = [&](int t) {
     const int n0 = t * kBC;
     return (kMasked && n0 + kBC > s_kv) || (kCausal && n0 + kBC - 1 > wave_q_lo);
   };
-  // Ragged S: keys past key_lim_h + 16*half are dead, past s_kv or (causal) past the query;
-  // one limit per lane keeps the masked variants within their registers. Unmasked causal
-  // kernels compare each key with the query row.
-  const int key_lim_h = (kCausal ? min(q_row, s_kv - 1) : s_kv - 1) - 16 * half;
-  auto apply_mask = [&](f32x16(&s)[2], int t) {
-    if constexpr (kMasked) {
-      const int rel = key_lim_h - t * kBC;  // element i of block kb is dead if 32kb + i > rel
+  // Ragged S: a score of query block qb and tile-relative key 16kb + 4lr + i is dead if
+  // 16kb + i > key_lim[qb] - t*kBC (keys past s_kv or, causal, past the query). Unmasked
+  // causal kernels compare each key with the query row.
+  auto apply_mask = [&](Scores& s, int t) {
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+    for (int qb = 0; qb < 2; ++qb) {
+      const int q = q_row0 + 16 * qb;
+      if constexpr (kMasked) {
+        const int rel = (kCausal ? min(q, s_kv - 1) : s_kv - 1) - 4 * lr - t * kBC;
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-          if (32 * kb + i > rel) s[kb][i] = -INFINITY;
-    } else {
-      const int key0 = t * kBC + 16 * half;
+        for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+          for (int i = 0; i < 4; ++i)
+            if (16 * kb + i > rel) s[qb][kb][i] = -INFINITY;
+      } else {
+        const int key0 = t * kBC + 4 * lr;
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-          if (kCausal && key0 + 32 * kb + i > q_row) s[kb][i] = -INFINITY;
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (kCausal && key0 + 16 * kb + i > q) s[qb][kb][i] = -INFINITY;
+      }
     }
   };
-  // max op k (0..15) over the 32 scores of a lane: v_maximum3_f32 chains
-  auto max_op = [&](const f32x16(&s)[2], int k, float& mx) {
-    auto e = [&](int x) { return s[x >> 4][x & 15]; };
+  // max op k (0..7) over the 16 scores of query block qb: v_maximum3_f32 chains
+  auto max_op = [&](const Scores& s, int qb, int k, float& mx) {
+    auto e = [&](int x) { return s[qb][x >> 2][x & 3]; };
     if (k == 0) mx = max3f(e(0), e(1), e(2));
-    else if (k < 15) mx = max3f(mx, e(1 + 2 * k), e(2 + 2 * k));
-    else mx = __builtin_elementwise_maximum(mx, e(31));
+    else if (k < 7) mx = max3f(mx, e(1 + 2 * k), e(2 + 2 * k));
+    else mx = __builtin_elementwise_maximum(mx, e(15));
   };
-  auto rescale = [&]() {
-    const bool raise = m_cur > m_run + kRescaleSlack;
-    if (__builtin_amdgcn_ballot_w64(raise)) {
-      const float alpha = raise ? __builtin_amdgcn_exp2f(m_run - m_cur) : 1.f;  // 0 on the first tile
-      m_run = raise ? m_cur : m_run;
-      l_run *= alpha;
+  auto tile_max = [&](float (&mx)[2]) {
+    rows4_combine<true>(mx[0], mx[1]);
+    m_cur[0] = mx[0] * scale_log2;
+    m_cur[1] = mx[1] * scale_log2;
+  };
+  // kAlways: scale without the wave-uniform branch (alpha 1 where nothing is raised)
+  auto rescale = [&](auto always_tag) {
+    constexpr bool kAlways = decltype(always_tag)::value != 0;
+    const bool raise0 = m_cur[0] > m_run[0] + kRescaleSlack;
+    const bool raise1 = m_cur[1] > m_run[1] + kRescaleSlack;
+    if (kAlways || __builtin_amdgcn_ballot_w64(raise0 || raise1)) {
+      // alpha is 0 on the first tile (m_run = -inf)
+      const float a0 = raise0 ? __builtin_amdgcn_exp2f(m_run[0] - m_cur[0]) : 1.f;
+      const float a1 = raise1 ? __builtin_amdgcn_exp2f(m_run[1] - m_cur[1]) : 1.f;
+      m_run[0] = raise0 ? m_cur[0] : m_run[0];
+      m_run[1] = raise1 ? m_cur[1] : m_run[1];
+      l_run[0] *= a0;
+      l_run[1] *= a1;
 #pragma unroll
-      for (int db = 0; db < NDB; ++db)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+      for (int db = 0; db < NDB; ++db) {
+        o[db][0] *= a0;
+        o[db][1] *= a1;
+      }
     }
   };
-  auto sm_elem = [&](f32x16(&s)[2], int e) {
-    s[e >> 4][e & 15] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e >> 4][e & 15], scale_log2, -m_run));
+  // softmax element e (0..31): pack group G = e/8 = 2c + qb, in the order the PV MFMAs use
+  // them (chunk 0 of both query blocks first); within a group, kb = 2c + (e/4)%2, i = e%4
+  auto sm_elem = [&](Scores& s, int e) {
+    const int G = e >> 3, c = G >> 1, qb = G & 1, kb = 2 * c + ((e >> 2) & 1), i = e & 3;
+    s[qb][kb][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][kb][i], scale_log2, -m_run[qb]));
   };
-  auto sm_pack = [&](const f32x16(&s)[2], int g) {
-    const int kb = g >> 1, t = g & 1;
+  auto sm_pack = [&](const Scores& s, int G) {
+    const int c = G >> 1, qb = G & 1;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      pp[g][q] = H::pack2(s[kb][8 * t + 2 * q], s[kb][8 * t + 2 * q + 1]);
-      l_run = H::sum2(pp[g][q], l_run);
-    }
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        pp[c][qb][2 * h + q] = H::pack2(s[qb][2 * c + h][2 * q], s[qb][2 * c + h][2 * q + 1]);
+        l_run[qb] = H::sum2(pp[c][qb][2 * h + q], l_run[qb]);
+      }
   };
+  // PV MFMA i: V fragment i/2 (chunk c, d block db), query block i%2
   auto pv = [&](int i, u32x4 vf) {
-    const int db = i % NDB;
-    o[db] = H::mfma32(vf, pp[i / NDB], o[db]);
+    const int f = i >> 1, qb = i & 1;
+    const int c = f / NDB, db = f % NDB;
+    o[db][qb] = H::mfma16(vf, pp[c][qb], o[db][qb]);
   };
-  auto s_mfma = [&](f32x16(&s)[2], int i, u32x4 kf) {
-    s[i & 1] = H::mfma32(kf, qf[i >> 1], i < 2 ? zero16 : s[i & 1]);
+  // S MFMA i: K fragment i/2 (key block kb, d step s), query block i%2
+  auto s_mfma = [&](Scores& s, int i, u32x4 kf) {
+    const int f = i >> 1, qb = i & 1;
+    const int kb = f / NDS, st = f % NDS;
+    s[qb][kb] = H::mfma16(kf, qf[qb][st], st == 0 ? zero4 : s[qb][kb]);
   };
 
   // One key tile. par = j & 1 (K(j+1) sits in K buffer par^1, V(j) in V buffer par);
   // kNext: tile j+1 exists, its S is computed here into sn.
-  auto iteration = [&](int j, auto par_tag, auto next_tag, f32x16(&sc)[2], f32x16(&sn)[2]) {
+  // kTail: the iterations after the loop, which rescale without a branch (a branch there
+  // leaves the compiler short of registers where its two paths meet)
+  auto iteration = [&](int j, auto par_tag, auto next_tag, Scores& sc, Scores& sn, auto tail_tag) {
     constexpr int par = decltype(par_tag)::value;
     constexpr bool kNext = decltype(next_tag)::value != 0;
     const bool copy_k2 = j + 2 < ntiles;  // K(j+2) exists (only if kNext)
-    rescale();
+    rescale(tail_tag);
     if constexpr (!kNext) {
-      u32x4 vf[NP];
-#pragma unroll
-      for (int i = 0; i < NP; ++i) vf[i] = read_v(par, i);
+      // last tile: the first two V fragments are read under the softmax, the rest two
+      // fragments ahead of their MFMAs (all 16 at once would not fit the registers)
+      u32x4 vf[NVF];
+      vf[0] = read_v(par, 0);
+      vf[1] = read_v(par, 1);
 #pragma unroll
       for (int e = 0; e < 32; ++e) {
         sm_elem(sc, e);
         if ((e & 7) == 7) sm_pack(sc, e >> 3);
       }
 #pragma unroll
-      for (int i = 0; i < NP; ++i) pv(i, vf[i]);
+      for (int i = 0; i < NP; ++i) {
+        pv(i, vf[i >> 1]);
+        if ((i & 1) == 0 && (i >> 1) + 2 < NVF) vf[(i >> 1) + 2] = read_v(par, (i >> 1) + 2);
+      }
     } else {
-      u32x4 kf[NS];
-      u32x4 vf[NP];
+      u32x4 kf[NKF];
+      u32x4 vf[NVF];
 #pragma unroll
-      for (int i = 0; i < 3; ++i) kf[i] = read_k(par ^ 1, i);
+      for (int f = 0; f < kKAhead; ++f) kf[f] = read_k(par ^ 1, f);
       __builtin_amdgcn_sched_barrier(0);
       // block 1: S(j+1) MFMAs; softmax elements 0..23 of S(j)
 #pragma unroll
       for (int i = 0; i < NS; ++i) {
-        s_mfma(sn, i, kf[i]);
+        s_mfma(sn, i, kf[i >> 1]);
         // this wave's 2*PW copies of K(j+2) and V(j+1), spread over the steps: a burst of
         // copies from all waves right after the barrier stalls their issue for hundreds of
         // cycles (the HBM/L2 -> LDS path moves about 64-80 bytes per clock per CU)
@@ -349,52 +414,52 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
             copy_piece(Vb, j + 1, lds0 + (2 + (par ^ 1)) * TB, true, c - PW);
           }
         }
-        if (i + 3 < NS) kf[i + 3] = read_k(par ^ 1, i + 3);
+        if ((i & 1) == 0 && (i >> 1) + kKAhead < NKF) kf[(i >> 1) + kKAhead] = read_k(par ^ 1, (i >> 1) + kKAhead);
         if (i == NS - 2) vf[0] = read_v(par, 0);
         if (i == NS - 1) vf[1] = read_v(par, 1);
         const int lo = 24 * i / NS, hi = 24 * (i + 1) / NS;
 #pragma unroll
         for (int e = lo; e < hi; ++e) sm_elem(sc, e);
 #pragma unroll
-        for (int g = 0; g < 3; ++g)
-          if (8 * (g + 1) > lo && 8 * (g + 1) <= hi) sm_pack(sc, g);
+        for (int G = 0; G < 3; ++G)
+          if (8 * (G + 1) > lo && 8 * (G + 1) <= hi) sm_pack(sc, G);
         __builtin_amdgcn_sched_barrier(0);
       }
-      // block 2, first half: PV of key block 0; softmax elements 24..31
+      // block 2, first half: PV of key chunk 0; softmax elements 24..31
 #pragma unroll
-      for (int i = 0; i < 2 * NDB; ++i) {
-        pv(i, vf[i]);
-        vf[i + 2] = read_v(par, i + 2);
-        const int lo = 24 + 8 * i / (2 * NDB), hi = 24 + 8 * (i + 1) / (2 * NDB);
+      for (int i = 0; i < NP / 2; ++i) {
+        pv(i, vf[i >> 1]);
+        if ((i & 1) == 0) vf[(i >> 1) + 2] = read_v(par, (i >> 1) + 2);
+        const int lo = 24 + 8 * i / (NP / 2), hi = 24 + 8 * (i + 1) / (NP / 2);
 #pragma unroll
         for (int e = lo; e < hi; ++e) sm_elem(sc, e);
-        if (i == 2 * NDB - 1) sm_pack(sc, 3);
+        if (i == NP / 2 - 1) sm_pack(sc, 3);
         __builtin_amdgcn_sched_barrier(0);
       }
-      // block 2, second half: PV of key block 1; max of S(j+1)
-      float mx = 0.f;
+      // block 2, second half: PV of key chunk 1; max of S(j+1)
+      float mx[2] = {0.f, 0.f};
       if (!need_mask(j + 1)) {
 #pragma unroll
-        for (int i = 2 * NDB; i < NP; ++i) {
-          pv(i, vf[i]);
-          if (i + 2 < NP) vf[i + 2] = read_v(par, i + 2);
-          const int r = i - 2 * NDB;
-          const int lo = 16 * r / (2 * NDB), hi = 16 * (r + 1) / (2 * NDB);
+        for (int i = NP / 2; i < NP; ++i) {
+          pv(i, vf[i >> 1]);
+          if ((i & 1) == 0 && (i >> 1) + 2 < NVF) vf[(i >> 1) + 2] = read_v(par, (i >> 1) + 2);
+          const int r = i - NP / 2;
+          const int lo = 16 * r / (NP / 2), hi = 16 * (r + 1) / (NP / 2);
 #pragma unroll
-          for (int k = lo; k < hi; ++k) max_op(sn, k, mx);
+          for (int k = lo; k < hi; ++k) max_op(sn, k >> 3, k & 7, mx[k >> 3]);
           __builtin_amdgcn_sched_barrier(0);
         }
       } else {
 #pragma unroll
-        for (int i = 2 * NDB; i < NP; ++i) {
-          pv(i, vf[i]);
-          if (i + 2 < NP) vf[i + 2] = read_v(par, i + 2);
+        for (int i = NP / 2; i < NP; ++i) {
+          pv(i, vf[i >> 1]);
+          if ((i & 1) == 0 && (i >> 1) + 2 < NVF) vf[(i >> 1) + 2] = read_v(par, (i >> 1) + 2);
         }
         apply_mask(sn, j + 1);
 #pragma unroll
-        for (int k = 0; k < 16; ++k) max_op(sn, k, mx);
+        for (int k = 0; k < 16; ++k) max_op(sn, k >> 3, k & 7, mx[k >> 3]);
       }
-      m_cur = halves_max(mx) * scale_log2;
+      tile_max(mx);
       wait_and_barrier<0>();
     }
   };
@@ -404,52 +469,55 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
   copy_v(0, 0);
   if (ntiles > 1) copy_k(1, 1);
   wait_and_barrier<0>();
-  f32x16 sa[2], sb[2];
+  Scores sa, sb;
   {
-    u32x4 kf[NS];
+    u32x4 kf[NKF];
 #pragma unroll
-    for (int i = 0; i < NS; ++i) kf[i] = read_k(0, i);
+    for (int f = 0; f < NKF; ++f) kf[f] = read_k(0, f);
 #pragma unroll
-    for (int i = 0; i < NS; ++i) s_mfma(sa, i, kf[i]);
+    for (int i = 0; i < NS; ++i) s_mfma(sa, i, kf[i >> 1]);
     if (need_mask(0)) apply_mask(sa, 0);
-    float mx = 0.f;
+    float mx[2] = {0.f, 0.f};
 #pragma unroll
-    for (int k = 0; k < 16; ++k) max_op(sa, k, mx);
-    m_cur = halves_max(mx) * scale_log2;
+    for (int k = 0; k < 16; ++k) max_op(sa, k >> 3, k & 7, mx[k >> 3]);
+    tile_max(mx);
   }
   wait_and_barrier<0>();  // every wave is done with K(0) before K(2) replaces it
 
   int j = 0;
   for (; j + 2 < ntiles; j += 2) {
-    iteration(j, Int<0>{}, Int<1>{}, sa, sb);
-    iteration(j + 1, Int<1>{}, Int<1>{}, sb, sa);
+    iteration(j, Int<0>{}, Int<1>{}, sa, sb, Int<0>{});
+    iteration(j + 1, Int<1>{}, Int<1>{}, sb, sa, Int<0>{});
   }
   if (j + 1 < ntiles) {
-    iteration(j, Int<0>{}, Int<1>{}, sa, sb);
-    iteration(j + 1, Int<1>{}, Int<0>{}, sb, sa);
+    iteration(j, Int<0>{}, Int<1>{}, sa, sb, Int<1>{});
+    iteration(j + 1, Int<1>{}, Int<0>{}, sb, sa, Int<1>{});
   } else {
-    iteration(j, Int<0>{}, Int<0>{}, sa, sb);
+    iteration(j, Int<0>{}, Int<0>{}, sa, sb, Int<1>{});
   }
 
-  const float inv = 1.f / halves_sum(l_run);
-  // masked variants take the output row and lane half from the lane id again: kept live
+  rows4_combine<false>(l_run[0], l_run[1]);
+  const float inv[2] = {1.f / l_run[0], 1.f / l_run[1]};
+  // masked variants take the output rows and lane row from the lane id again: kept live
   // across the loop they would take registers the loop needs (the compiler cannot tie
   // __lane_id() to threadIdx.x)
   const int lane_out = kMasked ? (int)__lane_id() : lane;
-  const int q_out = kMasked ? m0 + 32 * wave + (lane_out & 31) : q_row;
-  const int half_out = kMasked ? lane_out >> 5 : half;
-  if (!kMasked || q_out < s_q) {
-    uint16_t* orow = Oh + (long long)q_out * D;
+  const int q_out0 = kMasked ? m0 + 32 * wave + (lane_out & 15) : q_row0;
+  const int lr_out = kMasked ? lane_out >> 4 : lr;
 #pragma unroll
-    for (int db = 0; db < NDB; ++db)
+  for (int qb = 0; qb < 2; ++qb) {
+    const int q = q_out0 + 16 * qb;
+    if (!kMasked || q < s_q) {
+      uint16_t* orow = Oh + (long long)q * D;
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        // lane holds O^T[32db + 8jj + 4*half + r][q_row], r = 0..3
+      for (int db = 0; db < NDB; ++db) {
+        // lane holds O^T[16db + 4lr + i][q], i = 0..3
         u32x2 packed;
-        packed[0] = H::pack2(o[db][4 * jj] * inv, o[db][4 * jj + 1] * inv);
-        packed[1] = H::pack2(o[db][4 * jj + 2] * inv, o[db][4 * jj + 3] * inv);
-        st8(orow + 32 * db + 8 * jj + 4 * half_out, packed);
+        packed[0] = H::pack2(o[db][qb][0] * inv[qb], o[db][qb][1] * inv[qb]);
+        packed[1] = H::pack2(o[db][qb][2] * inv[qb], o[db][qb][3] * inv[qb]);
+        st8(orow + 16 * db + 4 * lr_out, packed);
       }
+    }
   }
 }
 

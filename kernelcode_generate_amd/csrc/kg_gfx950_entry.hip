@@ -737,7 +737,7 @@ int flash_attention_impl(const KgArgSlot* args, unsigned long long n) {
     const long long pairs = s.causal ? (long long)s.s_q * (s.s_q + 1) / 2 : (long long)s.s_q * s.s_kv;
     long long mfma = 0;
     if ((out.dtype == KG_DTYPE_BF16 || out.dtype == KG_DTYPE_F16) && fa_mfma_supported(s) && out.numel() > 0) {
-      // per workgroup: waves x key tiles x (D/8 MFMAs for S^T + D/8 for PV)
+      // per workgroup: waves x key tiles x (D/4 16x16x32 MFMAs for S^T + D/4 for PV)
       const int waves = fa_mfma_waves(s);
       const int bm = 32 * waves;
       const int nmb = (s.s_q + bm - 1) / bm;
@@ -746,7 +746,7 @@ int flash_attention_impl(const KgArgSlot* args, unsigned long long n) {
         const int n_end = s.causal ? std::min(s.s_kv, (mb + 1) * bm) : s.s_kv;
         tiles += (n_end + fa::kBC - 1) / fa::kBC;
       }
-      mfma = B_H * tiles * waves * (s.d / 4);
+      mfma = B_H * tiles * waves * (s.d / 2);
     }
     if (out.dtype == KG_DTYPE_F32 && fa_f32_mfma_supported(s) && out.numel() > 0) {
       // per workgroup and key tile: D MFMAs (32x32x2: D/2 for S^T, D/2 for PV) per wave that
@@ -767,7 +767,7 @@ int flash_attention_impl(const KgArgSlot* args, unsigned long long n) {
       mfma = B_H * waves_tiles * s.d;
     }
     const long long es = esize(out.dtype);
-    return record_cost(2 * B_H * pairs * D, mfma, out.dtype == KG_DTYPE_F32 ? 64 : 32,
+    return record_cost(2 * B_H * pairs * D, mfma, out.dtype == KG_DTYPE_F32 ? 64 : 16,
                        (q.numel() + k.numel() + v.numel()) * es, out.numel() * es);
   }
 
@@ -860,7 +860,7 @@ int kg_gfx950_cost(int op, const KgArgSlot* ordered_args, unsigned long long arg
   return rc;
 }
 
-int kg_gfx950_abi_version(void) { return 1; }
+int kg_gfx950_abi_version(void) { return 2; }
 
 int kg_gfx950_mfma_rate(int dtype_code, int mfma_m, int zero_operands, int iterations, int workgroups, double* tflops,
                         double* clock_ghz) {

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
     lib = native.load_library()
     for name in declared_functions():
         assert hasattr(lib, name), name
-    assert lib.kg_gfx950_abi_version() == 1
+    assert lib.kg_gfx950_abi_version() == 2
 
 
 def test_slot_layout_matches_reference():

@@ -5,8 +5,8 @@ result).
 
 MAC and byte counts are pinned by brute force (an oracle run gives the output shape; a
 mask count gives the causal pairs); MFMA counts are pinned by the MAC content of one
-MFMA (16x16x32: 8192 MACs in the pipelined GEMM; 32x32x16: 16384 in the conv and attention
-kernels; fp32 32x32x2: 2048) on exact-tile shapes, and by the hardware counter
+MFMA (16x16x32: 8192 MACs in the pipelined GEMM and the attention kernel; 32x32x16: 16384
+in the conv kernels; fp32 32x32x2: 2048) on exact-tile shapes, and by the hardware counter
 SQ_INSTS_MFMA on every kernel choice (profiles/mfma_instruction_counts.txt, made by
 tests/cost_cases.py under rocprofv3 --pmc). MFMA_CYCLES is the MFMA count times 16, 32 or
 64 by the same shapes.
@@ -39,8 +39,8 @@ from tests.cost_cases import CASES, modelled
 
 T = native.TensorSpec
 PIPE = "gfx950-lowering"
-MFMA_MACS = 32 * 32 * 16  # conv and attention kernels
-GEMM_MFMA_MACS = 16 * 16 * 32  # pipelined 16-bit GEMM
+MFMA_MACS = 32 * 32 * 16  # 16-bit conv kernels
+GEMM_MFMA_MACS = 16 * 16 * 32  # pipelined 16-bit GEMM and 16-bit attention
 PROFILE = Path(__file__).resolve().parents[1] / "profiles" / "mfma_instruction_counts.txt"
 
 
@@ -183,7 +183,7 @@ def test_attention_macs_count_mask(shape, causal):
 def test_attention_mfma_exact_tiles():
     shape = (4, 32, 2048, 128)
     c = costs(flash_attention_scaled_kernel, (T(shape, "bfloat16"),) * 4 + (128, 64, 0.088))
-    assert c["MFMA"] * MFMA_MACS == c["MAC"] and c["MFMA_CYCLES"] == 32 * c["MFMA"]
+    assert c["MFMA"] * GEMM_MFMA_MACS == c["MAC"] and c["MFMA_CYCLES"] == 16 * c["MFMA"]
     static = costs(flash_attention_inputs_static_tile_static_kernel, (T(shape, "bfloat16"),) * 4)
     assert static["MAC"] == c["MAC"] and static["MFMA"] == c["MFMA"]
 
@@ -195,7 +195,7 @@ def test_attention_causal_mfma_bounds():
     shape = (1, 32, 16384, 128)
     c = costs(flash_attention_scaled_causal_kernel, (T(shape, "bfloat16"),) * 4 + (128, 64, 0.088))
     full = 2 * 32 * 16384 * 16384 * 128
-    assert c["MAC"] <= c["MFMA"] * MFMA_MACS < 0.51 * full
+    assert c["MAC"] <= c["MFMA"] * GEMM_MFMA_MACS < 0.51 * full
 
 
 def _read_profile():
