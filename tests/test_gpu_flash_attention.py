@@ -163,6 +163,24 @@ def test_16bit(device, oracle_mod, dtype_name, shape, causal):
     assert_h16_close(to_numpy(out), ref, what=f"{dtype_name} {shape} causal={causal}")
 
 
+@pytest.mark.parametrize("dtype_name", ["float16", "bfloat16"])
+@pytest.mark.parametrize("shape,causal,scale", [((1, 2, 300, 64), True, 2.0), ((1, 1, 256, 128), False, 0.9),
+                                                ((2, 1, 130, 128), True, 0.05)])
+def test_16bit_scales(device, oracle_mod, dtype_name, shape, causal, scale):
+    """Scales away from 1/sqrt(D) (the kernel scales each fp32 score before its exp2; Q is used
+    as stored: multiplying it by the scale in its own 16-bit format would add a rounding of the
+    size of the format's unit roundoff to every score, twice the error of the exact scale for
+    bf16 on this test's inputs)."""
+    import torch
+
+    dt = getattr(torch, dtype_name)
+    rng = np.random.default_rng(shape[2] * 7 + shape[3])
+    (qt, q), (kt, k), (vt, v) = (round_to(rng.standard_normal(shape, dtype=np.float32), dt) for _ in range(3))
+    ref = oracle_mod.flash_attention_demo(q, k, v, 64, 64, scale=scale, causal=causal)
+    out = run(device, dt, qt, kt, vt, 64, 64, scale, causal)
+    assert_h16_close(to_numpy(out), ref, what=f"{dtype_name} {shape} causal={causal} scale={scale}")
+
+
 def _sampled_check(oracle_mod, got, q, k, v, heads, blocks, scale, causal, name):
     for (b, h) in heads:
         for m0, m1 in blocks:
