@@ -256,13 +256,16 @@ constexpr long long kMaxPipeLd = 1LL << 22;
 // grid covers the CUs, each workgroup row stores fp32 partial sums to a workspace, and a
 // second kernel adds them in chunk order. Returns the chunk count (1: no split). The decision
 // depends on the shape only, so every LDS ring depth gives the same bits.
-constexpr long long kSplitMaxTiles = 64;                 // split only below a quarter of the CUs
+constexpr long long kSplitMaxTiles = 64;                 // split below a quarter of the CUs, or
+constexpr long long kSplitMaxTilesLongK = 128;           // below half of them when K is long:
+constexpr long long kSplitLongK = 4096;                  // the fp32 partials then cost less than half the K loop
 constexpr long long kSplitMinChunk = 256;                // k per chunk, at least 8 slices
 constexpr long long kSplitMaxWorkspace = 64LL << 20;     // bytes of fp32 partials
 int pipe_splits(long long M, long long N, long long K, long long* chunk) {
   const long long tiles = cdiv(M, pipe_tile_m(M, N)) * cdiv(N, gemmp::kBN);
   *chunk = K;
-  if (tiles > kSplitMaxTiles || K < 2 * kSplitMinChunk) return 1;
+  const bool few = tiles <= kSplitMaxTiles || (tiles <= kSplitMaxTilesLongK && K >= kSplitLongK);
+  if (!few || K < 2 * kSplitMinChunk) return 1;
   long long splits = std::min(cdiv(kNumCUs, tiles), K / kSplitMinChunk);
   splits = std::min(splits, kSplitMaxWorkspace / (M * N * 4));
   if (splits < 2) return 1;

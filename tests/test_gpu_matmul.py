@@ -136,8 +136,9 @@ def test_pipe_256_row_tiles_with_bias(device, oracle_mod, bias_kind):
         ((128, 8192, 1024), "float16", "same", [(0, 16), (112, 128)]),  # 4 tiles: 32 chunks
         ((3, 1000, 136), "bfloat16", "none", None),  # one ragged tile, last chunk 8 deep short of a slice
         ((40, 2048, 520), "float16", "f32", None),  # 3 tiles, ragged N
+        ((2048, 4096, 2048), "bfloat16", "f32", [(0, 16), (2032, 2048)]),  # 128 tiles, long K: 2 chunks
     ],
-    ids=["16x4096x4096", "128x8192x1024", "3x1000x136", "40x2048x520"],
+    ids=["16x4096x4096", "128x8192x1024", "3x1000x136", "40x2048x520", "2048x4096x2048"],
 )
 def test_split_k_skinny(device, oracle_mod, shape, dtype_name, bias_kind, rows):
     """Outputs of few tiles run the pipelined kernel split over K (fp32 partial sums in a
