@@ -124,24 +124,6 @@ __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<
 __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 __device__ __forceinline__ void st8(void* p, u32x2 v) { *reinterpret_cast<u32x2*>(p) = v; }
 
-// Lane l and lane l ^ 32 combined, in every lane. v_permlane32_swap(a, b) swaps the high
-// half of a with the low half of b, so with a = b = x it returns x of the low half in
-// every lane (first result) and x of the high half in every lane (second result).
-// (The results are copied to scalars before any bit cast: __builtin_bit_cast of an
-// ext-vector element subscript reads element 0.)
-__device__ __forceinline__ float halves_max(float x) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, x);
-  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  const uint32_t lo = r[0], hi = r[1];
-  return __builtin_elementwise_maximum(__builtin_bit_cast(float, lo), __builtin_bit_cast(float, hi));
-}
-__device__ __forceinline__ float halves_sum(float x) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, x);
-  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  const uint32_t lo = r[0], hi = r[1];
-  return __builtin_bit_cast(float, lo) + __builtin_bit_cast(float, hi);
-}
-
 // Wave64 butterfly reductions through ds_swizzle/ds_bpermute (via __shfl_xor).
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
