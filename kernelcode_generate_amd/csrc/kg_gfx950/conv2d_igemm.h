@@ -51,6 +51,7 @@ struct Params {
   int K, P;   // C KH KW, Ho Wo
   int NP;     // N Ho Wo
   int w_vec;  // tap-major order with KH KW == 1 and 16-byte aligned weights: chunk loads
+  int kcs;    // split-K: k slices per workgroup row (blockIdx.y); 0 = the whole K range
   FastDiv div_khw, div_kw, div_p, div_wo, div_c;
 };
 
@@ -77,10 +78,15 @@ struct IgElem<F32Tag> {  // fp32 operands: 4 values per chunk, 16 per slice row
 // (kh, kw, c), so the values of one chunk share a tap: one bounds check and one address
 // per chunk (channels H W apart), weights read as scalars KH KW apart (as chunks for 1x1).
 enum ConvOrder { kChannelMajor = 0, kChannelMajorVecW = 1, kTapMajor = 2 };
+// Split-K (s.kcs > 0, for grids of fewer than two workgroups per CU): workgroup row y of the
+// grid runs k slices [y kcs, (y+1) kcs) and stores its fp32 sums, without bias, to
+// partial[y][N][F][Ho Wo]; conv_splitk_reduce_kernel adds the rows in y order, adds the bias
+// and rounds once.
 template <typename Tag, int kMI, int kBias, int kOrder>
 __global__ __launch_bounds__(convg::kThreads) void conv2d_igemm_kernel(
     const typename convg::IgElem<Tag>::T* __restrict__ x, const typename convg::IgElem<Tag>::T* __restrict__ wt,
-    typename convg::IgElem<Tag>::T* __restrict__ y, const void* __restrict__ bias, convg::Params s) {
+    typename convg::IgElem<Tag>::T* __restrict__ y, const void* __restrict__ bias, convg::Params s,
+    float* __restrict__ partial) {
   using namespace convg;
   using E = IgElem<Tag>;
   using T = typename E::T;
@@ -214,13 +220,19 @@ __global__ __launch_bounds__(convg::kThreads) void conv2d_igemm_kernel(
       for (int e = 0; e < 16; ++e) acc[i][b][e] = 0.f;
 
   const int frag = lane & 31, h = lane >> 5;
-  const int nk = (s.K + BK - 1) / BK;
-  load_regs(0);
+  int kt0 = 0, nk = (s.K + BK - 1) / BK;
+  if (s.kcs > 0) {  // split-K: this workgroup row's slices
+    kt0 = blockIdx.y * s.kcs;
+    nk = min(nk - kt0, s.kcs);
+    partial += (long long)blockIdx.y * s.NP * s.f;
+  }
+  load_regs(kt0);
   store_lds(0);
   __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    if (kt + 1 < nk) load_regs(kt + 1);  // gathers in flight during the MFMAs below
-    const u32x4* st = lds + (kt & 1) * (kStage / 16);
+  for (int it = 0; it < nk; ++it) {
+    const int kt = kt0 + it;
+    if (it + 1 < nk) load_regs(kt + 1);  // gathers in flight during the MFMAs below
+    const u32x4* st = lds + (it & 1) * (kStage / 16);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       u32x4 af[kMI], bf[2];
@@ -244,7 +256,7 @@ __global__ __launch_bounds__(convg::kThreads) void conv2d_igemm_kernel(
           }
         }
     }
-    if (kt + 1 < nk) store_lds((kt + 1) & 1);
+    if (it + 1 < nk) store_lds((it + 1) & 1);
     __syncthreads();
   }
 
@@ -258,6 +270,7 @@ __global__ __launch_bounds__(convg::kThreads) void conv2d_igemm_kernel(
     float bv = 0.f;
     if constexpr (kBias == 1) bv = static_cast<const float*>(bias)[f];
     if constexpr (kBias == 2) bv = E::to_float(static_cast<const T*>(bias)[f]);
+    if (s.kcs > 0) bv = 0.f;  // split-K: the reduction adds the bias
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
@@ -267,7 +280,16 @@ __global__ __launch_bounds__(convg::kThreads) void conv2d_igemm_kernel(
         float r[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) r[e] = acc[i][b][4 * q + e] + bv;
-        if (vec_out) {
+        if (s.kcs > 0) {  // fp32 partial sums in Y's layout
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int jv = j0 + e;
+            if (jv >= s.NP) break;
+            const uint32_t n = fdiv(jv, s.div_p);
+            const uint32_t p = jv - n * s.P;
+            partial[((long long)n * s.f + f) * s.P + p] = r[e];
+          }
+        } else if (vec_out) {
           const uint32_t n = fdiv(j0, s.div_p);
           const uint32_t p = j0 - n * s.P;
           T* yp = y + ((long long)n * s.f + f) * s.P + p;
@@ -299,6 +321,29 @@ __global__ __launch_bounds__(convg::kThreads) void conv2d_igemm_kernel(
   }
 }
 
+// y[e] = round(sum over the splits of partial[split][e] + bias[f]), e = (n F + f) P + p, in
+// split order. N F P < 2^31.
+constexpr int kConvReduceThreads = 256;
+template <typename Tag, int kBias>
+__global__ __launch_bounds__(kConvReduceThreads) void conv_splitk_reduce_kernel(
+    const float* __restrict__ partial, int splits, typename convg::IgElem<Tag>::T* __restrict__ y,
+    const void* __restrict__ bias, int nfp, FastDiv div_p, int f_count) {
+  using E = convg::IgElem<Tag>;
+  using T = typename E::T;
+  const int e = blockIdx.x * kConvReduceThreads + threadIdx.x;
+  if (e >= nfp) return;
+  float v = partial[e];
+  for (int sp = 1; sp < splits; ++sp) v += partial[(long long)sp * nfp + e];
+  if constexpr (kBias != 0) {
+    const uint32_t nf = fdiv((uint32_t)e, div_p);  // n F + f
+    const int f = (int)(nf % (uint32_t)f_count);
+    if constexpr (kBias == 1) v += static_cast<const float*>(bias)[f];
+    else v += E::to_float(static_cast<const T*>(bias)[f]);
+  }
+  if constexpr (E::kPerChunk == 8) y[e] = (T)(Half16<Tag>::pack2(v, 0.f) & 0xffffu);
+  else y[e] = v;
+}
+
 inline bool conv_igemm_supported(const ConvShape& s) {
   const long long K = (long long)s.c * s.kh * s.kw;
   const long long P = (long long)s.ho * s.wo;
@@ -319,6 +364,7 @@ inline convg::Params conv_igemm_params(const ConvShape& s) {
   p.div_wo = make_fast_div((uint32_t)s.wo);
   p.div_c = make_fast_div((uint32_t)s.c);
   p.w_vec = 0;
+  p.kcs = 0;
   return p;
 }
 
@@ -329,20 +375,46 @@ inline int conv_igemm_mi(const ConvShape& s) {
   return s.f > 64 && ((s.f + 127) / 128) * cols >= 512 ? 2 : 1;
 }
 
+// Split-K for grids of fewer than two workgroups per CU: the k slices are cut into chunks of
+// at least 4 until the grid reaches 512 workgroups (or the fp32 partials would pass
+// max_partial_bytes). Returns the split count (1: none) and the slices per chunk.
+inline int conv_igemm_splits(const ConvShape& s, bool f32, long long max_partial_bytes, int* kcs) {
+  const long long K = (long long)s.c * s.kh * s.kw;
+  const long long bk = f32 ? 16 : 32;
+  const long long nk = (K + bk - 1) / bk;
+  const long long np = (long long)s.n * s.ho * s.wo;
+  const long long nfp = np * s.f;
+  const int mi = conv_igemm_mi(s);
+  const long long grid = ((s.f + 64 * mi - 1) / (64 * mi)) * ((np + convg::kBN - 1) / convg::kBN);
+  *kcs = 0;
+  if (grid >= 512 || nk < 8 || nfp >= (1ll << 31)) return 1;
+  long long splits = std::min((512 + grid - 1) / grid, nk / 4);
+  splits = std::min(splits, max_partial_bytes / (nfp * 4));
+  if (splits < 2) return 1;
+  const long long c = (nk + splits - 1) / splits;
+  *kcs = (int)c;
+  return (int)((nk + c - 1) / c);
+}
+
+// splits > 1: split-K with kcs slices per chunk into the fp32 workspace `partial`
+// (splits x N F Ho Wo floats), then the reduction into y.
 template <typename Tag>
 hipError_t launch_conv2d_igemm(const void* x, const void* w, void* y, const void* bias, int bias_kind, int order,
-                               bool w_vec, const ConvShape& s, hipStream_t stream) {
+                               bool w_vec, const ConvShape& s, hipStream_t stream, float* partial = nullptr,
+                               int splits = 1, int kcs = 0) {
   using T = typename convg::IgElem<Tag>::T;
   convg::Params p = conv_igemm_params(s);
   p.w_vec = w_vec ? 1 : 0;
+  if (splits > 1) p.kcs = kcs;
+  else splits = 1;
   const int mi = conv_igemm_mi(s);
   const int grid = ((s.f + 64 * mi - 1) / (64 * mi)) * ((p.NP + convg::kBN - 1) / convg::kBN);
   const T* xp = static_cast<const T*>(x);
   const T* wp = static_cast<const T*>(w);
   T* yp = static_cast<T*>(y);
 #define KG_CONV_IG(MI, B, O)                                                                                  \
-  hipLaunchKernelGGL((conv2d_igemm_kernel<Tag, MI, B, O>), dim3(grid), dim3(convg::kThreads), 0, stream, xp, wp, yp, \
-                     bias, p)
+  hipLaunchKernelGGL((conv2d_igemm_kernel<Tag, MI, B, O>), dim3(grid, splits), dim3(convg::kThreads), 0, stream, xp, wp, \
+                     yp, bias, p, partial)
 #define KG_CONV_IG_B(MI, O)                  \
   if (bias_kind == 0) KG_CONV_IG(MI, 0, O);   \
   else if (bias_kind == 1) KG_CONV_IG(MI, 1, O); \
@@ -359,6 +431,21 @@ hipError_t launch_conv2d_igemm(const void* x, const void* w, void* y, const void
 #undef KG_CONV_IG_O
 #undef KG_CONV_IG_B
 #undef KG_CONV_IG
+  if (splits > 1) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int nfp = p.NP * s.f;
+    const int rgrid = (nfp + kConvReduceThreads - 1) / kConvReduceThreads;
+    if (bias_kind == 0)
+      hipLaunchKernelGGL((conv_splitk_reduce_kernel<Tag, 0>), dim3(rgrid), dim3(kConvReduceThreads), 0, stream, partial,
+                         splits, yp, bias, nfp, p.div_p, s.f);
+    else if (bias_kind == 1)
+      hipLaunchKernelGGL((conv_splitk_reduce_kernel<Tag, 1>), dim3(rgrid), dim3(kConvReduceThreads), 0, stream, partial,
+                         splits, yp, bias, nfp, p.div_p, s.f);
+    else
+      hipLaunchKernelGGL((conv_splitk_reduce_kernel<Tag, 2>), dim3(rgrid), dim3(kConvReduceThreads), 0, stream, partial,
+                         splits, yp, bias, nfp, p.div_p, s.f);
+  }
   return hipGetLastError();
 }
 

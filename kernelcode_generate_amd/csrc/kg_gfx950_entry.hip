@@ -659,9 +659,22 @@ int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
                                                                                      : kChannelMajor;
     const bool w_vec = order == kTapMajor && one_tap && vec_ok;
     const void* bp = bias.present ? bias.data : nullptr;
-    hipError_t e = out.dtype == KG_DTYPE_F32   ? launch_conv2d_igemm<F32Tag>(x.data, w.data, out.data, bp, bias_kind, order, w_vec, s, g_stream)
-                   : out.dtype == KG_DTYPE_BF16 ? launch_conv2d_igemm<Bf16Tag>(x.data, w.data, out.data, bp, bias_kind, order, w_vec, s, g_stream)
-                                                : launch_conv2d_igemm<F16Tag>(x.data, w.data, out.data, bp, bias_kind, order, w_vec, s, g_stream);
+    // grids of fewer than two workgroups per CU split K into fp32 partials (the workspace of
+    // the matmul's split-K, kept per stream)
+    int kcs = 0;
+    int splits = conv_igemm_splits(s, out.dtype == KG_DTYPE_F32, kSplitMaxWorkspace, &kcs);
+    float* partial = nullptr;
+    if (splits > 1) {
+      partial = static_cast<float*>(
+          split_workspace((size_t)splits * out.numel() * sizeof(float), g_stream));
+      if (partial == nullptr) splits = 1;  // no workspace: the whole K range in one pass
+    }
+    hipError_t e =
+        out.dtype == KG_DTYPE_F32
+            ? launch_conv2d_igemm<F32Tag>(x.data, w.data, out.data, bp, bias_kind, order, w_vec, s, g_stream, partial, splits, kcs)
+        : out.dtype == KG_DTYPE_BF16
+            ? launch_conv2d_igemm<Bf16Tag>(x.data, w.data, out.data, bp, bias_kind, order, w_vec, s, g_stream, partial, splits, kcs)
+            : launch_conv2d_igemm<F16Tag>(x.data, w.data, out.data, bp, bias_kind, order, w_vec, s, g_stream, partial, splits, kcs);
     if (e != hipSuccess) return fail(kHipFailure, "conv2d(igemm): %s", hipGetErrorString(e));
     return finish_launch("conv2d(igemm)");
   }

@@ -3,10 +3,12 @@ counter run can be laid beside the model:
 
     rocprofv3 --pmc SQ_INSTS_MFMA -d <dir> -- python3 -m tests.cost_cases
 
-Every case makes exactly one library kernel dispatch, in the order printed; inputs are
-generated on the host and copied, and the only other dispatches are the HIP runtime's own
-copy kernels (named __amd_rocclr_*) that some host-to-device copies use, so library
-dispatch i of the counter run is case i. Cases cover every kernel choice the model distinguishes: the
+Every case makes one library MFMA kernel dispatch, in the order printed, followed (for the
+implicit-GEMM conv cases whose grid is small enough to split K) by a split-K reduction
+kernel that issues no MFMA; inputs are generated on the host and copied, and the only other
+dispatches are the HIP runtime's own copy kernels (named __amd_rocclr_*) that some
+host-to-device copies use, so leaving out those and the *_splitk_reduce_kernel dispatches,
+library dispatch i of the counter run is case i. Cases cover every kernel choice the model distinguishes: the
 pipelined MFMA GEMM with 256- and 128-row tiles and with ragged edges, the fp32 MFMA GEMM
 aligned and ragged, the fp32 split-K GEMM, the SIMT GEMM, the MFMA conv with four and with two live waves and a
 ragged last row block, the implicit-GEMM conv (16-bit and fp32) and its row-piece form
@@ -23,8 +25,8 @@ import sys
 from kernelcode_generate_amd import native
 
 # (name, family, dtype, shapes, scalars): shapes are (out, in0, in1[, in2]) in the slot
-# order of the family's entry; bias is always absent. No case takes the split-K matmul path
-# (at most 64 output tiles with K >= 512), which adds a second (reduce) dispatch.
+# order of the family's entry; bias is always absent. No matmul case takes the split-K path;
+# the two implicit-GEMM conv cases do (their reduce dispatch issues no MFMA).
 CASES = (
     ("gemm_bf16_4096", "matmul", "bfloat16", ((4096, 4096), (4096, 4096), (4096, 4096)), ()),
     ("gemm_bf16_c2s_8192x1024x4096", "matmul", "bfloat16", ((8192, 1024), (8192, 4096), (4096, 1024)), ()),

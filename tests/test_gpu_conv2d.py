@@ -120,12 +120,16 @@ def test_general_params_f32(device, oracle_mod, xs, ws, stride, dil, pad):
         ((2, 3, 64, 64), (64, 3, 7, 7), (2, 2), (1, 1), (3, 3, 3, 3), "same"),  # K = 147: scalar weights
         ((1, 40, 19, 23), (96, 40, 3, 3), (1, 2), (2, 1), (2, 1, 0, 3), "f32"),  # F = 96, Ho*Wo odd
         ((3, 24, 10, 10), (20, 24, 5, 5), (1, 1), (2, 2), (4, 4, 4, 4), None),  # dilated, F < 32
+        ((2, 512, 7, 7), (512, 512, 3, 3), (1, 1), (1, 1), (1, 1, 1, 1), "f32"),  # 8 tiles: K split 36-58 ways
+        ((2, 256, 14, 14), (256, 256, 3, 3), (2, 2), (1, 1), (1, 1, 1, 1), "same"),  # stride 2, K split
     ],
-    ids=["s2", "c128", "1x1", "7x7s2", "f96_ragged", "dilated"],
+    ids=["s2", "c128", "1x1", "7x7s2", "f96_ragged", "dilated", "7x7_c512_splitk", "14x14s2_splitk"],
 )
 def test_implicit_gemm_shapes(device, oracle_mod, dtype_name, xs, ws, stride, dil, pad, bias):
     """Every conv the 3x3 kernel does not take runs as an implicit GEMM on matrix cores (16-bit
-    or fp32 MFMA). Reference: the oracle's demo loop nest on the identically rounded inputs.
+    or fp32 MFMA); grids of fewer than two workgroups per CU split K into fp32 partials added in
+    a fixed order (the 1x1, ragged, dilated and the last two cases). Reference: the oracle's
+    demo loop nest on the identically rounded inputs.
     fp32 tolerance: the demo's rtol 1e-4 / atol 1e-5 plus the rounding that two fp32 summation
     orders of K = C KH KW products can differ by, 4 sqrt(K) 2^-24 (|W| * |X|) (the
     probabilistic bound of Higham and Mary, SIAM J. Sci. Comput. 41 (2019))."""
