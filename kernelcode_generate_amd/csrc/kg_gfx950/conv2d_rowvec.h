@@ -54,6 +54,7 @@ struct Params {
   int P;     // Ho Wo
   int NP;    // N Ho Wo
   int bias_kind;  // 0 none, 1 fp32, 2 same 16-bit type
+  int kcs;        // split-K: slices per workgroup row (blockIdx.y); 0 = the whole K range
   FastDiv div_kh, div_p, div_wo;
 };
 
@@ -86,7 +87,8 @@ __global__ __launch_bounds__(convr::kThreads, 2) void conv2d_rowvec_kernel(const
                                                                         const uint16_t* __restrict__ wt,
                                                                         uint16_t* __restrict__ y,
                                                                         const void* __restrict__ bias,
-                                                                        convr::Params s) {
+                                                                        convr::Params s,
+                                                                        float* __restrict__ partial) {
   using namespace convr;
   using Geo = Geometry<KW, PL, G, S>;
   using Hf = Half16<Tag>;
@@ -221,7 +223,7 @@ __global__ __launch_bounds__(convr::kThreads, 2) void conv2d_rowvec_kernel(const
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][b][e] = 0.f;
 
-  const int nk = (s.runs + kRuns - 1) / kRuns;
+  int nk = (s.runs + kRuns - 1) / kRuns;
   auto compute = [&](int buf) {
     const char* st = lds + buf * kStage;
     const uint32_t sbase = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)st;
@@ -249,16 +251,23 @@ __global__ __launch_bounds__(convr::kThreads, 2) void conv2d_rowvec_kernel(const
   };
   // slice kt: its MFMAs read LDS stage kt & 1; slice kt + 1 goes from register set
   // (kt + 1) & 1 to the other stage; slice kt + 2 is loaded into set kt & 1 meanwhile.
+  // split-K: this workgroup row's slices kt0 .. kt0 + nk - 1 (kt below counts from kt0)
+  int kt0 = 0;
+  if (s.kcs > 0) {
+    kt0 = blockIdx.y * s.kcs;
+    nk = min(nk - kt0, s.kcs);
+    partial += (long long)blockIdx.y * s.NP * s.f;
+  }
   auto step = [&](int kt, auto par_tag) {
     constexpr int par = decltype(par_tag)::value;
-    if (kt + 2 < nk) load_regs(kt + 2, Int<par>{});
+    if (kt + 2 < nk) load_regs(kt0 + kt + 2, Int<par>{});
     compute(par);
     if (kt + 1 < nk) store_lds(par ^ 1, Int<par ^ 1>{});
     __syncthreads();
   };
-  load_regs(0, Int<0>{});
+  load_regs(kt0, Int<0>{});
   store_lds(0, Int<0>{});
-  if (nk > 1) load_regs(1, Int<1>{});
+  if (nk > 1) load_regs(kt0 + 1, Int<1>{});
   __syncthreads();
   for (int kt = 0; kt < nk; kt += 2) {
     step(kt, Int<0>{});
@@ -282,6 +291,11 @@ __global__ __launch_bounds__(convr::kThreads, 2) void conv2d_rowvec_kernel(const
         if (j >= s.NP) continue;
         const uint32_t n = fdiv(j, s.div_p);
         const uint32_t p = j - n * s.P;
+        if (s.kcs > 0) {  // fp32 partial sums in Y's layout, no bias
+          *reinterpret_cast<f32x4*>(partial + ((long long)n * s.f + f) * s.P + p) =
+              f32x4{acc[i][b][4 * q], acc[i][b][4 * q + 1], acc[i][b][4 * q + 2], acc[i][b][4 * q + 3]};
+          continue;
+        }
         u32x2 packed;
         packed[0] = Hf::pack2(acc[i][b][4 * q] + bv, acc[i][b][4 * q + 1] + bv);
         packed[1] = Hf::pack2(acc[i][b][4 * q + 2] + bv, acc[i][b][4 * q + 3] + bv);
@@ -324,7 +338,8 @@ __global__ __launch_bounds__(convr::kThreads, 2) void conv2d_rowvec_f32_kernel(c
                                                                               const float* __restrict__ wt,
                                                                               float* __restrict__ y,
                                                                               const float* __restrict__ bias,
-                                                                              convr::Params s) {
+                                                                              convr::Params s,
+                                                                              float* __restrict__ partial) {
   using namespace convr;
   using Geo = GeometryF32<KW, PL, S>;
   constexpr int G = Geo::G;
@@ -422,7 +437,7 @@ __global__ __launch_bounds__(convr::kThreads, 2) void conv2d_rowvec_f32_kernel(c
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][b][e] = 0.f;
 
-  const int nk = (s.runs + kRunsF32 - 1) / kRunsF32;
+  int nk = (s.runs + kRunsF32 - 1) / kRunsF32;
   auto compute = [&](int buf) {
     const uint32_t sbase = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)(lds + buf * kStage);
 #pragma unroll
@@ -446,16 +461,23 @@ __global__ __launch_bounds__(convr::kThreads, 2) void conv2d_rowvec_f32_kernel(c
       }
     }
   };
+  // split-K: this workgroup row's slices kt0 .. kt0 + nk - 1 (kt below counts from kt0)
+  int kt0 = 0;
+  if (s.kcs > 0) {
+    kt0 = blockIdx.y * s.kcs;
+    nk = min(nk - kt0, s.kcs);
+    partial += (long long)blockIdx.y * s.NP * s.f;
+  }
   auto step = [&](int kt, auto par_tag) {
     constexpr int par = decltype(par_tag)::value;
-    if (kt + 2 < nk) load_regs(kt + 2, Int<par>{});
+    if (kt + 2 < nk) load_regs(kt0 + kt + 2, Int<par>{});
     compute(par);
     if (kt + 1 < nk) store_lds(par ^ 1, Int<par ^ 1>{});
     __syncthreads();
   };
-  load_regs(0, Int<0>{});
+  load_regs(kt0, Int<0>{});
   store_lds(0, Int<0>{});
-  if (nk > 1) load_regs(1, Int<1>{});
+  if (nk > 1) load_regs(kt0 + 1, Int<1>{});
   __syncthreads();
   for (int kt = 0; kt < nk; kt += 2) {
     step(kt, Int<0>{});
@@ -476,9 +498,12 @@ __global__ __launch_bounds__(convr::kThreads, 2) void conv2d_rowvec_f32_kernel(c
         if (j >= s.NP) continue;
         const uint32_t n = fdiv(j, s.div_p);
         const uint32_t p = j - n * s.P;
-        *reinterpret_cast<f32x4*>(y + ((long long)n * s.f + f) * s.P + p) =
-            f32x4{acc[i][b][4 * qq] + bv, acc[i][b][4 * qq + 1] + bv, acc[i][b][4 * qq + 2] + bv,
-                  acc[i][b][4 * qq + 3] + bv};
+        // split-K: fp32 partial sums in Y's layout, no bias
+        const float bj = s.kcs > 0 ? 0.f : bv;
+        float* dst = s.kcs > 0 ? partial : y;
+        *reinterpret_cast<f32x4*>(dst + ((long long)n * s.f + f) * s.P + p) =
+            f32x4{acc[i][b][4 * qq] + bj, acc[i][b][4 * qq + 1] + bj, acc[i][b][4 * qq + 2] + bj,
+                  acc[i][b][4 * qq + 3] + bj};
       }
   }
 }
@@ -518,6 +543,39 @@ inline long long conv_rowvec_mfma(const ConvShape& s, bool f32 = false) {
   return tiles * slices * 4 * mi * 2 * s.kw * (f32 ? 4 : 1);
 }
 
+// Split-K for grids of fewer than two workgroups per CU: slices (16 or, fp32, 8 (c, kh) runs)
+// cut into chunks of at least 2, the split count chosen by a time model fitted to measured
+// row-piece convs of grids under 512 workgroups: a slice takes 280 + 135 KW ns (fp32
+// 515 + 250 KW) on a CU of its own and twice that per workgroup on a CU shared by two (the
+// grid runs in ceil(workgroups / 256) rounds), the fp32 partials' write and read move 8
+// bytes per output element and split at about 4 bytes/ns, and the reduction launch adds
+// 4 us. Small outputs gain most (N=1 28x28 C=F=128 3x3: 8 splits, 20 -> 10 us); large ones
+// keep one pass (N=32 of that: the partials would cost 19 us to save 8).
+// Returns the split count (1: none) and the slices per chunk; the fp32 partials stay
+// under max_partial_bytes.
+inline int conv_rowvec_splits(const ConvShape& s, bool f32, long long max_partial_bytes, int* kcs) {
+  const long long runs = f32 ? convr::kRunsF32 : convr::kRuns;
+  const long long nk = ((long long)s.c * s.kh + runs - 1) / runs;
+  const long long np = (long long)s.n * s.ho * s.wo;
+  const long long nfp = np * s.f;
+  const int mi = conv_rowvec_mi(s);
+  const long long grid = ((s.f + 64 * mi - 1) / (64 * mi)) * ((np + convr::kBN - 1) / convr::kBN);
+  *kcs = 0;
+  if (grid >= 512 || nk < 4 || nfp >= (1ll << 31)) return 1;
+  const long long smax =
+      std::min(std::min((512 + grid - 1) / grid, nk / 2), max_partial_bytes / (nfp * 4));
+  const long long slice_ns = f32 ? 515 + 250 * s.kw : 280 + 135 * s.kw;
+  long long best = 1, best_ns = (grid + 255) / 256 * nk * slice_ns;
+  for (long long sp = 2; sp <= smax; ++sp) {
+    const long long t = (grid * sp + 255) / 256 * ((nk + sp - 1) / sp) * slice_ns + sp * nfp * 8 / 4000 + 4000;
+    if (t < best_ns) { best = sp; best_ns = t; }
+  }
+  if (best < 2) return 1;
+  const long long c = (nk + best - 1) / best;
+  *kcs = (int)c;
+  return (int)((nk + c - 1) / c);
+}
+
 inline convr::Params conv_rowvec_params(const ConvShape& s, int bias_kind) {
   convr::Params p;
   p.n = s.n; p.c = s.c; p.h = s.h; p.w = s.w; p.f = s.f; p.kh = s.kh; p.ho = s.ho; p.wo = s.wo; p.pt = s.pt;
@@ -526,6 +584,7 @@ inline convr::Params conv_rowvec_params(const ConvShape& s, int bias_kind) {
   p.P = s.ho * s.wo;
   p.NP = s.n * p.P;
   p.bias_kind = bias_kind;
+  p.kcs = 0;
   p.div_kh = make_fast_div((uint32_t)s.kh);
   p.div_p = make_fast_div((uint32_t)p.P);
   p.div_wo = make_fast_div((uint32_t)s.wo);
@@ -533,13 +592,19 @@ inline convr::Params conv_rowvec_params(const ConvShape& s, int bias_kind) {
 }
 
 // fp32 operands; a bias (kind 1 or 2) is fp32 either way.
+// splits > 1: split-K into the fp32 workspace `partial` (splits x N F Ho Wo floats) with kcs
+// slices per chunk, then the reduction into y (conv_splitk_reduce_kernel).
 inline hipError_t launch_conv2d_rowvec_f32(const float* x, const float* w, float* y, const float* bias, int bias_kind,
-                                           const ConvShape& s, hipStream_t stream) {
-  const convr::Params p = conv_rowvec_params(s, bias_kind);
+                                           const ConvShape& s, hipStream_t stream, float* partial = nullptr,
+                                           int splits = 1, int kcs = 0) {
+  convr::Params p = conv_rowvec_params(s, bias_kind);
+  if (splits > 1) p.kcs = kcs;
+  else splits = 1;
   const int mi = conv_rowvec_mi(s);
   const int grid = ((s.f + 64 * mi - 1) / (64 * mi)) * ((p.NP + convr::kBN - 1) / convr::kBN);
 #define KG_CONV_RVF(MI, KW_, PL_, S_) \
-  hipLaunchKernelGGL((conv2d_rowvec_f32_kernel<MI, KW_, PL_, S_>), dim3(grid), dim3(convr::kThreads), 0, stream, x, w, y, bias, p)
+  hipLaunchKernelGGL((conv2d_rowvec_f32_kernel<MI, KW_, PL_, S_>), dim3(grid, splits), dim3(convr::kThreads), 0, stream, x, w, \
+                     y, bias, p, partial)
 #define KG_CONV_RVF_MI(KW_, PL_, S_) \
   if (mi == 2) { KG_CONV_RVF(2, KW_, PL_, S_); } else { KG_CONV_RVF(1, KW_, PL_, S_); }
   if (s.kw == 3) {
@@ -549,19 +614,34 @@ inline hipError_t launch_conv2d_rowvec_f32(const float* x, const float* w, float
   }
 #undef KG_CONV_RVF_MI
 #undef KG_CONV_RVF
+  if (splits > 1) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int nfp = p.NP * s.f;
+    const int rgrid = (nfp + kConvReduceThreads - 1) / kConvReduceThreads;
+    if (bias_kind == 0)
+      hipLaunchKernelGGL((conv_splitk_reduce_kernel<F32Tag, 0>), dim3(rgrid), dim3(kConvReduceThreads), 0, stream,
+                         partial, splits, y, bias, nfp, p.div_p, s.f);
+    else
+      hipLaunchKernelGGL((conv_splitk_reduce_kernel<F32Tag, 1>), dim3(rgrid), dim3(kConvReduceThreads), 0, stream,
+                         partial, splits, y, bias, nfp, p.div_p, s.f);
+  }
   return hipGetLastError();
 }
 
 template <typename Tag>
 hipError_t launch_conv2d_rowvec(const uint16_t* x, const uint16_t* w, uint16_t* y, const void* bias, int bias_kind,
-                                const ConvShape& s, hipStream_t stream) {
-  const convr::Params p = conv_rowvec_params(s, bias_kind);
+                                const ConvShape& s, hipStream_t stream, float* partial = nullptr, int splits = 1,
+                                int kcs = 0) {
+  convr::Params p = conv_rowvec_params(s, bias_kind);
+  if (splits > 1) p.kcs = kcs;
+  else splits = 1;
   const int mi = conv_rowvec_mi(s);
   const int piece = conv_rowvec_piece(s);
   const int grid = ((s.f + 64 * mi - 1) / (64 * mi)) * ((p.NP + convr::kBN - 1) / convr::kBN);
 #define KG_CONV_RV(MI, KW_, PL_, G_, S_)                                                                     \
-  hipLaunchKernelGGL((conv2d_rowvec_kernel<Tag, MI, KW_, PL_, G_, S_>), dim3(grid), dim3(convr::kThreads), 0, stream, x, \
-                     w, y, bias, p)
+  hipLaunchKernelGGL((conv2d_rowvec_kernel<Tag, MI, KW_, PL_, G_, S_>), dim3(grid, splits), dim3(convr::kThreads), 0, \
+                     stream, x, w, y, bias, p, partial)
 #define KG_CONV_RV_MI(KW_, PL_, G_, S_) \
   if (mi == 2) KG_CONV_RV(2, KW_, PL_, G_, S_); \
   else KG_CONV_RV(1, KW_, PL_, G_, S_)
@@ -575,6 +655,21 @@ hipError_t launch_conv2d_rowvec(const uint16_t* x, const uint16_t* w, uint16_t* 
 #undef KG_CONV_RV_G
 #undef KG_CONV_RV_MI
 #undef KG_CONV_RV
+  if (splits > 1) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int nfp = p.NP * s.f;
+    const int rgrid = (nfp + kConvReduceThreads - 1) / kConvReduceThreads;
+    if (bias_kind == 0)
+      hipLaunchKernelGGL((conv_splitk_reduce_kernel<Tag, 0>), dim3(rgrid), dim3(kConvReduceThreads), 0, stream, partial,
+                         splits, y, bias, nfp, p.div_p, s.f);
+    else if (bias_kind == 1)
+      hipLaunchKernelGGL((conv_splitk_reduce_kernel<Tag, 1>), dim3(rgrid), dim3(kConvReduceThreads), 0, stream, partial,
+                         splits, y, bias, nfp, p.div_p, s.f);
+    else
+      hipLaunchKernelGGL((conv_splitk_reduce_kernel<Tag, 2>), dim3(rgrid), dim3(kConvReduceThreads), 0, stream, partial,
+                         splits, y, bias, nfp, p.div_p, s.f);
+  }
   return hipGetLastError();
 }
 

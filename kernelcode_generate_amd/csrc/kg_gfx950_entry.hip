@@ -623,12 +623,23 @@ int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
     if (e != hipSuccess) return fail(kHipFailure, "conv2d(mfma): %s", hipGetErrorString(e));
     return finish_launch("conv2d(mfma)");
   }
+  // split-K for conv grids of fewer than two workgroups per CU: fp32 partials in the
+  // matmul's per-stream split-K workspace (no workspace: the whole K range in one pass)
+  auto conv_partials = [&](int& splits) -> float* {
+    if (splits <= 1) return nullptr;
+    float* ws = static_cast<float*>(split_workspace((size_t)splits * out.numel() * sizeof(float), g_stream));
+    if (ws == nullptr) splits = 1;
+    return ws;
+  };
   if (out.dtype == KG_DTYPE_F32 && conv_rowvec_supported(s, true) && aligned16(x.data) && aligned16(w.data) &&
       aligned16(out.data)) {
+    int kcs = 0;
+    int splits = conv_rowvec_splits(s, true, kSplitMaxWorkspace, &kcs);
+    float* partial = conv_partials(splits);
     hipError_t e = launch_conv2d_rowvec_f32(static_cast<const float*>(x.data), static_cast<const float*>(w.data),
                                             static_cast<float*>(out.data),
                                             bias.present ? static_cast<const float*>(bias.data) : nullptr,
-                                            bias.present ? 1 : 0, s, g_stream);
+                                            bias.present ? 1 : 0, s, g_stream, partial, splits, kcs);
     if (e != hipSuccess) return fail(kHipFailure, "conv2d(rowvec f32): %s", hipGetErrorString(e));
     return finish_launch("conv2d(rowvec f32)");
   }
@@ -639,8 +650,12 @@ int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
     const uint16_t* wp = static_cast<const uint16_t*>(w.data);
     uint16_t* yp = static_cast<uint16_t*>(out.data);
     const void* bp = bias.present ? bias.data : nullptr;
-    hipError_t e = out.dtype == KG_DTYPE_BF16 ? launch_conv2d_rowvec<Bf16Tag>(xp, wp, yp, bp, bias_kind, s, g_stream)
-                                              : launch_conv2d_rowvec<F16Tag>(xp, wp, yp, bp, bias_kind, s, g_stream);
+    int kcs = 0;
+    int splits = conv_rowvec_splits(s, false, kSplitMaxWorkspace, &kcs);
+    float* partial = conv_partials(splits);
+    hipError_t e = out.dtype == KG_DTYPE_BF16
+                       ? launch_conv2d_rowvec<Bf16Tag>(xp, wp, yp, bp, bias_kind, s, g_stream, partial, splits, kcs)
+                       : launch_conv2d_rowvec<F16Tag>(xp, wp, yp, bp, bias_kind, s, g_stream, partial, splits, kcs);
     if (e != hipSuccess) return fail(kHipFailure, "conv2d(rowvec): %s", hipGetErrorString(e));
     return finish_launch("conv2d(rowvec)");
   }
@@ -659,16 +674,9 @@ int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
                                                                                      : kChannelMajor;
     const bool w_vec = order == kTapMajor && one_tap && vec_ok;
     const void* bp = bias.present ? bias.data : nullptr;
-    // grids of fewer than two workgroups per CU split K into fp32 partials (the workspace of
-    // the matmul's split-K, kept per stream)
     int kcs = 0;
     int splits = conv_igemm_splits(s, out.dtype == KG_DTYPE_F32, kSplitMaxWorkspace, &kcs);
-    float* partial = nullptr;
-    if (splits > 1) {
-      partial = static_cast<float*>(
-          split_workspace((size_t)splits * out.numel() * sizeof(float), g_stream));
-      if (partial == nullptr) splits = 1;  // no workspace: the whole K range in one pass
-    }
+    float* partial = conv_partials(splits);
     hipError_t e =
         out.dtype == KG_DTYPE_F32
             ? launch_conv2d_igemm<F32Tag>(x.data, w.data, out.data, bp, bias_kind, order, w_vec, s, g_stream, partial, splits, kcs)

@@ -227,8 +227,11 @@ def _rowvec_mfma(xs, ws, stride, pad, f32=False):
         ((1, 24, 17, 32), (40, 24, 3, 3), 2, (1, 0, 1, 1), "f32", None),  # stride 2, odd H, 8-pixel pieces
         ((2, 32, 32, 64), (64, 32, 1, 1), 2, (0, 0, 0, 0), "same", None),  # 1x1 stride 2
         ((1, 16, 8, 40), (24, 16, 1, 1), 2, (0, 0, 0, 0), None, None),  # 1x1 stride 2, Wo = 20
+        ((1, 120, 28, 28), (96, 120, 3, 3), 1, (1, 1, 1, 1), "same", None),  # 7 workgroups: K split, last chunk short
+        ((1, 256, 8, 32), (64, 256, 1, 1), 1, (0, 0, 0, 0), "f32", None),  # 1x1, 2 workgroups: K split
     ],
-    ids=["p8", "p4_f80", "kh5", "pads_0_2", "1x1_rpad", "bm128", "s2_p4", "s2_p8", "1x1_s2", "1x1_s2_p4"],
+    ids=["p8", "p4_f80", "kh5", "pads_0_2", "1x1_rpad", "bm128", "s2_p4", "s2_p8", "1x1_s2", "1x1_s2_p4",
+         "splitk", "1x1_splitk"],
 )
 def test_row_piece_path(device, oracle_mod, dtype_name, xs, ws, stride, pad, bias, images):
     """Convs of stride 1 or 2 whose rows split into whole 8- or 4-pixel pieces (fp32: 4), with
