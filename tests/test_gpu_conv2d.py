@@ -176,6 +176,8 @@ def test_implicit_gemm_shapes(device, oracle_mod, dtype_name, xs, ws, stride, di
         ((1, 64, 12, 24), (64, 64, 3, 3), "f32"),  # MFMA: 7-row blocks with a 5-row tail, W <= 32
         ((3, 64, 20, 40), (64, 64, 3, 3), "h16"),  # MFMA: 6-row tail, second pixel block partly live
         ((1, 64, 1, 8), (64, 64, 3, 3), "f32"),  # MFMA: one row, one 8-column block
+        ((2, 64, 9, 32), (64, 64, 3, 3), "h16"),  # MFMA: second window live for pixels 28-31 only
+        ((1, 64, 15, 48), (64, 64, 3, 3), None),  # MFMA: 1-row tail, second window partly live
         ((1, 64, 12, 20), (64, 64, 3, 3), "f32"),  # W % 8 != 0: implicit GEMM on 4-pixel row pieces
         ((3, 16, 9, 13), (32, 16, 3, 3), "f32"),
         ((1, 8, 7, 7), (5, 8, 3, 3), None),
