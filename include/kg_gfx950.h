@@ -91,6 +91,9 @@ int kg_gfx950_matmul_entry(const KgArgSlot* ordered_args, unsigned long long arg
  *    [, tile_f, tile_c, tile_n, tile_ho, tile_wo])
  * 12 or 17 slots. Static demos bake stride/dilation/pad into their generated entry,
  * which forwards the constants here. Ho/Wo follow kernel/conv2d/inputs_static_tile_static.py:155-156.
+ * 16-bit and fp32 convs whose grid would leave CUs idle (small batches, deep 14x14 / 7x7
+ * layers) split the contraction over workgroups and add the fp32 partial sums in a second
+ * kernel, in the matmul's per-(device, stream) workspace (allocated on first use, kept).
  */
 int kg_gfx950_conv2d_entry(const KgArgSlot* ordered_args, unsigned long long arg_count);
 
