@@ -4,8 +4,8 @@ counter run can be laid beside the model:
     rocprofv3 --pmc SQ_INSTS_MFMA -d <dir> -- python3 -m tests.cost_cases
 
 Every case makes one library MFMA kernel dispatch, in the order printed, followed (for the
-implicit-GEMM conv cases whose grid is small enough to split K) by a split-K reduction
-kernel that issues no MFMA; inputs are generated on the host and copied, and the only other
+conv cases whose grid is small enough to split K) by a split-K reduction kernel that issues
+no MFMA; inputs are generated on the host and copied, and the only other
 dispatches are the HIP runtime's own copy kernels (named __amd_rocclr_*) that some
 host-to-device copies use, so leaving out those and the *_splitk_reduce_kernel dispatches,
 library dispatch i of the counter run is case i. Cases cover every kernel choice the model distinguishes: the
@@ -26,7 +26,8 @@ from kernelcode_generate_amd import native
 
 # (name, family, dtype, shapes, scalars): shapes are (out, in0, in1[, in2]) in the slot
 # order of the family's entry; bias is always absent. No matmul case takes the split-K path;
-# the two implicit-GEMM conv cases do (their reduce dispatch issues no MFMA).
+# the two implicit-GEMM conv cases and three of the row-piece ones do (their reduce dispatch
+# issues no MFMA).
 CASES = (
     ("gemm_bf16_4096", "matmul", "bfloat16", ((4096, 4096), (4096, 4096), (4096, 4096)), ()),
     ("gemm_bf16_c2s_8192x1024x4096", "matmul", "bfloat16", ((8192, 1024), (8192, 4096), (4096, 1024)), ()),
