@@ -31,7 +31,9 @@
 // LDS layout (64 banks of 4 bytes; ds_read_b128 serves 16 lanes per cycle): a pixel of the
 // input tile is 128 bytes (8 chunks of 8 channels); chunk c of column col sits at slot
 // c ^ ((col >> 1) & 7), so 16 consecutive pixels at one chunk hit 16 distinct 16-byte bank
-// groups. Weights are [f][576 values] with rows padded to 1168 bytes, so 16 consecutive
+// groups. Tile rows are 16 bytes longer than their 58 columns: a staging write (lanes =
+// (tile row, 8-column block) at one column offset and chunk) then meets each bank group from
+// at most 4 addresses where a whole-256-byte pitch put up to 9 on one. Weights are [f][576 values] with rows padded to 1168 bytes, so 16 consecutive
 // filters at one offset fall in distinct bank groups. Output buffers (in the weight area,
 // once the weights are in registers) are laid out [f][row][w] like Y with filter planes
 // padded so the 8-byte writes of 32 consecutive filters spread over all bank groups.
@@ -52,7 +54,8 @@ constexpr int kCols = 58;           // LDS tile columns: W <= 56 plus two zero c
 constexpr int kC = 64;
 constexpr int kF = 64;
 constexpr int kKSteps = 36;                      // 9 taps x 4 groups of 16 channels
-constexpr int kXBytes = kInRows * kCols * 128;   // channel-last input tile
+constexpr int kRowPitch = kCols * 128 + 16;      // bytes per tile row (see the LDS layout)
+constexpr int kXBytes = kInRows * kRowPitch;     // channel-last input tile
 constexpr int kWPitch = kC * 9 * 2 + 16;         // one filter's weights in LDS, padded
 constexpr int kWBytes = kF * kWPitch;
 constexpr int kMaxPhaseRows = 3;
@@ -125,7 +128,7 @@ __global__ __launch_bounds__(convk::kThreads, 1) void conv2d_3x3s1p1_mfma_kernel
     load_half(0);
     auto store_half = [&](int q) {
       if (lrow >= kHalfRows[q]) return;
-      const int base = ((kHalfRow0[q] + lrow) * kCols + 1 + 8 * col) * 8;
+      const int base = (kHalfRow0[q] + lrow) * (kRowPitch / 16) + (1 + 8 * col) * 8;
 #pragma unroll
       for (int o = 0; o < 2; ++o) {
         u32x4 cols[8];
@@ -160,7 +163,7 @@ __global__ __launch_bounds__(convk::kThreads, 1) void conv2d_3x3s1p1_mfma_kernel
       const int zc = (i >> 3) % zcols;
       const int r = (i >> 3) / zcols;
       const int zcol = zc == 0 ? 0 : W + zc;
-      x_lds[(r * kCols + zcol) * 8 + x_slot(zcol, c8)] = u32x4{0, 0, 0, 0};
+      x_lds[r * (kRowPitch / 16) + zcol * 8 + x_slot(zcol, c8)] = u32x4{0, 0, 0, 0};
     }
     __syncthreads();  // 1
     store_half(0);
@@ -219,7 +222,7 @@ __global__ __launch_bounds__(convk::kThreads, 1) void conv2d_3x3s1p1_mfma_kernel
 
   const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)&lds[0];
   // A operand: pixel w = 32pb + lane%32 (dead lanes past W read column W-1), channels
-  // 16cg + 8hsel .. +7 at tap (kh, kw): LDS byte ((r + kh)*58 + w + kw)*128 + 16*slot.
+  // 16cg + 8hsel .. +7 at tap (kh, kw): LDS byte (r + kh)*pitch + (w + kw)*128 + 16*slot.
   const int wpix = min(32 * pb + (lane & 31), W - 1);
   uint32_t a_off[3][4];
 #pragma unroll
@@ -230,7 +233,7 @@ __global__ __launch_bounds__(convk::kThreads, 1) void conv2d_3x3s1p1_mfma_kernel
       a_off[kw][cg] = lds0 + col * 128 + 16 * x_slot(col, 2 * cg + hsel);
     }
   auto read_a = [&](int kw, int cg, int trow) -> u32x4 {  // tile row trow, column offset kw
-    return *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(a_off[kw][cg] + trow * kCols * 128);
+    return *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(a_off[kw][cg] + trow * kRowPitch);
   };
   float bv = 0.f;
   if constexpr (kBias == 1) bv = static_cast<const float*>(bias)[f];
