@@ -15,7 +15,11 @@ kernel_gen/dsl/ast/mlir_gen.py:66-95). This front end does the same walk over Py
     any test on plain Python values decided while walking;
   - `min` / `max` and integer arithmetic on symbols as symbolic expressions;
   - each DSL operation call (kernel_gen.operation's `dma.*`, `kernel.*`, `nn.transpose`;
-    here kernelcode_generate_amd.operation) as the IR operation of the same name.
+    here kernelcode_generate_amd.operation) as the IR operation of the same name; the
+    operations that return a new tile (`slice`, `load`, `copy`, `cast`, `transpose`) as an
+    allocation followed by the target-first operation, as the reference's lowering bridges
+    them (kernel_gen/operation/dma.py:945-975); `flatten` as a reshape;
+  - the `arch` launch queries (`get_block_id()` ...) as symbolic launch values.
 
 Runtime arguments decide parameter kinds, as they do for the reference's mlir_gen: a tensor
 or array is a memory parameter (its rank and element type are taken from it), None an
@@ -30,13 +34,15 @@ import builtins
 import inspect
 import math
 import textwrap
-from dataclasses import dataclass
+import types
+from dataclasses import dataclass, replace
 from enum import Enum
 from numbers import Integral, Real
 from typing import Any, Callable, Sequence
 
 from ..core.error import ErrorKind, ErrorModule, KernelCodeError
 from ..ir import TORCH_DTYPE_NAMES, Cmp, FVal, Func, Mem, Op, Param, Present, Sym, as_sym, smax, smin, sym_bin
+from ..ir.sym import HW_QUERIES
 from ..operation.kernel import KernelBinaryElewiseKind, KernelReduceKind
 from ..symbol_variable import MemorySpace, NumericType
 
@@ -98,22 +104,31 @@ _BINARY_KINDS = {"kernel.add": "add", "kernel.sub": "sub", "kernel.mul": "mul", 
 
 
 class _Builder:
-    def __init__(self, func_obj: Callable, runtime_args: Sequence[Any]) -> None:
-        self.func_obj = func_obj
-        self.globals = getattr(func_obj, "__globals__", {})
-        source = textwrap.dedent(inspect.getsource(func_obj))
-        tree = ast.parse(source)
-        fdefs = [n for n in tree.body if isinstance(n, ast.FunctionDef)]
-        if not fdefs:
-            raise _error(f"{func_obj!r} is not a Python function with source")
-        self.fdef = fdefs[0]
-        self.scopes: list[dict[str, Any]] = [{}]
+    def __init__(self, fdef: ast.FunctionDef, globals_: dict, free: dict, runtime_args: Sequence[Any]) -> None:
+        self.globals = globals_
+        self.fdef = fdef
+        self.scopes: list[dict[str, Any]] = [dict(free)]
+        self.depth = 0
         self.block: list[Op] = []
         self.counter = 0
         self.names: set[str] = set()
         self.params: list[Param] = []
         self.args: dict[str, Mem] = {}
         self._bind_params(runtime_args)
+
+    @classmethod
+    def of_function(cls, func_obj: Callable, runtime_args: Sequence[Any]) -> "_Builder":
+        try:
+            source = textwrap.dedent(inspect.getsource(func_obj))
+        except (OSError, TypeError):
+            raise _error(f"{func_obj!r} is not a Python function with source") from None
+        fdefs = [n for n in ast.parse(source).body if isinstance(n, ast.FunctionDef)]
+        if not fdefs:
+            raise _error(f"{func_obj!r} is not a Python function with source")
+        # free variables of a kernel defined inside another function are visible too
+        cells = getattr(func_obj, "__closure__", None) or ()
+        free = dict(zip(func_obj.__code__.co_freevars, (c.cell_contents for c in cells)))
+        return cls(fdefs[0], getattr(func_obj, "__globals__", {}), free, runtime_args)
 
     # -- names -------------------------------------------------------------------------
     def fresh(self, hint: str) -> str:
@@ -194,6 +209,7 @@ class _Builder:
 
     # -- statements --------------------------------------------------------------------
     def run(self) -> Func:
+        _check_returns(self.fdef.body, self.fdef.name)
         self.exec_block(self.fdef.body)
         return Func(self.fdef.name, self.params, self.args, self.block)
 
@@ -376,7 +392,11 @@ class _Builder:
         if isinstance(op, (ast.Is, ast.IsNot)):
             if right is not None:
                 raise _error("`is` compares with None only", node)
-            if isinstance(left, Mem) and left.origin == "arg" and left.optional:
+            if isinstance(left, Mem) and left.origin == "arg":
+                if not left.optional:
+                    # tested inside a called subroutine: the argument may be absent too
+                    left.optional = True
+                    self.params = [replace(p, optional=True) if p.name == left.name else p for p in self.params]
                 return Present(left.name) if isinstance(op, ast.IsNot) else _Not(Present(left.name))
             present = left is not None
             return present if isinstance(op, ast.IsNot) else not present
@@ -416,10 +436,49 @@ class _Builder:
                 if any(isinstance(a, (Sym, FVal, Mem)) for a in args):
                     raise _error(f"{getattr(fn, '__name__', fn)} of a runtime value is not supported", node)
                 return fn(*args, **kwargs)
+            if isinstance(fn, types.FunctionType):
+                return self.inline(fn, args, kwargs, node)
             raise _error(f"call of {getattr(fn, '__name__', fn)!r} is not a DSL operation", node)
         if name == "scf.loop":
             raise _error("loop() is only valid as a for-loop iterator", node)
         return self.op(name, args, kwargs, node)
+
+    def inline(self, fn: Callable, args: list, kwargs: dict, node: ast.AST) -> Any:
+        """A call of a Python function from a kernel body: its body is walked in place,
+        with its parameters bound to the caller's values (memories, symbols, float
+        operands or plain Python values) and its own globals, so DSL programs can share
+        subroutines. The function may return a value with its last statement."""
+
+        if self.depth >= 32:
+            raise _error(f"{fn.__name__}: calls nest more than 32 deep", node)
+        try:
+            source = textwrap.dedent(inspect.getsource(fn))
+        except (OSError, TypeError):
+            raise _error(f"{fn.__name__}: no source to walk", node) from None
+        fdefs = [n for n in ast.parse(source).body if isinstance(n, ast.FunctionDef)]
+        if not fdefs:
+            raise _error(f"{fn.__name__}: not a function definition", node)
+        try:
+            bound = inspect.signature(fn).bind(*args, **kwargs)
+        except TypeError as exc:
+            raise _error(f"{fn.__name__}: {exc}", node) from None
+        bound.apply_defaults()
+        scope = dict(zip(fn.__code__.co_freevars, (c.cell_contents for c in (fn.__closure__ or ()))))
+        scope.update(bound.arguments)
+        body = fdefs[0].body
+        _check_returns(body, fdefs[0].name)
+        saved = self.scopes, self.globals
+        self.scopes, self.globals = [scope], fn.__globals__
+        self.depth += 1
+        try:
+            for st in body:
+                if isinstance(st, ast.Return):
+                    return None if st.value is None else self.ev(st.value)
+                self.exec_stmt(st)
+            return None
+        finally:
+            self.depth -= 1
+            self.scopes, self.globals = saved
 
     def mem(self, value: Any, what: str, node: ast.AST) -> Mem:
         if not isinstance(value, Mem):
@@ -477,24 +536,59 @@ class _Builder:
             mem = self.new_mem(self.syms(shape, node), src.dtype, src.space, "reshape", src)
             self.emit("dma.reshape", [src], {"shape": mem.shape}, mem)
             return mem
-        if name == "dma.slice":
+        if name in ("dma.slice", "dma.load"):
             source, offsets, sizes, strides, space = take(("source", "offsets", "sizes", "strides", "space"),
-                                                          {"space": MemorySpace.TSM})
-            src = self.mem(source, "slice source", node)
-            offsets, sizes, strides = (self.syms(v, node) for v in (offsets, sizes, strides))
-            self.check_rank(src, offsets, sizes, strides, name, node)
-            dst = self.new_mem(sizes, src.dtype, _space(space))
+                                                          {"strides": None, "space": None})
+            src = self.mem(source, f"{name[4:]} source", node)
+            offsets, sizes, strides = self.region(src, offsets, sizes, strides, name, node)
+            dst = self.new_mem(sizes, src.dtype, src.space if space is None else _space(space))
             self.emit("dma.alloc", [], {}, dst)
-            self.emit("dma.slice", [dst, src], {"offsets": offsets, "sizes": sizes, "strides": strides})
+            self.emit(name, [dst, src], {"offsets": offsets, "sizes": sizes, "strides": strides})
             return dst
-        if name == "dma.deslice":
-            target, source, offsets, sizes, strides = take(("target", "source", "offsets", "sizes", "strides"))
-            dst = self.mem(target, "deslice target", node)
-            src = self.mem(source, "deslice source", node)
-            offsets, sizes, strides = (self.syms(v, node) for v in (offsets, sizes, strides))
-            self.check_rank(dst, offsets, sizes, strides, name, node)
-            self.emit("dma.deslice", [dst, src], {"offsets": offsets, "sizes": sizes, "strides": strides})
+        if name in ("dma.deslice", "dma.store"):
+            target, source, offsets, sizes, strides = take(("target", "source", "offsets", "sizes", "strides"),
+                                                           {"strides": None})
+            dst = self.mem(target, f"{name[4:]} target", node)
+            src = self.mem(source, f"{name[4:]} source", node)
+            offsets, sizes, strides = self.region(dst, offsets, sizes, strides, name, node)
+            self.emit(name, [dst, src], {"offsets": offsets, "sizes": sizes, "strides": strides})
             return None
+        if name == "dma.copy":
+            source, space = take(("source", "space"), {"space": None})
+            src = self.mem(source, "copy source", node)
+            dst = self.new_mem(src.shape, src.dtype, src.space if space is None else _space(space))
+            self.emit("dma.alloc", [], {}, dst)
+            self.emit("dma.copy", [dst, src])
+            return dst
+        if name == "dma.cast":
+            source, dtype, space = take(("source", "dtype", "memoryspace"), {"memoryspace": None})
+            src = self.mem(source, "cast source", node)
+            dst = self.new_mem(src.shape, _element(dtype), src.space if space is None else _space(space))
+            self.emit("dma.alloc", [], {}, dst)
+            self.emit("dma.cast", [dst, src])
+            return dst
+        if name == "dma.free":
+            (value,) = take(("value",))
+            mem = self.mem(value, "free operand", node)
+            if mem.root().origin == "arg":
+                raise _error("dma.free: arguments are owned by the caller; free releases allocated tiles", node)
+            self.emit("dma.free", [mem])
+            return None
+        if name == "dma.flatten":
+            (source,) = take(("source",))
+            src = self.mem(source, "flatten source", node)
+            count = Sym.const(1)
+            for d in src.shape:
+                count = count * d
+            mem = self.new_mem((count,), src.dtype, src.space, "reshape", src)
+            self.emit("dma.reshape", [src], {"shape": mem.shape}, mem)
+            return mem
+        if name.startswith("arch.get_"):
+            take(())
+            query = name[len("arch.get_"):]
+            if query not in HW_QUERIES:
+                raise _error(f"{name} is not a launch query", node)
+            return Sym.hw(query)
         if name == "dma.broadcast":
             target, source = take(("target", "source"))
             self.emit("dma.broadcast", [self.mem(target, "broadcast target", node), self.mem(source, "broadcast source", node)])
@@ -574,9 +668,30 @@ class _Builder:
             raise _error(f"fill value must be a number or a float argument, got {value!r}", node)
         return FVal(value=float(value))
 
+    def region(self, mem: Mem, offsets, sizes, strides, name: str, node: ast.AST):
+        """offsets / sizes / strides of a region of `mem` (strides default to 1)."""
+
+        if strides is None:
+            strides = [1] * len(sizes)
+        offsets, sizes, strides = (self.syms(v, node) for v in (offsets, sizes, strides))
+        self.check_rank(mem, offsets, sizes, strides, name, node)
+        return offsets, sizes, strides
+
     def check_rank(self, mem: Mem, offsets, sizes, strides, name: str, node: ast.AST) -> None:
         if not (len(offsets) == len(sizes) == len(strides) == mem.rank):
             raise _error(f"{name}: offsets/sizes/strides must have rank {mem.rank}", node)
+
+
+def _check_returns(body: list[ast.stmt], name: str) -> None:
+    """A DSL function returns only from its last top-level statement: a return inside a
+    loop or a branch would end the walk of that block, not the run-time execution."""
+
+    for i, st in enumerate(body):
+        nested = [n for n in ast.walk(st) if isinstance(n, ast.Return)]
+        if isinstance(st, ast.Return):
+            nested = nested[1:] if i == len(body) - 1 else nested
+        if nested:
+            raise _error(f"{name}: return is allowed only as the last statement of the function", nested[0])
 
 
 @dataclass(frozen=True)
@@ -590,7 +705,56 @@ class _Not:
 def mlir_gen(func_obj: Callable, runtime_args: Sequence[Any]) -> Func:
     """The gfx950 IR of ``func_obj`` specialised to the kinds of ``runtime_args``."""
 
-    func = _Builder(func_obj, runtime_args).run()
+    return _finish(_Builder.of_function(func_obj, runtime_args).run())
+
+
+# The reference's DSL modules and the modules of this package that provide the same names.
+REFERENCE_MODULES = {
+    "kernel_gen.operation": "kernelcode_generate_amd.operation",
+    "kernel_gen.operation.arch": "kernelcode_generate_amd.operation.arch",
+    "kernel_gen.operation.dma": "kernelcode_generate_amd.operation.dma",
+    "kernel_gen.operation.kernel": "kernelcode_generate_amd.operation.kernel",
+    "kernel_gen.operation.nn": "kernelcode_generate_amd.operation.nn",
+    "kernel_gen.operation.scf": "kernelcode_generate_amd.operation.scf",
+    "kernel_gen.symbol_variable.memory": "kernelcode_generate_amd.symbol_variable",
+    "kernel_gen.symbol_variable.type": "kernelcode_generate_amd.symbol_variable",
+    "kernel_gen.symbol_variable.symbol_dim": "kernelcode_generate_amd.symbol_variable",
+}
+
+
+def source_namespace(source: str, constants: dict | None = None) -> dict:
+    """Globals for walking a DSL module given as text, without running it: the names its
+    `from kernel_gen... import ...` statements bind, taken from this package's modules of
+    the same role (REFERENCE_MODULES), plus ``constants`` for the module-level values its
+    kernels read (tile sizes, pads, seeds' draws). Other imports are left out: a kernel
+    body that used them fails with a name error."""
+
+    import importlib
+
+    namespace: dict = dict(constants or {})
+    for node in ast.parse(source).body:
+        if isinstance(node, ast.ImportFrom) and node.module in REFERENCE_MODULES:
+            module = importlib.import_module(REFERENCE_MODULES[node.module])
+            for alias in node.names:
+                if hasattr(module, alias.name):
+                    namespace[alias.asname or alias.name] = getattr(module, alias.name)
+                elif alias.name in ("kernel", "dma", "nn", "scf", "arch"):
+                    namespace[alias.asname or alias.name] = importlib.import_module(f"{module.__name__}.{alias.name}")
+    return namespace
+
+
+def mlir_gen_source(source: str, function: str, runtime_args: Sequence[Any], constants: dict | None = None) -> Func:
+    """The gfx950 IR of the DSL function ``function`` defined in the module text
+    ``source`` (walked, never executed), specialised to the kinds of ``runtime_args``;
+    names resolve through ``source_namespace(source, constants)``."""
+
+    fdefs = [n for n in ast.parse(source).body if isinstance(n, ast.FunctionDef) and n.name == function]
+    if not fdefs:
+        raise _error(f"no function {function!r} in the source")
+    return _finish(_Builder(fdefs[0], source_namespace(source, constants), {}, runtime_args).run())
+
+
+def _finish(func: Func) -> Func:
     for op in func.walk():
         if op.name == "scf.if" and isinstance(op.attrs["cond"], _Not):
             op.attrs["cond"] = op.attrs["cond"].inner
@@ -598,4 +762,4 @@ def mlir_gen(func_obj: Callable, runtime_args: Sequence[Any]) -> Func:
     return func
 
 
-__all__ = ["mlir_gen"]
+__all__ = ["REFERENCE_MODULES", "mlir_gen", "mlir_gen_source", "source_namespace"]

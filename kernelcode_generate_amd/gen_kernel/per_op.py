@@ -38,6 +38,20 @@ ENUM_LIMIT = 4_000_000
 MAX_GRID = 2048
 SCRATCH_BYTES = 32 << 20  # scratch of the allocation-free entry, per GPU
 MAX_DEVICES = 64
+QUERY_GRID = 256  # workgroups of a kernel that distributes work with arch.get_block_id / get_block_num
+
+# Launch queries. Each workgroup is one DSL block; the operations of its body are executed
+# cooperatively by the workgroup's lanes, so a block runs one DSL thread (thread and
+# subthread ids are 0 and their counts 1, as on the reference's npu_demo target, whose
+# thread_num is 1: kernel_gen/target/targets/npu_demo.txt).
+HW_DEVICE = {"block_id": "((long long)blockIdx.x)", "block_num": "((long long)gridDim.x)", "thread_id": "0LL",
+             "thread_num": "1LL", "subthread_id": "0LL", "subthread_num": "1LL"}
+# On the host (workspace bounds) the block id ranges over the grid: hw_block_id is the
+# enumeration variable of the bound's outermost loop.
+_BLOCK_ID = Sym.hw("block_id")
+_HOST_BLOCK_IV = "__hw_block_id"
+HW_HOST = {"block_id": "hw_block_id", "block_num": f"{QUERY_GRID}LL", "thread_id": "0LL", "thread_num": "1LL",
+           "subthread_id": "0LL", "subthread_num": "1LL"}
 
 
 @dataclass
@@ -53,10 +67,32 @@ def _significant(block: list[Op]) -> list[Op]:
     return [op for op in block if op.name not in ("dma.alloc", "dma.view", "dma.reshape")]
 
 
+def _syms_of(func: Func):
+    for op in func.walk():
+        for value in op.attrs.values():
+            for x in (value if isinstance(value, (list, tuple)) else (value,)):
+                if isinstance(x, Sym):
+                    yield x
+                elif isinstance(x, Cmp):
+                    yield x.a
+                    yield x.b
+        for mem in op.operands + ([op.result] if op.result is not None else []):
+            yield from mem.shape
+
+
+def uses_block_queries(func: Func) -> bool:
+    """The kernel distributes work itself with arch.get_block_id / get_block_num."""
+
+    return any(s.leaves("hw") & {"block_id", "block_num"} for s in _syms_of(func))
+
+
 def parallel_loops(func: Func) -> list[Op]:
     """arch-parallelize: the leading perfectly nested loops whose bounds use no index of
-    the loops around them."""
+    the loops around them. A kernel that queries its block id or block count is left as
+    written (the reference pass skips such functions: arch_parallelize.py:186-206)."""
 
+    if uses_block_queries(func):
+        return []
     chosen: list[Op] = []
     block = func.body
     while len(block) == 1 and block[0].name == "symbol.for":
@@ -103,6 +139,8 @@ class _Emitter:
             return f"a.i_{s.args[0]}"
         if s.op == "dim":
             return f"a.s_{s.args[0]}[{s.args[1]}]"
+        if s.op == "hw":
+            return HW_DEVICE[s.args[0]]
         return f"iv_{s.args[0]}"
 
     def host_leaf(self, s: Sym) -> str:
@@ -110,6 +148,8 @@ class _Emitter:
             return f"a.i_{s.args[0]}"
         if s.op == "dim":
             return f"a.s_{s.args[0]}[{s.args[1]}]"
+        if s.op == "hw":
+            return HW_HOST[s.args[0]]
         return f"iv_{s.args[0]}"
 
     def dev(self, s: Sym) -> str:
@@ -198,19 +238,26 @@ class _Emitter:
         if n == "dma.fill":
             L(f"{ind}kg_tile::fill({self.var(op.operands[0])}, {self.fval(op.attrs['value'])});")
             return
-        if n in ("dma.deslice", "dma.slice"):
+        if n in ("dma.deslice", "dma.slice", "dma.store", "dma.load"):
             dst, src = op.operands
             a = op.attrs
-            region_of = dst if n == "dma.deslice" else src
+            region_of = dst if n in ("dma.deslice", "dma.store") else src
             vt = self.vtype(region_of)
             L(f"{ind}{{")
             L(f"{ind}  {self.arr('o_', a['offsets'])} {self.arr('z_', a['sizes'])} {self.arr('s_', a['strides'])}")
             L(f"{ind}  const {vt} r_ = kg_tile::subview({self.var(region_of)}, o_, z_, s_, {err});")
-            if n == "dma.deslice":
+            if n in ("dma.deslice", "dma.store"):
                 L(f"{ind}  kg_tile::copy(r_, {self.var(src)}, {err});")
             else:
                 L(f"{ind}  kg_tile::copy({self.var(dst)}, r_, {err});")
             L(f"{ind}}}")
+            return
+        if n in ("dma.copy", "dma.cast"):
+            # whole-tile copy; a cast rounds each element to the target type (to nearest even)
+            L(f"{ind}kg_tile::copy({self.var(op.operands[0])}, {self.var(op.operands[1])}, {err});")
+            return
+        if n == "dma.free":
+            L(f"{ind}// dma.free({self.var(op.operands[0])}): workspace tiles live for the whole launch")
             return
         if n == "dma.broadcast":
             L(f"{ind}kg_tile::broadcast({self.var(op.operands[0])}, {self.var(op.operands[1])}, {err});")
@@ -276,21 +323,31 @@ class _Emitter:
         return order
 
     def interval_ub(self, e: Sym) -> Sym:
-        def rng(iv: str):
-            loop = self.plan.loops[iv]
-            return loop.attrs["start"], loop.attrs["end"] - 1
+        block = Sym.iv(_HOST_BLOCK_IV)
 
-        return interval(e, rng)[1]
+        def rng(iv: str):
+            if iv == _HOST_BLOCK_IV:
+                return Sym.const(0), Sym.const(QUERY_GRID - 1)
+            loop = self.plan.loops[iv]
+            return (loop.attrs["start"].substitute({_BLOCK_ID: block}),
+                    (loop.attrs["end"] - 1).substitute({_BLOCK_ID: block}))
+
+        return interval(e.substitute({_BLOCK_ID: block}), rng)[1]
 
     def host_bound(self, e: Sym, name: str, ind: str) -> list[str]:
         out = [f"{ind}long long {name} = 0;"]
         ivs = e.ivs()
-        if not ivs:
-            return [f"{ind}long long {name} = {self.host(e)};"]
         order = self.closure(ivs)
+        per_block = "block_id" in e.leaves("hw") or any(
+            "block_id" in self.plan.loops[iv].attrs[k].leaves("hw") for iv in order for k in ("start", "end", "step"))
+        if not ivs and not per_block:
+            return [f"{ind}long long {name} = {self.host(e)};"]
         out.append(f"{ind}{{")
         out.append(f"{ind}  long long steps = 0;")
         depth = ind + "  "
+        if per_block:
+            out.append(f"{depth}for (long long hw_block_id = 0; hw_block_id < {QUERY_GRID}LL; ++hw_block_id) {{")
+            depth += "  "
         for iv in order:
             loop = self.plan.loops[iv]
             st = self.host(loop.attrs["step"])
@@ -299,7 +356,7 @@ class _Emitter:
             depth += "  "
         out.append(f"{depth}if (++steps > {ENUM_LIMIT}LL) {{ {name} = {self.host(self.interval_ub(e))}; goto done_{name}; }}")
         out.append(f"{depth}{name} = kg_tile::kg_max({name}, {self.host(e)});")
-        for _ in order:
+        for _ in range(len(order) + (1 if per_block else 0)):
             depth = depth[:-2]
             out.append(f"{depth}}}")
         out.append(f"{ind}}}")
@@ -362,6 +419,9 @@ class _Emitter:
                          f"{self.dev(loop.attrs['step'])};")
                 L.append(f"    rem /= tr_{iv};")
             L.append("    (void)rem;")
+            ind = "    "
+        elif uses_block_queries(f):
+            L.append("  {  // every workgroup runs the body: the kernel distributes its work by block id")
             ind = "    "
         else:
             L.append("  if (blockIdx.x == 0) {")
@@ -454,6 +514,8 @@ class _Emitter:
                 f"kg_tile::kg_trips({self.host(l.attrs['start'])}, {self.host(l.attrs['end'])}, {self.host(l.attrs['step'])})"
                 for l in par)
             L.append(f"  const long long total = {trips};")
+        elif uses_block_queries(f):
+            L.append(f"  const long long total = {QUERY_GRID};  // arch.get_block_num() of the launch")
         else:
             L.append("  const long long total = 1;")
         L.append("  if (total <= 0) return kg_gfx950_finish_launch(\"" + function + "(empty)\");")
@@ -470,7 +532,9 @@ class _Emitter:
             "      return kg_gfx950_fail(-3, msg);",
             "    }",
             "    const long long fit = (kScratchBytes - 256) / (a.ws_per_block > 0 ? a.ws_per_block : 1);",
-            "    if (grid > fit) grid = fit;",
+            ("    if (grid > fit) grid = fit;" if not uses_block_queries(f) else
+             f'    if (grid > fit) return kg_gfx950_fail(-3, "{function}: the {QUERY_GRID} workgroups the kernel\'s '
+             f'block queries assume do not fit the scratch of the allocation-free entry");'),
             "    if (scratch_of_current_device(&ws) != 0) return -2;",
             "  } else {",
             "    const size_t bytes = (size_t)(grid * a.ws_per_block) + 256;",

@@ -4,9 +4,11 @@ The reference's DSL keeps shapes, tile sizes and loop indices as `symbol` dialec
 (kernel_gen/dialect/symbol; `symbol.for` induction variables, `min(tile, size - i)` tail
 extents, kernel_gen/symbol_variable/symbol_dim.py). Here they are immutable expression
 trees over five leaves -- integer constants, INT runtime arguments, dimensions of memory
-arguments, loop induction variables and the `i`-th lane of nothing else -- combined with
-+, -, *, floor division, modulo, min and max (Python semantics: `//` and `%` round toward
-negative infinity, as the DSL's Python source means them).
+arguments, loop induction variables and the launch queries of the `arch` operations
+(`hw` leaves: block_id, block_num, thread_id, thread_num, subthread_id, subthread_num;
+kernel_gen/operation/arch.py:652-776) -- combined with +, -, *, floor division, modulo,
+min and max (Python semantics: `//` and `%` round toward negative infinity, as the DSL's
+Python source means them).
 
 An expression can be evaluated (runtime values for its leaves), rendered as C++ for the
 generated entry and device code, and bounded over the iteration space of its loops
@@ -19,11 +21,12 @@ from dataclasses import dataclass
 from typing import Callable, Mapping
 
 _BIN = ("add", "sub", "mul", "floordiv", "mod", "min", "max")
+HW_QUERIES = ("block_id", "block_num", "thread_id", "thread_num", "subthread_id", "subthread_num")
 
 
 @dataclass(frozen=True)
 class Sym:
-    op: str                 # const | arg | dim | iv | add | sub | mul | floordiv | mod | min | max
+    op: str                 # const | arg | dim | iv | hw | add | sub | mul | floordiv | mod | min | max
     args: tuple = ()
 
     # -- construction ------------------------------------------------------------------
@@ -42,6 +45,12 @@ class Sym:
     @staticmethod
     def iv(name: str) -> "Sym":
         return Sym("iv", (name,))
+
+    @staticmethod
+    def hw(name: str) -> "Sym":
+        if name not in HW_QUERIES:
+            raise ValueError(f"unknown launch query {name!r}")
+        return Sym("hw", (name,))
 
     @property
     def is_const(self) -> bool:
@@ -109,7 +118,7 @@ class Sym:
 
         if self.op == "const":
             return self.args[0]
-        if self.op in ("arg", "dim", "iv"):
+        if self.op in ("arg", "dim", "iv", "hw"):
             return int(env(self))
         a = self.args[0].evaluate(env)
         b = self.args[1].evaluate(env)
@@ -124,6 +133,8 @@ class Sym:
             return f"{self.args[0]}.shape[{self.args[1]}]"
         if self.op == "iv":
             return self.args[0]
+        if self.op == "hw":
+            return f"arch.get_{self.args[0]}()"
         a, b = self.args
         if self.op in ("min", "max"):
             return f"{self.op}({a}, {b})"
@@ -135,7 +146,7 @@ class Sym:
 
         if self.op == "const":
             return f"{self.args[0]}LL"
-        if self.op in ("arg", "dim", "iv"):
+        if self.op in ("arg", "dim", "iv", "hw"):
             return leaf(self)
         a = self.args[0].to_c(leaf)
         b = self.args[1].to_c(leaf)
@@ -246,7 +257,7 @@ def interval(expr: Sym, iv_range: Callable[[str], tuple[Sym, Sym]]) -> tuple[Sym
     arguments and dimensions. Division and modulo need a positive divisor (strides,
     tiles), which the front end requires of every loop step."""
 
-    if expr.op in ("const", "arg", "dim"):
+    if expr.op in ("const", "arg", "dim", "hw"):
         return expr, expr
     if expr.op == "iv":
         first, last = iv_range(expr.args[0])

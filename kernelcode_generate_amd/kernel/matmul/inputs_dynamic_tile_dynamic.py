@@ -1,13 +1,11 @@
-"""Matmul demo, runtime shapes and runtime tiles (kernel/matmul/inputs_dynamic_tile_dynamic.py:
-57-113 of the reference): the static demo's program with tile_h / tile_w / tile_k as INT
-parameters."""
+"""Matmul demo, runtime shapes and tiles (the reference's
+kernel/matmul/inputs_dynamic_tile_dynamic.py:57-113): `tiled_matmul` with the tile sizes as
+INT parameters."""
 
 from __future__ import annotations
 
-from kernelcode_generate_amd.operation import kernel
-from kernelcode_generate_amd.operation.dma import alloc, broadcast, deslice, fill, reshape, view
-from kernelcode_generate_amd.operation.scf import loop
-from kernelcode_generate_amd.symbol_variable import MemorySpace, NumericType, SymbolDim
+from kernelcode_generate_amd.kernel.matmul.tiled import tiled_matmul
+from kernelcode_generate_amd.symbol_variable import SymbolDim
 
 
 def matmul_inputs_dynamic_tile_dynamic_kernel(
@@ -19,36 +17,4 @@ def matmul_inputs_dynamic_tile_dynamic_kernel(
     tile_w: SymbolDim,
     tile_k: SymbolDim,
 ) -> None:
-    h_size = lhs.get_shape()[0]
-    k_size = lhs.get_shape()[1]
-    w_size = rhs.get_shape()[1]
-    for h0 in loop(0, h_size, tile_h):
-        for w0 in loop(0, w_size, tile_w):
-            cur_h = min(tile_h, h_size - h0)
-            cur_w = min(tile_w, w_size - w0)
-            acc = alloc([cur_h, cur_w], NumericType.Float32, MemorySpace.TSM)
-            fill(acc, 0)
-            bias_tile = alloc([cur_w], NumericType.Float32, MemorySpace.TSM)
-            fill(bias_tile, 0)
-            bias_row = reshape(bias_tile, [1, cur_w])
-            bias_full = alloc([cur_h, cur_w], NumericType.Float32, MemorySpace.TSM)
-            for k0 in loop(0, k_size, tile_k):
-                cur_k = min(tile_k, k_size - k0)
-                lhs_tile = alloc([cur_h, cur_k], NumericType.Float32, MemorySpace.TSM)
-                rhs_tile = alloc([cur_k, cur_w], NumericType.Float32, MemorySpace.TSM)
-                fill(lhs_tile, 0)
-                fill(rhs_tile, 0)
-                lhs_region = view(lhs, [h0, k0], [cur_h, cur_k], [1, 1])
-                rhs_region = view(rhs, [k0, w0], [cur_k, cur_w], [1, 1])
-                deslice(lhs_tile, lhs_region, [0, 0], [cur_h, cur_k], [1, 1])
-                deslice(rhs_tile, rhs_region, [0, 0], [cur_k, cur_w], [1, 1])
-                partial = alloc([cur_h, cur_w], NumericType.Float32, MemorySpace.TSM)
-                kernel.matmul(partial, lhs_tile, rhs_tile)
-                kernel.add(acc, acc, partial)
-            if bias is not None:
-                bias_region = view(bias, [w0], [cur_w], [1])
-                deslice(bias_tile, bias_region, [0], [cur_w], [1])
-                broadcast(bias_full, bias_row)
-                kernel.add(acc, acc, bias_full)
-            out_region = view(acc, [0, 0], [cur_h, cur_w], [1, 1])
-            deslice(out, out_region, [h0, w0], [cur_h, cur_w], [1, 1])
+    tiled_matmul(out, lhs, rhs, bias, tile_h, tile_w, tile_k)

@@ -1,5 +1,5 @@
-"""DSL operations (the reference's kernel_gen.operation): `kernel`, `dma`, `nn`, `scf`."""
+"""DSL operations (the reference's kernel_gen.operation): `arch`, `dma`, `kernel`, `nn`, `scf`."""
 
-from . import dma, kernel, nn, scf
+from . import arch, dma, kernel, nn, scf
 
-__all__ = ["dma", "kernel", "nn", "scf"]
+__all__ = ["arch", "dma", "kernel", "nn", "scf"]

@@ -33,6 +33,8 @@ class _Env:
             else:
                 self.vals[p.name] = a
         self.ivs: dict[str, int] = {}
+        self.hw = {"block_id": 0, "block_num": 1, "thread_id": 0, "thread_num": 1, "subthread_id": 0,
+                   "subthread_num": 1}
 
     def sym(self, s: Sym) -> int:
         def leaf(x: Sym) -> int:
@@ -41,6 +43,8 @@ class _Env:
             if x.op == "dim":
                 a = self.vals[x.args[0]]
                 return int(a.shape[x.args[1]]) if a is not None else 0
+            if x.op == "hw":
+                return self.hw[x.args[0]]
             return self.ivs[x.args[0]]
 
         return s.evaluate(leaf)
@@ -69,6 +73,16 @@ def _region(arr: np.ndarray, offsets, sizes, steps) -> np.ndarray:
 
 def _store(dst: np.ndarray, values: np.ndarray) -> None:
     dst[...] = values.astype(dst.dtype, copy=False).reshape(dst.shape)
+
+
+def bf16_round(values: np.ndarray) -> np.ndarray:
+    """float32 values rounded to bfloat16 (to nearest even), kept as float32."""
+
+    u = np.ascontiguousarray(values, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = np.where(nan, u | 0x400000, r)
+    return r.astype(np.uint32).view(np.float32)
 
 
 def _run(block: list[Op], env: _Env) -> None:
@@ -105,11 +119,18 @@ def _run(block: list[Op], env: _Env) -> None:
         mems = [env.mems[id(m)] for m in op.operands]
         if n == "dma.fill":
             mems[0][...] = env.fval(a["value"])
-        elif n == "dma.deslice":
+        elif n in ("dma.copy", "dma.cast"):
+            v = mems[1].astype(np.float32)
+            if n == "dma.cast" and op.operands[0].dtype == "bf16":
+                v = bf16_round(v)
+            _store(mems[0], v)
+        elif n == "dma.free":
+            pass
+        elif n in ("dma.deslice", "dma.store"):
             region = _region(mems[0], [env.sym(x) for x in a["offsets"]], [env.sym(x) for x in a["sizes"]],
                              [env.sym(x) for x in a["strides"]])
             _store(region, mems[1])
-        elif n == "dma.slice":
+        elif n in ("dma.slice", "dma.load"):
             region = _region(mems[1], [env.sym(x) for x in a["offsets"]], [env.sym(x) for x in a["sizes"]],
                              [env.sym(x) for x in a["strides"]])
             _store(mems[0], region)
@@ -167,8 +188,13 @@ def _run(block: list[Op], env: _Env) -> None:
             raise NotImplementedError(n)
 
 
-def run(func: Func, args: tuple) -> None:
-    """Execute ``func`` on host arrays (memory args are written in place)."""
+def run(func: Func, args: tuple, blocks: int = 1) -> None:
+    """Execute ``func`` on host arrays (memory args are written in place): once, or, for a
+    kernel that distributes its work with the launch queries, once per block of a launch of
+    ``blocks`` blocks."""
 
     with np.errstate(invalid="ignore", over="ignore"):
-        _run(func.body, _Env(func, args))
+        for b in range(blocks):
+            env = _Env(func, args)
+            env.hw.update(block_id=b, block_num=blocks)
+            _run(func.body, env)

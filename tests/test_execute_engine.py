@@ -283,3 +283,21 @@ def test_memory_stage_slot_validated_without_gpu():
         with pytest.raises(native.NativeLibraryError, match="memory_stage"):
             native.cost("matmul", base + [bad])
     assert lib is not None
+
+
+def test_real_hipcc_builds_every_demo_per_operation():
+    """The per-operation kernels of the matmul and conv demo programs (loads, stores, frees,
+    reshaped accumulators, img2col) cross-compile too."""
+
+    import numpy as np
+
+    a = np.zeros((4, 4), np.float32)
+    x = np.zeros((1, 2, 6, 6), np.float32)
+    w = np.zeros((2, 2, 3, 3), np.float32)
+    for fn, args in ((matmul_inputs_static_tile_dynamic_kernel, (a, a, a, a[0], 4, 4, 4)),
+                     (conv2d_inputs_dynamic_tile_dynamic_kernel, (x, x, w, None, 1, 1, 1, 1, 1, 1, 1, 1, 2, 2, 1, 3, 3))):
+        kernel = ExecutionEngine("gfx950").compile(source=gen_kernel(lower(fn, *args, fuse="false")), function="demo")
+        try:
+            assert hasattr(ctypes.CDLL(kernel.soname_path), "kg_execute_entry")
+        finally:
+            kernel.close()
