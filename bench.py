@@ -37,7 +37,6 @@ import json
 import math
 import os
 import re
-import statistics
 import sys
 import time
 from pathlib import Path
@@ -73,6 +72,48 @@ class PreparedCall:
         rc = self.fn(self.slots, self.count)
         if rc != 0:
             raise RuntimeError(f"{self.entry} returned {rc}: {self.lib.kg_gfx950_last_error().decode()}")
+
+
+PROBE_LIBRARY = REPO_ROOT / "kernelcode_generate_amd" / "libkg_gfx950_probe.so"
+_PROBE = None
+
+
+def probe_library():
+    """bench.py's measurement library (built next to libkg_gfx950.so by build()), loaded
+    after the product library so that both use torch's HIP runtime."""
+
+    global _PROBE
+    if _PROBE is None:
+        import ctypes
+
+        from kernelcode_generate_amd import native
+
+        native.load_library()
+        if not PROBE_LIBRARY.is_file():
+            raise RuntimeError(f"{PROBE_LIBRARY} is missing: build it with __graft_entry__.build()")
+        lib = ctypes.CDLL(str(PROBE_LIBRARY))
+        lib.kg_gfx950_probe_mfma_rate.argtypes = [ctypes.c_int] * 5 + [ctypes.POINTER(ctypes.c_double)] * 2
+        lib.kg_gfx950_probe_mfma_rate.restype = ctypes.c_int
+        lib.kg_gfx950_probe_last_error.restype = ctypes.c_char_p
+        _PROBE = lib
+    return _PROBE
+
+
+def mfma_rate(dtype: str = "bf16", zero_operands: bool = False, iterations: int = 20000, workgroups: int = 2048,
+              mfma_m: int = 16) -> dict:
+    """Sustained rate of v_mfma_f32_16x16x32 (mfma_m=16) or v_mfma_f32_32x32x16 (mfma_m=32)
+    on register operands, N(0,1)*0.02 or zeros (the probe library's kg_gfx950_probe_mfma_rate)."""
+
+    import ctypes
+
+    lib = probe_library()
+    tf, ghz = ctypes.c_double(0.0), ctypes.c_double(0.0)
+    code = {"bf16": 6, "f16": 5}[dtype]
+    rc = lib.kg_gfx950_probe_mfma_rate(code, int(mfma_m), int(bool(zero_operands)), int(iterations), int(workgroups),
+                                       ctypes.byref(tf), ctypes.byref(ghz))
+    if rc != 0:
+        raise RuntimeError(f"kg_gfx950_probe_mfma_rate failed ({rc}): {lib.kg_gfx950_probe_last_error().decode()}")
+    return {"tflops": tf.value, "clock_ghz": ghz.value}
 
 
 def time_steps(call: PreparedCall, steps: int, warmup: int, min_warmup_s: float = 0.0):
@@ -114,21 +155,12 @@ def read_traffic(path: Path):
     return float(m.group(1)) if m else None
 
 
-# "zeros": analysis mode (--only runs): the GEMM lines run on all-zero operands. The kernel,
-# its instruction stream and its memory traffic are unchanged; only the switching activity of
-# the data, and with it the power the part draws and the clock it holds, differ.
-GEMM_OPERANDS = ["random"]
-
-
 def gemm_workload(dev, m: int, n: int, k: int, seed: int):
     import torch
 
     g = torch.Generator(device=dev).manual_seed(seed)
     a = (torch.randn(m, k, generator=g, device=dev) * 0.02).to(torch.bfloat16)
     b = (torch.randn(k, n, generator=g, device=dev) * 0.02).to(torch.bfloat16)
-    if GEMM_OPERANDS[0] == "zeros":
-        a.zero_()
-        b.zero_()
     c = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
     return a, b, c
 
@@ -316,14 +348,13 @@ def c1(dev, add, steps):
 
 def c2(dev, add, steps):
     a, b, c = gemm_workload(dev, 4096, 4096, 4096, 20261202)
-    add("C2 bf16 matmul M=N=K=4096" + ("" if GEMM_OPERANDS[0] == "random" else " (zero operands)"), 2 * 4096**3, PreparedCall("kg_gfx950_matmul_entry", (c, a, b, None)),
+    add("C2 bf16 matmul M=N=K=4096", 2 * 4096**3, PreparedCall("kg_gfx950_matmul_entry", (c, a, b, None)),
         PEAK_BF16_TFLOPS, max(steps, 200))
 
 
 def c2s(dev, add, steps):
     a, b, c = gemm_workload(dev, 8192, 1024, 4096, 20261203)
-    add("C2' bf16 matmul M=8192 N=1024 K=4096" + ("" if GEMM_OPERANDS[0] == "random" else " (zero operands)"),
-        2 * 8192 * 1024 * 4096,
+    add("C2' bf16 matmul M=8192 N=1024 K=4096", 2 * 8192 * 1024 * 4096,
         PreparedCall("kg_gfx950_matmul_entry", (c, a, b, None)), PEAK_BF16_TFLOPS, max(steps, 200))
 
 
@@ -398,14 +429,6 @@ def main() -> int:
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--only", nargs="+", choices=PROFILE_KEYS,
                     help="profiling aid: run only these secondary workloads (no headline GEMM, no CPU baseline)")
-    ap.add_argument("--operands", choices=("random", "zeros"), default="random",
-                    help="with --only: run the GEMM lines on all-zero operands (power/clock analysis)")
-    ap.add_argument("--mfma-ceiling", action="store_true",
-                    help="analysis mode: the sustained MFMA rate with no operand movement, random and zero bf16 "
-                         "operands (kg_gfx950_mfma_rate), as one JSON line")
-    ap.add_argument("--vs-library", action="store_true",
-                    help="analysis mode: the C2 GEMM and torch.matmul (hipBLASLt) on the same operands, timed in "
-                         "alternating blocks in one process, as one JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (reference point for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -417,11 +440,6 @@ def main() -> int:
         )
         return 2
 
-    if args.operands != "random" and not args.only:
-        print("--operands zeros is an analysis mode for --only runs; the headline uses random operands", file=sys.stderr)
-        return 2
-    GEMM_OPERANDS[0] = args.operands
-
     import torch
 
     from kernelcode_generate_amd import native
@@ -430,39 +448,6 @@ def main() -> int:
     native.load_library()
     stream = torch.cuda.current_stream()
     native.set_launch_mode(False, stream.cuda_stream)
-    if args.mfma_ceiling:
-        rates = {}
-        for shape, mfma_m in (("16x16x32", 16), ("32x32x16", 32)):
-            for zeros in (False, True):
-                r = native.mfma_rate("bf16", zeros, mfma_m=mfma_m)
-                key = f"{shape}_{'zero' if zeros else 'random'}_operands"
-                rates[key] = {"tflops": round(r["tflops"], 1), "clock_ghz": round(r["clock_ghz"], 3),
-                              "frac_of_peak": round(r["tflops"] / PEAK_BF16_TFLOPS, 4)}
-                log(f"[bench] mfma ceiling, bf16 {key}: {r['tflops']:.1f} TFLOP/s at {r['clock_ghz']:.3f} GHz")
-        print(json.dumps({"mfma_ceiling": rates, "peak": PEAK_BF16_TFLOPS,
-                          "kernel": "back-to-back v_mfma_f32_{16x16x32,32x32x16}_bf16 on register operands, "
-                                    "2048 workgroups x 4 waves"}),
-              flush=True)
-        native.set_launch_mode(True, None)
-        return 0
-    if args.vs_library:
-        a, b, c = gemm_workload(dev, 4096, 4096, 4096, 20261202)
-        flop = 2.0 * 4096 ** 3
-        calls = {"ours": PreparedCall("kg_gfx950_matmul_entry", (c, a, b, None)),
-                 "hipblaslt": lambda: torch.matmul(a, b, out=c)}
-        rates = {name: [] for name in calls}
-        torch.cuda.synchronize()
-        for rnd in range(3):  # alternating blocks: both see the same clock and temperature drift
-            for name, fn in calls.items():
-                _, ev_ms, _ = time_steps(fn, args.steps, 20, SECONDARY_WARMUP_S)
-                rates[name].append(flop / (ev_ms * 1e-3) / 1e12)
-                log(f"[bench] round {rnd} {name}: {ev_ms * 1e3:.1f} us {rates[name][-1]:.1f} TFLOP/s")
-        print(json.dumps({"vs_library": {name: {"tflops_median": round(statistics.median(v), 1),
-                                                 "tflops_rounds": [round(x, 1) for x in v]}
-                                          for name, v in rates.items()},
-                          "workload": "bf16 4096^3, A,B ~ N(0,1)*0.02", "peak": PEAK_BF16_TFLOPS}), flush=True)
-        native.set_launch_mode(True, None)
-        return 0
     if args.only:
         print(json.dumps({"secondary": secondary(dev, args.steps, args.warmup, args.only)}), flush=True)
         native.set_launch_mode(True, None)
@@ -510,11 +495,11 @@ def main() -> int:
     del a, b, c
     # the part's sustained matrix-core rate on this data (random bf16, no operand movement):
     # the power-limited ceiling the headline's fraction is read against
-    ceiling = native.mfma_rate("bf16", False, mfma_m=16)
+    ceiling = mfma_rate("bf16", False, mfma_m=16)
     result["roofline"]["mfma_ceiling"] = {
         "tflops": round(ceiling["tflops"], 1), "clock_ghz": round(ceiling["clock_ghz"], 3),
         "what": "back-to-back v_mfma_f32_16x16x32_bf16 (the headline kernel's instruction) on N(0,1)*0.02 "
-                "register operands (kg_gfx950_mfma_rate)"}
+                "register operands (the probe library's kg_gfx950_probe_mfma_rate)"}
     result["roofline"]["frac_of_mfma_ceiling"] = round(achieved / ceiling["tflops"], 4)
     log(f"[bench] mfma ceiling (random bf16 operands): {ceiling['tflops']:.1f} TFLOP/s at {ceiling['clock_ghz']:.3f} GHz; "
         f"headline {achieved / ceiling['tflops']:.3f} of it")

@@ -143,22 +143,10 @@ int kg_gfx950_finish_launch(const char* what);
 const char* kg_gfx950_last_error(void);
 
 /* ABI revision of this library (bumped on any change of a declaration here or of the slot
- * contract). 2: kg_gfx950_cost writes five kinds (KG_COST_MFMA_CYCLES added);
- * kg_gfx950_mfma_rate takes the MFMA shape. */
+ * contract). 2: kg_gfx950_cost writes five kinds (KG_COST_MFMA_CYCLES added). 3: the
+ * measurement aid kg_gfx950_mfma_rate left the library (bench.py's probe library has it);
+ * memory_stage slots on the attention (slot 8) and conv2d (slot 17) entries. */
 int kg_gfx950_abi_version(void);
-
-/*
- * Measurement aid (no counterpart in the reference): the sustained rate of
- * v_mfma_f32_32x32x16_{bf16,f16} (mfma_m = 32) or v_mfma_f32_16x16x32_{bf16,f16} (mfma_m = 16)
- * with no operand movement. `workgroups` workgroups of 4 waves each load 8 operand registers
- * once (N(0,1)*0.02 values, or zeros when zero_operands != 0) and issue `iterations` x 8
- * back-to-back MFMAs into 8 accumulators; after two untimed launches one launch is timed with
- * HIP events. Writes the achieved TFLOP/s and the median clock the workgroups saw (s_memtime
- * ticks per s_memrealtime tick x 100 MHz). Allocates and frees its own device buffers;
- * synchronous on the null stream. 0, -1 (bad arguments) or -2 (HIP error).
- */
-int kg_gfx950_mfma_rate(int dtype_code, int mfma_m, int zero_operands, int iterations, int workgroups,
-                        double* tflops, double* clock_ghz);
 
 /* Operations and cost kinds of kg_gfx950_cost. */
 enum {

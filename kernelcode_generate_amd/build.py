@@ -1,4 +1,4 @@
-"""Build libkg_gfx950.so in-tree with hipcc for gfx950.
+"""Build libkg_gfx950.so in-tree with hipcc for gfx950 (object files under _build/).
 
     python -m kernelcode_generate_amd.build
 
@@ -18,6 +18,7 @@ PACKAGE_DIR = Path(__file__).resolve().parent
 REPO_ROOT = PACKAGE_DIR.parent
 CSRC = PACKAGE_DIR / "csrc"
 OUTPUT = PACKAGE_DIR / "libkg_gfx950.so"
+PROBE_OUTPUT = PACKAGE_DIR / "libkg_gfx950_probe.so"  # bench.py's measurement library
 OFFLOAD_ARCH = "gfx950"
 
 HIP_FLAGS = (
@@ -43,15 +44,49 @@ def include_flags() -> list[str]:
     return [f"-I{REPO_ROOT / 'include'}", f"-I{CSRC}"]
 
 
+SOURCES = ("kg_gfx950_entry.hip", "kg_gfx950_gemm.hip", "kg_gfx950_fa.hip", "kg_gfx950_conv_rowvec.hip",
+           "kg_gfx950_conv_igemm.hip")
+
+
 def build_library(output: Path = OUTPUT, extra_flags: tuple[str, ...] = (), verbose: bool = False) -> Path:
-    """Compile csrc/kg_gfx950_entry.hip (+ the kg_gfx950 device headers) into `output`."""
+    """Compile csrc/kg_gfx950_entry.hip and the kernel-family translation units (the
+    explicit instantiations of kg_gfx950/instances.h), one hipcc process each, in parallel,
+    and link them into `output`."""
+
+    from concurrent.futures import ThreadPoolExecutor
+
+    workdir = output.parent / "_build"
+    workdir.mkdir(exist_ok=True)
+    env = dict(os.environ)
+
+    def run(cmd: list[str]) -> None:
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        proc = subprocess.run(cmd, capture_output=True, text=True, env=env)
+        if proc.returncode != 0:
+            raise RuntimeError(f"hipcc failed ({proc.returncode}): {' '.join(cmd[-3:])}\n{proc.stderr[-4000:]}")
+
+    objects = [workdir / (Path(src).stem + ".o") for src in SOURCES]
+    cmds = [[hipcc(), *HIP_FLAGS, *extra_flags, "-c", *include_flags(), str(CSRC / src), "-o", str(obj)]
+            for src, obj in zip(SOURCES, objects)]
+    with ThreadPoolExecutor(max_workers=min(len(cmds), max(1, os.cpu_count() or 1))) as pool:
+        for future in [pool.submit(run, cmd) for cmd in cmds]:
+            future.result()
+    tmp = output.with_suffix(".so.tmp")
+    run([hipcc(), *HIP_FLAGS, *extra_flags, "-shared", *(str(o) for o in objects), "-o", str(tmp)])
+    os.replace(tmp, output)
+    return output
+
+
+def build_probe_library(output: Path = PROBE_OUTPUT, verbose: bool = False) -> Path:
+    """Compile csrc/probe/mfma_rate.hip, the MFMA-rate probe bench.py reports its ceiling
+    from, into its own shared object (it is not part of libkg_gfx950.so)."""
 
     tmp = output.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIP_FLAGS, *extra_flags, "-shared", *include_flags(), str(CSRC / "kg_gfx950_entry.hip"), "-o", str(tmp)]
+    cmd = [hipcc(), *HIP_FLAGS, "-shared", *include_flags(), str(CSRC / "probe" / "mfma_rate.hip"), "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)
-    env = dict(os.environ)
-    proc = subprocess.run(cmd, capture_output=True, text=True, env=env)
+    proc = subprocess.run(cmd, capture_output=True, text=True, env=dict(os.environ))
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stderr[-4000:]}")
     os.replace(tmp, output)
@@ -61,6 +96,7 @@ def build_library(output: Path = OUTPUT, extra_flags: tuple[str, ...] = (), verb
 def main() -> int:
     path = build_library(verbose=True)
     print(f"built {path}")
+    print(f"built {build_probe_library(verbose=True)}")
     return 0
 
 

@@ -82,7 +82,7 @@ enum ConvOrder { kChannelMajor = 0, kChannelMajorVecW = 1, kTapMajor = 2 };
 // grid runs k slices [y kcs, (y+1) kcs) and stores its fp32 sums, without bias, to
 // partial[y][N][F][Ho Wo]; conv_splitk_reduce_kernel adds the rows in y order, adds the bias
 // and rounds once.
-template <typename Tag, int kMI, int kBias, int kOrder>
+template <typename Tag, int kMI, int kBias, int kOrder, int kRing>
 __global__ __launch_bounds__(convg::kThreads) void conv2d_igemm_kernel(
     const typename convg::IgElem<Tag>::T* __restrict__ x, const typename convg::IgElem<Tag>::T* __restrict__ wt,
     typename convg::IgElem<Tag>::T* __restrict__ y, const void* __restrict__ bias, convg::Params s,
@@ -94,7 +94,10 @@ __global__ __launch_bounds__(convg::kThreads) void conv2d_igemm_kernel(
   constexpr int BK = 4 * V;  // k per slice
   constexpr int BM = 64 * kMI;
   constexpr int kStage = (BM + kBN) * 64;  // bytes
-  __shared__ __attribute__((aligned(1024))) u32x4 lds[2 * kStage / 16];
+  static_assert(kRing >= 2 && kRing <= 4, "LDS ring");
+  // slice it is read from stage it % kRing; slice it + 1 is stored after its MFMAs into the
+  // stage slice it + 1 - kRing was read from, before the previous step's barrier
+  __shared__ __attribute__((aligned(1024))) u32x4 lds[kRing * kStage / 16];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -232,7 +235,7 @@ __global__ __launch_bounds__(convg::kThreads) void conv2d_igemm_kernel(
   for (int it = 0; it < nk; ++it) {
     const int kt = kt0 + it;
     if (it + 1 < nk) load_regs(kt + 1);  // gathers in flight during the MFMAs below
-    const u32x4* st = lds + (it & 1) * (kStage / 16);
+    const u32x4* st = lds + ((unsigned)it % kRing) * (kStage / 16);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       u32x4 af[kMI], bf[2];
@@ -256,7 +259,7 @@ __global__ __launch_bounds__(convg::kThreads) void conv2d_igemm_kernel(
           }
         }
     }
-    if (it + 1 < nk) store_lds((it + 1) & 1);
+    if (it + 1 < nk) store_lds((unsigned)(it + 1) % kRing);
     __syncthreads();
   }
 
@@ -398,10 +401,10 @@ inline int conv_igemm_splits(const ConvShape& s, bool f32, long long max_partial
 
 // splits > 1: split-K with kcs slices per chunk into the fp32 workspace `partial`
 // (splits x N F Ho Wo floats), then the reduction into y.
-template <typename Tag>
-hipError_t launch_conv2d_igemm(const void* x, const void* w, void* y, const void* bias, int bias_kind, int order,
-                               bool w_vec, const ConvShape& s, hipStream_t stream, float* partial = nullptr,
-                               int splits = 1, int kcs = 0) {
+template <typename Tag, int kRing>
+hipError_t launch_conv2d_igemm_ring(const void* x, const void* w, void* y, const void* bias, int bias_kind, int order,
+                                    bool w_vec, const ConvShape& s, hipStream_t stream, float* partial, int splits,
+                                    int kcs) {
   using T = typename convg::IgElem<Tag>::T;
   convg::Params p = conv_igemm_params(s);
   p.w_vec = w_vec ? 1 : 0;
@@ -413,7 +416,7 @@ hipError_t launch_conv2d_igemm(const void* x, const void* w, void* y, const void
   const T* wp = static_cast<const T*>(w);
   T* yp = static_cast<T*>(y);
 #define KG_CONV_IG(MI, B, O)                                                                                  \
-  hipLaunchKernelGGL((conv2d_igemm_kernel<Tag, MI, B, O>), dim3(grid, splits), dim3(convg::kThreads), 0, stream, xp, wp, \
+  hipLaunchKernelGGL((conv2d_igemm_kernel<Tag, MI, B, O, kRing>), dim3(grid, splits), dim3(convg::kThreads), 0, stream, xp, wp, \
                      yp, bias, p, partial)
 #define KG_CONV_IG_B(MI, O)                  \
   if (bias_kind == 0) KG_CONV_IG(MI, 0, O);   \
@@ -447,6 +450,18 @@ hipError_t launch_conv2d_igemm(const void* x, const void* w, void* y, const void
                          splits, yp, bias, nfp, p.div_p, s.f);
   }
   return hipGetLastError();
+}
+
+// ring: the LDS stage count (2, 3 or 4); the register set stays one slice ahead either way
+template <typename Tag>
+hipError_t launch_conv2d_igemm(const void* x, const void* w, void* y, const void* bias, int bias_kind, int order,
+                               bool w_vec, const ConvShape& s, hipStream_t stream, float* partial = nullptr,
+                               int splits = 1, int kcs = 0, int ring = 2) {
+  if (ring == 3)
+    return launch_conv2d_igemm_ring<Tag, 3>(x, w, y, bias, bias_kind, order, w_vec, s, stream, partial, splits, kcs);
+  if (ring == 4)
+    return launch_conv2d_igemm_ring<Tag, 4>(x, w, y, bias, bias_kind, order, w_vec, s, stream, partial, splits, kcs);
+  return launch_conv2d_igemm_ring<Tag, 2>(x, w, y, bias, bias_kind, order, w_vec, s, stream, partial, splits, kcs);
 }
 
 }  // namespace kg_gfx950

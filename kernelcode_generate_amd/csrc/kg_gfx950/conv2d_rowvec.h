@@ -27,7 +27,8 @@
 //
 // A workgroup (4 waves, 2 x 2) computes BM (64 or 128) filters x 128 output pixels and walks
 // K in slices of 16 KW k-rows (16 runs (c, kh) x KW taps): KW MFMA steps of 16 per slice,
-// two LDS stages and two register sets, so a slice's loads are issued two slices before its
+// two LDS stages (or the 3 or 4 of a deeper ring the lowering asks for) and two register
+// sets, so a slice's loads are issued two slices before its
 // MFMAs; register use is bounded for two waves per SIMD (unbounded, the 128-filter
 // instantiations took one wave per SIMD and ran 7-12 % slower on 3x3 shapes). Each lane ends with 4 consecutive output pixels of one filter (Wo % 4 == 0 keeps
 // them in one row of one image) and stores them as one 8-byte piece.
@@ -82,7 +83,7 @@ constexpr int rowvec_stage_bytes() {
 }
 }  // namespace convr
 
-template <typename Tag, int kMI, int KW, int PL, int G, int S>
+template <typename Tag, int kMI, int KW, int PL, int G, int S, int kRing>
 __global__ __launch_bounds__(convr::kThreads, 2) void conv2d_rowvec_kernel(const uint16_t* __restrict__ x,
                                                                         const uint16_t* __restrict__ wt,
                                                                         uint16_t* __restrict__ y,
@@ -99,7 +100,8 @@ __global__ __launch_bounds__(convr::kThreads, 2) void conv2d_rowvec_kernel(const
   constexpr int kWChunks = BM * 2 * KW;  // 16-byte weight chunks per slice
   constexpr int kWPerThread = (kWChunks + kThreads - 1) / kThreads;
   using Piece = typename std::conditional<G == 8, u32x4, u32x2>::type;
-  __shared__ __attribute__((aligned(1024))) char lds[2 * kStage];
+  static_assert(kRing >= 2 && kRing <= 4 && kRing * kStage <= 160 * 1024, "LDS ring");
+  __shared__ __attribute__((aligned(1024))) char lds[kRing * kStage];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -249,8 +251,10 @@ __global__ __launch_bounds__(convr::kThreads, 2) void conv2d_rowvec_kernel(const
         for (int b = 0; b < 2; ++b) acc[i][b] = Hf::mfma32(bf[b], af[i], acc[i][b]);
     }
   };
-  // slice kt: its MFMAs read LDS stage kt & 1; slice kt + 1 goes from register set
-  // (kt + 1) & 1 to the other stage; slice kt + 2 is loaded into set kt & 1 meanwhile.
+  // slice kt: its MFMAs read LDS stage kt % kRing; slice kt + 1 goes from register set
+  // (kt + 1) & 1 to stage (kt + 1) % kRing; slice kt + 2 is loaded into set kt & 1 meanwhile.
+  // The stage a slice is stored to was last read kRing - 1 steps earlier, before that
+  // step's barrier.
   // split-K: this workgroup row's slices kt0 .. kt0 + nk - 1 (kt below counts from kt0)
   int kt0 = 0;
   if (s.kcs > 0) {
@@ -261,8 +265,8 @@ __global__ __launch_bounds__(convr::kThreads, 2) void conv2d_rowvec_kernel(const
   auto step = [&](int kt, auto par_tag) {
     constexpr int par = decltype(par_tag)::value;
     if (kt + 2 < nk) load_regs(kt0 + kt + 2, Int<par>{});
-    compute(par);
-    if (kt + 1 < nk) store_lds(par ^ 1, Int<par ^ 1>{});
+    compute(kRing == 2 ? par : (int)((unsigned)kt % kRing));
+    if (kt + 1 < nk) store_lds(kRing == 2 ? (par ^ 1) : (int)((unsigned)(kt + 1) % kRing), Int<par ^ 1>{});
     __syncthreads();
   };
   load_regs(kt0, Int<0>{});
@@ -333,7 +337,7 @@ constexpr int rowvec_f32_stage_bytes() {
 }
 }  // namespace convr
 
-template <int kMI, int KW, int PL, int S>
+template <int kMI, int KW, int PL, int S, int kRing>
 __global__ __launch_bounds__(convr::kThreads, 2) void conv2d_rowvec_f32_kernel(const float* __restrict__ x,
                                                                               const float* __restrict__ wt,
                                                                               float* __restrict__ y,
@@ -349,7 +353,8 @@ __global__ __launch_bounds__(convr::kThreads, 2) void conv2d_rowvec_f32_kernel(c
   constexpr int kStage = rowvec_f32_stage_bytes<BM, KW, PL, S>();
   constexpr int kWChunks = BM * (KR / 4);  // 16-byte weight chunks per slice
   constexpr int kWPerThread = (kWChunks + kThreads - 1) / kThreads;
-  __shared__ __attribute__((aligned(1024))) char lds[2 * kStage];
+  static_assert(kRing >= 2 && kRing <= 4 && kRing * kStage <= 160 * 1024, "LDS ring");
+  __shared__ __attribute__((aligned(1024))) char lds[kRing * kStage];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -468,11 +473,11 @@ __global__ __launch_bounds__(convr::kThreads, 2) void conv2d_rowvec_f32_kernel(c
     nk = min(nk - kt0, s.kcs);
     partial += (long long)blockIdx.y * s.NP * s.f;
   }
-  auto step = [&](int kt, auto par_tag) {
+  auto step = [&](int kt, auto par_tag) {  // LDS stages as in the 16-bit kernel
     constexpr int par = decltype(par_tag)::value;
     if (kt + 2 < nk) load_regs(kt0 + kt + 2, Int<par>{});
-    compute(par);
-    if (kt + 1 < nk) store_lds(par ^ 1, Int<par ^ 1>{});
+    compute(kRing == 2 ? par : (int)((unsigned)kt % kRing));
+    if (kt + 1 < nk) store_lds(kRing == 2 ? (par ^ 1) : (int)((unsigned)(kt + 1) % kRing), Int<par ^ 1>{});
     __syncthreads();
   };
   load_regs(kt0, Int<0>{});
@@ -594,16 +599,16 @@ inline convr::Params conv_rowvec_params(const ConvShape& s, int bias_kind) {
 // fp32 operands; a bias (kind 1 or 2) is fp32 either way.
 // splits > 1: split-K into the fp32 workspace `partial` (splits x N F Ho Wo floats) with kcs
 // slices per chunk, then the reduction into y (conv_splitk_reduce_kernel).
-inline hipError_t launch_conv2d_rowvec_f32(const float* x, const float* w, float* y, const float* bias, int bias_kind,
-                                           const ConvShape& s, hipStream_t stream, float* partial = nullptr,
-                                           int splits = 1, int kcs = 0) {
+template <int kRing>
+hipError_t launch_conv2d_rowvec_f32_ring(const float* x, const float* w, float* y, const float* bias, int bias_kind,
+                                         const ConvShape& s, hipStream_t stream, float* partial, int splits, int kcs) {
   convr::Params p = conv_rowvec_params(s, bias_kind);
   if (splits > 1) p.kcs = kcs;
   else splits = 1;
   const int mi = conv_rowvec_mi(s);
   const int grid = ((s.f + 64 * mi - 1) / (64 * mi)) * ((p.NP + convr::kBN - 1) / convr::kBN);
 #define KG_CONV_RVF(MI, KW_, PL_, S_) \
-  hipLaunchKernelGGL((conv2d_rowvec_f32_kernel<MI, KW_, PL_, S_>), dim3(grid, splits), dim3(convr::kThreads), 0, stream, x, w, \
+  hipLaunchKernelGGL((conv2d_rowvec_f32_kernel<MI, KW_, PL_, S_, kRing>), dim3(grid, splits), dim3(convr::kThreads), 0, stream, x, w, \
                      y, bias, p, partial)
 #define KG_CONV_RVF_MI(KW_, PL_, S_) \
   if (mi == 2) { KG_CONV_RVF(2, KW_, PL_, S_); } else { KG_CONV_RVF(1, KW_, PL_, S_); }
@@ -629,10 +634,9 @@ inline hipError_t launch_conv2d_rowvec_f32(const float* x, const float* w, float
   return hipGetLastError();
 }
 
-template <typename Tag>
-hipError_t launch_conv2d_rowvec(const uint16_t* x, const uint16_t* w, uint16_t* y, const void* bias, int bias_kind,
-                                const ConvShape& s, hipStream_t stream, float* partial = nullptr, int splits = 1,
-                                int kcs = 0) {
+template <typename Tag, int kRing>
+hipError_t launch_conv2d_rowvec_ring(const uint16_t* x, const uint16_t* w, uint16_t* y, const void* bias, int bias_kind,
+                                     const ConvShape& s, hipStream_t stream, float* partial, int splits, int kcs) {
   convr::Params p = conv_rowvec_params(s, bias_kind);
   if (splits > 1) p.kcs = kcs;
   else splits = 1;
@@ -640,7 +644,7 @@ hipError_t launch_conv2d_rowvec(const uint16_t* x, const uint16_t* w, uint16_t* 
   const int piece = conv_rowvec_piece(s);
   const int grid = ((s.f + 64 * mi - 1) / (64 * mi)) * ((p.NP + convr::kBN - 1) / convr::kBN);
 #define KG_CONV_RV(MI, KW_, PL_, G_, S_)                                                                     \
-  hipLaunchKernelGGL((conv2d_rowvec_kernel<Tag, MI, KW_, PL_, G_, S_>), dim3(grid, splits), dim3(convr::kThreads), 0, \
+  hipLaunchKernelGGL((conv2d_rowvec_kernel<Tag, MI, KW_, PL_, G_, S_, kRing>), dim3(grid, splits), dim3(convr::kThreads), 0, \
                      stream, x, w, y, bias, p, partial)
 #define KG_CONV_RV_MI(KW_, PL_, G_, S_) \
   if (mi == 2) KG_CONV_RV(2, KW_, PL_, G_, S_); \
@@ -671,6 +675,24 @@ hipError_t launch_conv2d_rowvec(const uint16_t* x, const uint16_t* w, uint16_t* 
                          splits, y, bias, nfp, p.div_p, s.f);
   }
   return hipGetLastError();
+}
+
+// ring: the LDS stage count (2, 3 or 4); the register sets stay two either way
+inline hipError_t launch_conv2d_rowvec_f32(const float* x, const float* w, float* y, const float* bias, int bias_kind,
+                                           const ConvShape& s, hipStream_t stream, float* partial = nullptr,
+                                           int splits = 1, int kcs = 0, int ring = 2) {
+  if (ring == 3) return launch_conv2d_rowvec_f32_ring<3>(x, w, y, bias, bias_kind, s, stream, partial, splits, kcs);
+  if (ring == 4) return launch_conv2d_rowvec_f32_ring<4>(x, w, y, bias, bias_kind, s, stream, partial, splits, kcs);
+  return launch_conv2d_rowvec_f32_ring<2>(x, w, y, bias, bias_kind, s, stream, partial, splits, kcs);
+}
+
+template <typename Tag>
+hipError_t launch_conv2d_rowvec(const uint16_t* x, const uint16_t* w, uint16_t* y, const void* bias, int bias_kind,
+                                const ConvShape& s, hipStream_t stream, float* partial = nullptr, int splits = 1,
+                                int kcs = 0, int ring = 2) {
+  if (ring == 3) return launch_conv2d_rowvec_ring<Tag, 3>(x, w, y, bias, bias_kind, s, stream, partial, splits, kcs);
+  if (ring == 4) return launch_conv2d_rowvec_ring<Tag, 4>(x, w, y, bias, bias_kind, s, stream, partial, splits, kcs);
+  return launch_conv2d_rowvec_ring<Tag, 2>(x, w, y, bias, bias_kind, s, stream, partial, splits, kcs);
 }
 
 }  // namespace kg_gfx950

@@ -4,7 +4,8 @@
 // Work split: a workgroup holds query rows of one (b,h), 32 per wave (Cfg<D>: 8 waves for
 // D=128, 4 for D=64 and for D=128 grids too small to give every CU an 8-wave workgroup;
 // two waves per SIMD either way). Key/value tiles of 64 keys are copied
-// HBM -> LDS (two buffers each for K and V) and shared by the workgroup's waves. Workgroup
+// HBM -> LDS into rings of kStages buffers each for K and V (2 by default; 3 or 4 when the
+// lowering's memory_stage asks for a deeper ring) and shared by the workgroup's waves. Workgroup
 // ids are dealt to the 8 XCDs round-robin; they are remapped so that each XCD runs the query
 // blocks of the same (b,h) together and its L2 serves their K/V.
 //
@@ -36,8 +37,11 @@
 //            reads slotted between them;
 //   block 2: the PV(j) MFMAs, with the last quarter of softmax(j), the V(j) fragment reads
 //            and the max of S(j+1) slotted between them.
-// The copies of K(j+2) and V(j+1) (into the buffers iteration j-1 finished with) are
-// slotted between the block-1 MFMAs of iteration j; one wait + barrier ends the iteration.
+// The copies of K(j+S) and V(j+S-1), S = kStages (into the buffers iteration j-1 finished
+// with: K(j) and V(j-1)), are slotted between the block-1 MFMAs of iteration j; one wait +
+// barrier ends the iteration. With two buffers it waits for every copy; with deeper rings
+// only for the copies issued before this iteration (the next one needs K(j+2) and V(j+1),
+// issued at least one iteration earlier), so a copy may take S-1 iterations to land.
 //
 // LDS chunk swizzles (16-byte chunks, 64 banks of 4 bytes; ds_read_b128 serves 16 lanes per
 // cycle, 64-bit reads 32): K chunk c of key row r sits at slot c ^ k_mask(r) and V chunk c
@@ -52,6 +56,7 @@ namespace kg_gfx950 {
 namespace fa {
 
 constexpr int kBC = 64;  // keys per tile
+constexpr int kDefaultStages = 2;  // K/V ring depth unless the lowering asks for another
 // Waves per workgroup (32 queries each): D=128 uses one 8-wave workgroup per CU (K/V tiles
 // shared by 256 queries halve the HBM/L2 -> LDS copy traffic per query), D=64 two 4-wave
 // workgroups per CU. Either way two waves share each SIMD.
@@ -136,7 +141,7 @@ __device__ __forceinline__ void rows4_combine(float& a, float& b) {
 
 }  // namespace fa
 
-template <typename Tag, int D, bool kCausal, bool kMasked, int W>
+template <typename Tag, int D, bool kCausal, bool kMasked, int W, int kStages>
 __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU)) void fa_fwd_mfma_kernel(const uint16_t* __restrict__ Q,
                                                                       const uint16_t* __restrict__ K,
                                                                       const uint16_t* __restrict__ V,
@@ -159,8 +164,9 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
   static_assert(PW >= 1 && 2 * PW <= NS, "copy slots");
   constexpr int RPP = 1024 / RB;     // rows per copy instruction
   constexpr int kKAhead = 3;         // K fragments read ahead of their MFMAs
+  static_assert(kStages >= 2 && kStages <= 4, "K/V ring depth");
 
-  __shared__ __attribute__((aligned(1024))) u32x4 lds[4 * TB / 16];  // K0 K1 V0 V1
+  __shared__ __attribute__((aligned(1024))) u32x4 lds[2 * kStages * TB / 16];  // K ring, then V ring
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -194,7 +200,7 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
   const int n_end = kCausal ? min(s_kv, m0 + kBM) : s_kv;
   const int ntiles = (n_end + kBC - 1) / kBC;
 
-  // ---- HBM -> LDS copies: K tile t into K buffer b (LDS bytes b*TB), V into 2*TB + b*TB ----
+  // ---- HBM -> LDS copies: K tile t into K buffer b (LDS bytes b*TB), V into (kStages+b)*TB ----
   // Copy instruction p of wave w covers the KiB (w + kWaves*p) of the tile: rows
   // (w + kWaves*p)*RPP + lane/DCH, LDS slot lane%DCH. The rows of one lane's copies lie
   // kWaves*RPP (at least 32) rows apart, so they share their K and V masks: one per-lane
@@ -226,7 +232,7 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
   };
   auto copy_v = [&](int t, int buf) {
 #pragma unroll
-    for (int p = 0; p < PW; ++p) copy_piece(Vb, t, lds0 + (2 + buf) * TB, true, p);
+    for (int p = 0; p < PW; ++p) copy_piece(Vb, t, lds0 + (kStages + buf) * TB, true, p);
   };
 
   // ---- fragment reads ----
@@ -248,16 +254,17 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
       const int c16 = 2 * db + ((l16 & 3) >> 1);
-      v_rd[db] = lds0 + 2 * TB + row * RB + 16 * (c16 ^ vm) + 8 * (l16 & 1);
+      v_rd[db] = lds0 + kStages * TB + row * RB + 16 * (c16 ^ vm) + 8 * (l16 & 1);
     }
   }
-  auto read_k = [&](int buf, int f) -> u32x4 {
+  // boff: the byte offset of the tile's ring buffer (buffer index x TB)
+  auto read_k = [&](uint32_t boff, int f) -> u32x4 {
     const int kb = f / NDS, s = f % NDS;
-    return *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(k_rd[s] + buf * TB + kb * 16 * RB);
+    return *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(k_rd[s] + boff + kb * 16 * RB);
   };
-  auto read_v = [&](int buf, int f) -> u32x4 {
+  auto read_v = [&](uint32_t boff, int f) -> u32x4 {
     const int c = f / NDB, db = f % NDB;
-    const uint32_t a = v_rd[db] + buf * TB + 32 * c * RB;
+    const uint32_t a = v_rd[db] + boff + 32 * c * RB;
     const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(uintptr_t)a);
     const s16x4 hi =
         __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(uintptr_t)(a + 16 * RB));
@@ -367,21 +374,27 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
     s[qb][kb] = H::mfma16(kf, qf[qb][st], st == 0 ? zero4 : s[qb][kb]);
   };
 
-  // One key tile. par = j & 1 (K(j+1) sits in K buffer par^1, V(j) in V buffer par);
-  // kNext: tile j+1 exists, its S is computed here into sn.
+  // One key tile. par = j & 1 selects the score registers (and, with two buffers, the ring
+  // buffers as immediates: K(j+1) sits in K buffer par^1, V(j) in V buffer par; deeper rings
+  // take tile t's buffer t % kStages); kNext: tile j+1 exists, its S is computed here into sn.
   // kTail: the iterations after the loop, which rescale without a branch (a branch there
   // leaves the compiler short of registers where its two paths meet)
   auto iteration = [&](int j, auto par_tag, auto next_tag, Scores& sc, Scores& sn, auto tail_tag) {
     constexpr int par = decltype(par_tag)::value;
     constexpr bool kNext = decltype(next_tag)::value != 0;
-    const bool copy_k2 = j + 2 < ntiles;  // K(j+2) exists (only if kNext)
+    const bool copy_k2 = j + kStages < ntiles;      // K(j+S) exists (only if kNext)
+    const bool copy_v1 = kStages == 2 || j + kStages - 1 < ntiles;  // V(j+S-1) exists
+    const uint32_t kb_next = (kStages == 2 ? (par ^ 1) : (j + 1) % kStages) * TB;  // K(j+1)
+    const uint32_t kb_copy = (kStages == 2 ? par : j % kStages) * TB;              // K(j+S): where K(j) was
+    const uint32_t vb_cur = (kStages == 2 ? par : j % kStages) * TB;               // V(j)
+    const uint32_t vb_copy = (kStages == 2 ? (par ^ 1) : (j + kStages - 1) % kStages) * TB;  // V(j+S-1)
     rescale(tail_tag);
     if constexpr (!kNext) {
       // last tile: the first two V fragments are read under the softmax, the rest two
       // fragments ahead of their MFMAs (all 16 at once would not fit the registers)
       u32x4 vf[NVF];
-      vf[0] = read_v(par, 0);
-      vf[1] = read_v(par, 1);
+      vf[0] = read_v(vb_cur, 0);
+      vf[1] = read_v(vb_cur, 1);
 #pragma unroll
       for (int e = 0; e < 32; ++e) {
         sm_elem(sc, e);
@@ -390,33 +403,33 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
 #pragma unroll
       for (int i = 0; i < NP; ++i) {
         pv(i, vf[i >> 1]);
-        if ((i & 1) == 0 && (i >> 1) + 2 < NVF) vf[(i >> 1) + 2] = read_v(par, (i >> 1) + 2);
+        if ((i & 1) == 0 && (i >> 1) + 2 < NVF) vf[(i >> 1) + 2] = read_v(vb_cur, (i >> 1) + 2);
       }
     } else {
       u32x4 kf[NKF];
       u32x4 vf[NVF];
 #pragma unroll
-      for (int f = 0; f < kKAhead; ++f) kf[f] = read_k(par ^ 1, f);
+      for (int f = 0; f < kKAhead; ++f) kf[f] = read_k(kb_next, f);
       __builtin_amdgcn_sched_barrier(0);
       // block 1: S(j+1) MFMAs; softmax elements 0..23 of S(j)
 #pragma unroll
       for (int i = 0; i < NS; ++i) {
         s_mfma(sn, i, kf[i >> 1]);
-        // this wave's 2*PW copies of K(j+2) and V(j+1), spread over the steps: a burst of
+        // this wave's 2*PW copies of K(j+S) and V(j+S-1), spread over the steps: a burst of
         // copies from all waves right after the barrier stalls their issue for hundreds of
         // cycles (the HBM/L2 -> LDS path moves about 64-80 bytes per clock per CU)
         constexpr int kGap = NS / (2 * PW);
         if (i % kGap == kGap - 1) {
           const int c = i / kGap;
           if (c < PW) {
-            if (copy_k2) copy_piece(Kb, j + 2, lds0 + par * TB, false, c);
+            if (copy_k2) copy_piece(Kb, j + kStages, lds0 + kb_copy, false, c);
           } else {
-            copy_piece(Vb, j + 1, lds0 + (2 + (par ^ 1)) * TB, true, c - PW);
+            if (copy_v1) copy_piece(Vb, j + kStages - 1, lds0 + kStages * TB + vb_copy, true, c - PW);
           }
         }
-        if ((i & 1) == 0 && (i >> 1) + kKAhead < NKF) kf[(i >> 1) + kKAhead] = read_k(par ^ 1, (i >> 1) + kKAhead);
-        if (i == NS - 2) vf[0] = read_v(par, 0);
-        if (i == NS - 1) vf[1] = read_v(par, 1);
+        if ((i & 1) == 0 && (i >> 1) + kKAhead < NKF) kf[(i >> 1) + kKAhead] = read_k(kb_next, (i >> 1) + kKAhead);
+        if (i == NS - 2) vf[0] = read_v(vb_cur, 0);
+        if (i == NS - 1) vf[1] = read_v(vb_cur, 1);
         const int lo = 24 * i / NS, hi = 24 * (i + 1) / NS;
 #pragma unroll
         for (int e = lo; e < hi; ++e) sm_elem(sc, e);
@@ -429,7 +442,7 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
 #pragma unroll
       for (int i = 0; i < NP / 2; ++i) {
         pv(i, vf[i >> 1]);
-        if ((i & 1) == 0) vf[(i >> 1) + 2] = read_v(par, (i >> 1) + 2);
+        if ((i & 1) == 0) vf[(i >> 1) + 2] = read_v(vb_cur, (i >> 1) + 2);
         const int lo = 24 + 8 * i / (NP / 2), hi = 24 + 8 * (i + 1) / (NP / 2);
 #pragma unroll
         for (int e = lo; e < hi; ++e) sm_elem(sc, e);
@@ -442,7 +455,7 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
 #pragma unroll
         for (int i = NP / 2; i < NP; ++i) {
           pv(i, vf[i >> 1]);
-          if ((i & 1) == 0 && (i >> 1) + 2 < NVF) vf[(i >> 1) + 2] = read_v(par, (i >> 1) + 2);
+          if ((i & 1) == 0 && (i >> 1) + 2 < NVF) vf[(i >> 1) + 2] = read_v(vb_cur, (i >> 1) + 2);
           const int r = i - NP / 2;
           const int lo = 16 * r / (NP / 2), hi = 16 * (r + 1) / (NP / 2);
 #pragma unroll
@@ -453,21 +466,30 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
 #pragma unroll
         for (int i = NP / 2; i < NP; ++i) {
           pv(i, vf[i >> 1]);
-          if ((i & 1) == 0 && (i >> 1) + 2 < NVF) vf[(i >> 1) + 2] = read_v(par, (i >> 1) + 2);
+          if ((i & 1) == 0 && (i >> 1) + 2 < NVF) vf[(i >> 1) + 2] = read_v(vb_cur, (i >> 1) + 2);
         }
         apply_mask(sn, j + 1);
 #pragma unroll
         for (int k = 0; k < 16; ++k) max_op(sn, k >> 3, k & 7, mx[k >> 3]);
       }
       tile_max(mx);
-      wait_and_barrier<0>();
+      if constexpr (kStages == 2) {
+        wait_and_barrier<0>();
+      } else {
+        // leave this iteration's copies in flight: every older one has landed after this
+        if (copy_k2 && copy_v1) wait_and_barrier<2 * PW>();
+        else if (copy_k2 || copy_v1) wait_and_barrier<PW>();
+        else wait_and_barrier<0>();
+      }
     }
   };
 
-  // ---- prologue: tiles 0 (K, V) and 1 (K); S(0) and its max ----
-  copy_k(0, 0);
-  copy_v(0, 0);
-  if (ntiles > 1) copy_k(1, 1);
+  // ---- prologue: K tiles 0..S-1 and V tiles 0..S-2 (those that exist); S(0) and its max ----
+#pragma unroll
+  for (int t = 0; t < kStages; ++t) {
+    if (t < ntiles) copy_k(t, t);
+    if (t < kStages - 1 && t < ntiles) copy_v(t, t);
+  }
   wait_and_barrier<0>();
   Scores sa, sb;
   {
@@ -482,7 +504,7 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
     for (int k = 0; k < 16; ++k) max_op(sa, k >> 3, k & 7, mx[k >> 3]);
     tile_max(mx);
   }
-  wait_and_barrier<0>();  // every wave is done with K(0) before K(2) replaces it
+  wait_and_barrier<0>();  // every wave is done with K(0) before K(S) replaces it
 
   int j = 0;
   for (; j + 2 < ntiles; j += 2) {
@@ -526,7 +548,7 @@ inline bool fa_mfma_supported(const FaShape& s) {
          (long long)((s.s_q + fa::Cfg<64>::kBM - 1) / fa::Cfg<64>::kBM) * s.bh < (1ll << 31);
 }
 
-template <typename Tag, int D, int W>
+template <typename Tag, int D, int W, int kStages>
 hipError_t launch_fa_fwd_mfma_dw(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, const FaShape& s,
                                  hipStream_t stream) {
   using C = fa::Cfg<D, W>;
@@ -535,7 +557,7 @@ hipError_t launch_fa_fwd_mfma_dw(const uint16_t* q, const uint16_t* k, const uin
   const bool masked = (s.s_q % C::kBM) != 0 || (s.s_kv % fa::kBC) != 0;
   const float scale_log2 = s.scale * 1.4426950408889634f;
 #define KG_FA(CAUSAL, MASKED)                                                                                    \
-  hipLaunchKernelGGL((fa_fwd_mfma_kernel<Tag, D, CAUSAL, MASKED, W>), grid, dim3(C::kThreads), 0, stream, q, k, v, o, \
+  hipLaunchKernelGGL((fa_fwd_mfma_kernel<Tag, D, CAUSAL, MASKED, W, kStages>), grid, dim3(C::kThreads), 0, stream, q, k, v, o, \
                      s.bh, s.s_q, s.s_kv, scale_log2)
   if (s.causal) {
     if (masked) KG_FA(true, true); else KG_FA(true, false);
@@ -554,14 +576,23 @@ inline int fa_mfma_waves(const FaShape& s) {
   return wg8 < 256 ? 4 : 8;
 }
 
+template <typename Tag, int kStages>
+hipError_t launch_fa_fwd_mfma_st(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, const FaShape& s,
+                                 hipStream_t stream) {
+  if (s.d == 128) {
+    if (fa_mfma_waves(s) == 4) return launch_fa_fwd_mfma_dw<Tag, 128, 4, kStages>(q, k, v, o, s, stream);
+    return launch_fa_fwd_mfma_dw<Tag, 128, 8, kStages>(q, k, v, o, s, stream);
+  }
+  return launch_fa_fwd_mfma_dw<Tag, 64, 4, kStages>(q, k, v, o, s, stream);
+}
+
+// stages: the K/V ring depth (2, 3 or 4)
 template <typename Tag>
 hipError_t launch_fa_fwd_mfma(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, const FaShape& s,
-                              hipStream_t stream) {
-  if (s.d == 128) {
-    if (fa_mfma_waves(s) == 4) return launch_fa_fwd_mfma_dw<Tag, 128, 4>(q, k, v, o, s, stream);
-    return launch_fa_fwd_mfma_dw<Tag, 128, 8>(q, k, v, o, s, stream);
-  }
-  return launch_fa_fwd_mfma_dw<Tag, 64, 4>(q, k, v, o, s, stream);
+                              hipStream_t stream, int stages = fa::kDefaultStages) {
+  if (stages == 3) return launch_fa_fwd_mfma_st<Tag, 3>(q, k, v, o, s, stream);
+  if (stages == 4) return launch_fa_fwd_mfma_st<Tag, 4>(q, k, v, o, s, stream);
+  return launch_fa_fwd_mfma_st<Tag, 2>(q, k, v, o, s, stream);
 }
 
 }  // namespace kg_gfx950

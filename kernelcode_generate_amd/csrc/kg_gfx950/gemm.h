@@ -455,4 +455,21 @@ __global__ __launch_bounds__(256) void gemm_simt_kernel(const TA* __restrict__ A
   }
 }
 
+// One launch of gemm_pipe_kernel (grid x splits workgroups; splits > 1: fp32 partials of
+// k_chunk-deep K chunks into `partial`, reduced by gemm_splitk_reduce_kernel afterwards).
+// bias_kind: 0 none, 1 fp32, 2 16-bit.
+template <typename Tag, int kTM, int kStages, bool kRagged>
+hipError_t launch_gemm_pipe(const uint16_t* A, const uint16_t* B, uint16_t* C, const void* bias, int bias_kind, int M,
+                            int N, int K, long long lda, long long ldb, long long ldc, float* partial, int k_chunk,
+                            int grid, int splits, hipStream_t stream) {
+#define KG_GEMM_PIPE(BIAS)                                                                                             \
+  hipLaunchKernelGGL((gemm_pipe_kernel<Tag, BIAS, kTM, kStages, kRagged>), dim3(grid, splits), dim3(gemmp::kThreads), 0, \
+                     stream, A, B, C, bias, M, N, K, lda, ldb, ldc, partial, k_chunk)
+  if (bias_kind == 0) KG_GEMM_PIPE(0);
+  else if (bias_kind == 1) KG_GEMM_PIPE(1);
+  else KG_GEMM_PIPE(2);
+#undef KG_GEMM_PIPE
+  return hipGetLastError();
+}
+
 }  // namespace kg_gfx950

@@ -32,18 +32,20 @@ namespace kg_gfx950 {
 namespace gemmf {
 constexpr int kTile = 128;
 constexpr int kBK = 16;
-constexpr int kStages = 3;
+constexpr int kDefaultStages = 3;  // LDS ring depth unless the lowering asks for another
 constexpr int kThreads = 256;
 constexpr int kStageBytes = 2 * kTile * kBK * 4;  // lhs + rhs slice, 16 KiB
 __device__ __forceinline__ int a_mask(int m) { return (m >> 2) & 3; }
 __device__ __forceinline__ int b_mask(int k) { return 8 * ((k >> 2) & 1); }
 }  // namespace gemmf
 
-template <int kBias, bool kRagged>  // kBias: 0 none, 1 fp32 bias
+// kBias: 0 none, 1 fp32 bias; kStages: the LDS ring depth (slices are copied kStages - 1 ahead)
+template <int kBias, bool kRagged, int kStages>
 __global__ __launch_bounds__(gemmf::kThreads, 3) void gemm_f32_mfma_kernel(
     const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, const float* __restrict__ bias,
     int M, int N, int K, long long lda, long long ldb, long long ldc) {
   using namespace gemmf;
+  static_assert(kStages >= 2 && kStages <= 4, "LDS ring depth");
   __shared__ __attribute__((aligned(1024))) char lds[kStages * kStageBytes];
 
   const int tid = threadIdx.x;
@@ -142,14 +144,18 @@ __global__ __launch_bounds__(gemmf::kThreads, 3) void gemm_f32_mfma_kernel(
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
   const int ktiles = kRagged ? (K + kBK - 1) / kBK : K / kBK;
-  issue(0);
-  if (ktiles > 1) issue(1);
+#pragma unroll
+  for (int t = 0; t < kStages - 1; ++t)
+    if (t < ktiles) issue(t);
   for (int kt = 0; kt < ktiles; ++kt) {
-    // slice kt has landed once at most slice kt+1's copies are outstanding; the barrier
-    // also ends every wave's reads of slice kt-1, whose stage slice kt+2 refills
-    if (kt + 1 < ktiles) wait_and_barrier<4>();
+    // slice kt has landed once at most the copies of the slices after it (4 per slice and
+    // wave, up to kStages - 2 slices) are outstanding; the barrier also ends every wave's
+    // reads of slice kt-1, whose stage slice kt+kStages-1 refills
+    const int later = min(kStages - 2, ktiles - 1 - kt);
+    if (later >= 2) wait_and_barrier<8>();
+    else if (later == 1) wait_and_barrier<4>();
     else wait_and_barrier<0>();
-    if (kt + 2 < ktiles) issue(kt + 2);
+    if (kt + kStages - 1 < ktiles) issue(kt + kStages - 1);
     const uint32_t st = lds0 + (kt % kStages) * kStageBytes;
     // all fragments of the slice are read before its MFMAs: the reads of half 1 land while
     // the MFMAs of half 0 run

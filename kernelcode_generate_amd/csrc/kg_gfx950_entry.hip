@@ -11,6 +11,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <memory>
 #include <mutex>
 #include <vector>
 
@@ -25,7 +26,7 @@
 #include "kg_gfx950/conv2d_rowvec.h"
 #include "kg_gfx950/flash_attn_mfma.h"
 #include "kg_gfx950/flash_attn_f32.h"
-#include "kg_gfx950/mfma_rate.h"
+#include "kg_gfx950/instances.h"  // the heavy kernel families are compiled in their own translation units
 
 namespace {
 
@@ -276,12 +277,18 @@ int pipe_splits(long long M, long long N, long long K, long long* chunk) {
 
 // Split-K workspaces, one per (device, stream) and kept for the life of the process: work
 // enqueued on one stream runs in order, so its calls can share one buffer, and calls on
-// different streams never do. A larger request replaces the buffer (the old one is released
-// in stream order, after the work already enqueued). At most kSplitCachedStreams buffers are
-// kept per device: a call on another stream then takes the least recently used slot and
-// releases that slot's buffer with hipFree, which waits for the device's pending work (the
-// stream the buffer was used on may no longer exist). An allocation per call
-// (hipMallocAsync/hipFreeAsync) cost about 60 us of host time per matmul.
+// different streams never do. A split call enqueues two kernels (the partial sums, then
+// their reduction), and a call holds its slot's lock (the lease) from the lookup until both
+// are enqueued: two host threads on one stream (every thread's default is the null stream)
+// therefore enqueue whole pairs, never A's partials, B's partials, A's reduction. A larger
+// request replaces the buffer (the old one is released in stream order, after the work
+// already enqueued). At most kSplitCachedStreams buffers are kept per device: a call on
+// another stream then takes the least recently used slot, waits for that slot's lease (so no
+// call is between its two launches) and releases its buffer with hipFree, which waits for
+// the device's pending work (the stream the buffer was used on may no longer exist). Lock
+// order: the table's mutex, then a slot's. An allocation per call (hipMallocAsync /
+// hipFreeAsync) cost about 60 us of host time per matmul. Calls that split allocate on the
+// first use per stream (or a larger shape): they are not capturable in a HIP graph then.
 constexpr int kSplitCachedStreams = 8;
 struct SplitWorkspace {
   int device;
@@ -289,45 +296,63 @@ struct SplitWorkspace {
   void* ptr;
   size_t bytes;
   unsigned long long last_use;
+  std::shared_ptr<std::mutex> busy;  // the lease: held from the lookup through the reduction's launch
+};
+struct SplitLease {
+  void* ptr = nullptr;
+  std::unique_lock<std::mutex> hold;
 };
 std::mutex g_split_ws_mutex;
 std::vector<SplitWorkspace> g_split_ws;
 unsigned long long g_split_ws_clock = 0;
 
-void* split_workspace(size_t bytes, hipStream_t stream) {
+SplitLease split_workspace(size_t bytes, hipStream_t stream) {
+  SplitLease lease;
   int device = 0;
-  if (hipGetDevice(&device) != hipSuccess) return nullptr;
+  if (hipGetDevice(&device) != hipSuccess) return lease;
   std::lock_guard<std::mutex> lock(g_split_ws_mutex);
-  SplitWorkspace* slot = nullptr;
-  SplitWorkspace* lru = nullptr;
-  int on_device = 0;
-  for (auto& w : g_split_ws) {
+  int slot = -1, lru = -1, on_device = 0;
+  for (int i = 0; i < (int)g_split_ws.size(); ++i) {
+    const auto& w = g_split_ws[i];
     if (w.device != device) continue;
     ++on_device;
-    if (w.stream == stream) slot = &w;
-    if (lru == nullptr || w.last_use < lru->last_use) lru = &w;
+    if (w.stream == stream) slot = i;
+    if (lru < 0 || w.last_use < g_split_ws[lru].last_use) lru = i;
   }
-  if (slot != nullptr && slot->bytes >= bytes) {
-    slot->last_use = ++g_split_ws_clock;
-    return slot->ptr;
+  if (slot >= 0) {
+    lease.hold = std::unique_lock<std::mutex>(*g_split_ws[slot].busy);
+    if (g_split_ws[slot].bytes >= bytes) {
+      g_split_ws[slot].last_use = ++g_split_ws_clock;
+      lease.ptr = g_split_ws[slot].ptr;
+      return lease;
+    }
   }
   void* ptr = nullptr;
   const size_t want = std::max(bytes, (size_t)(4u << 20));
   if (hipMalloc(&ptr, want) != hipSuccess) {
     (void)hipGetLastError();
-    return nullptr;
+    lease.hold = {};
+    return lease;
   }
-  if (slot != nullptr) {
-    (void)hipFreeAsync(slot->ptr, stream);
+  if (slot >= 0) {
+    (void)hipFreeAsync(g_split_ws[slot].ptr, stream);
   } else if (on_device >= kSplitCachedStreams) {
-    (void)hipFree(lru->ptr);  // waits for the device's pending work
     slot = lru;
+    lease.hold = std::unique_lock<std::mutex>(*g_split_ws[slot].busy);  // the evicted call has launched both kernels
+    (void)hipFree(g_split_ws[slot].ptr);                                 // waits for the device's pending work
   } else {
-    g_split_ws.push_back({device, stream, nullptr, 0, 0});
-    slot = &g_split_ws.back();
+    g_split_ws.push_back({device, stream, nullptr, 0, 0, std::make_shared<std::mutex>()});
+    slot = (int)g_split_ws.size() - 1;
+    lease.hold = std::unique_lock<std::mutex>(*g_split_ws[slot].busy);
   }
-  *slot = {device, stream, ptr, want, ++g_split_ws_clock};
-  return ptr;
+  SplitWorkspace& w = g_split_ws[slot];
+  w.device = device;
+  w.stream = stream;
+  w.ptr = ptr;
+  w.bytes = want;
+  w.last_use = ++g_split_ws_clock;
+  lease.ptr = ptr;
+  return lease;
 }
 
 template <typename Tag>
@@ -346,30 +371,29 @@ int launch_gemm_mfma(const Mem& out, const Mem& lhs, const Mem& rhs, const Mem& 
   long long chunk = K;
   int splits = pipe_splits(M, N, K, &chunk);
   float* partial = nullptr;
+  SplitLease lease;  // held until both kernels of a split call are enqueued (this function's return)
   if (splits > 1) {
-    partial = static_cast<float*>(split_workspace((size_t)splits * M * N * sizeof(float), g_stream));
+    lease = split_workspace((size_t)splits * M * N * sizeof(float), g_stream);
+    partial = static_cast<float*>(lease.ptr);
     if (partial == nullptr) splits = 1;  // no workspace: the whole K range in one pass
   }
   const int k_chunk = splits > 1 ? (int)chunk : 0;
-#define KG_GEMM_PIPE(BIAS, TM, ST, RAG)                                                                  \
-  hipLaunchKernelGGL((gemm_pipe_kernel<Tag, BIAS, TM, ST, RAG>), dim3(grid, splits), dim3(gemmp::kThreads), 0, \
-                     g_stream, A, B, C, bp, M, N, K, lda, ldb, ldc, partial, k_chunk)
-#define KG_GEMM_PIPE_BIAS(TM, ST, RAG)               \
-  if (bias_kind == 0) KG_GEMM_PIPE(0, TM, ST, RAG);   \
-  else if (bias_kind == 1) KG_GEMM_PIPE(1, TM, ST, RAG); \
-  else KG_GEMM_PIPE(2, TM, ST, RAG)
-#define KG_GEMM_PIPE_DEPTH(TM, RAG)                        \
-  if (stages == 2) { KG_GEMM_PIPE_BIAS(TM, 2, RAG); }      \
-  else if (stages == 3) { KG_GEMM_PIPE_BIAS(TM, 3, RAG); } \
-  else { KG_GEMM_PIPE_BIAS(TM, 4, RAG); }
+#define KG_GEMM_PIPE(TM, ST, RAG)                                                                          \
+  e = launch_gemm_pipe<Tag, TM, ST, RAG>(A, B, C, bp, bias_kind, M, N, K, lda, ldb, ldc, partial, k_chunk, grid, splits, \
+                                         g_stream)
+#define KG_GEMM_PIPE_DEPTH(TM, RAG)                  \
+  if (stages == 2) { KG_GEMM_PIPE(TM, 2, RAG); }      \
+  else if (stages == 3) { KG_GEMM_PIPE(TM, 3, RAG); } \
+  else { KG_GEMM_PIPE(TM, 4, RAG); }
+  hipError_t e = hipSuccess;
   if (tm == 128) {
     if (ragged) { KG_GEMM_PIPE_DEPTH(128, true) } else { KG_GEMM_PIPE_DEPTH(128, false) }
   } else {
     if (ragged) { KG_GEMM_PIPE_DEPTH(256, true) } else { KG_GEMM_PIPE_DEPTH(256, false) }
   }
 #undef KG_GEMM_PIPE_DEPTH
-#undef KG_GEMM_PIPE_BIAS
 #undef KG_GEMM_PIPE
+  if (e != hipSuccess) return fail(kHipFailure, "matmul(mfma-pipe): %s", hipGetErrorString(e));
   if (splits > 1) {
     const int rgrid = (int)cdiv((long long)M * (N / 4), kSplitReduceThreads);
     if (bias_kind == 0)
@@ -393,7 +417,8 @@ bool gemm_f32_mfma_pays(long long M, long long N, long long K) {
   return cdiv(M, gemmf::kTile) * cdiv(N, gemmf::kTile) >= kF32MfmaMinTiles && K >= 4 * gemmf::kBK;
 }
 
-int launch_gemm_f32_mfma(const Mem& out, const Mem& lhs, const Mem& rhs, const Mem& bias, int M, int N, int K) {
+int launch_gemm_f32_mfma(const Mem& out, const Mem& lhs, const Mem& rhs, const Mem& bias, int M, int N, int K,
+                         int stages) {
   const float* A = static_cast<const float*>(lhs.data);
   const float* B = static_cast<const float*>(rhs.data);
   float* C = static_cast<float*>(out.data);
@@ -401,14 +426,19 @@ int launch_gemm_f32_mfma(const Mem& out, const Mem& lhs, const Mem& rhs, const M
   const bool ragged = M % gemmf::kTile || N % gemmf::kTile || K % gemmf::kBK;
   const int grid = (int)(cdiv(M, gemmf::kTile) * cdiv(N, gemmf::kTile));
   const long long lda = lhs.stride[0], ldb = rhs.stride[0], ldc = out.stride[0];
-#define KG_GEMM_F32(BIAS, RAG)                                                                                   \
-  hipLaunchKernelGGL((gemm_f32_mfma_kernel<BIAS, RAG>), dim3(grid), dim3(gemmf::kThreads), 0, g_stream, A, B, C, bp, \
+#define KG_GEMM_F32(BIAS, RAG, ST)                                                                                   \
+  hipLaunchKernelGGL((gemm_f32_mfma_kernel<BIAS, RAG, ST>), dim3(grid), dim3(gemmf::kThreads), 0, g_stream, A, B, C, bp, \
                      M, N, K, lda, ldb, ldc)
+#define KG_GEMM_F32_ST(BIAS, RAG)                                       \
+  if (stages == 2) { KG_GEMM_F32(BIAS, RAG, 2); }                       \
+  else if (stages == 4) { KG_GEMM_F32(BIAS, RAG, 4); }                  \
+  else { KG_GEMM_F32(BIAS, RAG, 3); }
   if (ragged) {
-    if (bp) KG_GEMM_F32(1, true); else KG_GEMM_F32(0, true);
+    if (bp) { KG_GEMM_F32_ST(1, true) } else { KG_GEMM_F32_ST(0, true) }
   } else {
-    if (bp) KG_GEMM_F32(1, false); else KG_GEMM_F32(0, false);
+    if (bp) { KG_GEMM_F32_ST(1, false) } else { KG_GEMM_F32_ST(0, false) }
   }
+#undef KG_GEMM_F32_ST
 #undef KG_GEMM_F32
   return finish_launch(ragged ? "matmul(f32-mfma-ragged)" : "matmul(f32-mfma)");
 }
@@ -454,9 +484,12 @@ int matmul_impl(const KgArgSlot* args, unsigned long long n) {
     }
   }
   long long stages = gemmp::kDefaultStages;  // LDS ring depth of the pipelined MFMA kernel
-  if (n == 8) {
+  long long stages_f32 = gemmf::kDefaultStages;  // and of the fp32 MFMA kernel
+  const bool staged = n == 8;
+  if (staged) {
     if ((rc = read_int(args, 7, "memory_stage", &stages))) return rc;
     if (stages < 2 || stages > 4) return fail(kInvalid, "matmul: memory_stage must be 2, 3 or 4, got %lld", stages);
+    stages_f32 = stages;
   }
   const long long M = lhs.shape[0], K = lhs.shape[1], N = rhs.shape[1];
   if (rhs.shape[0] != K) return fail(kInvalid, "matmul: lhs K=%lld != rhs K=%lld", K, rhs.shape[0]);
@@ -501,11 +534,17 @@ int matmul_impl(const KgArgSlot* args, unsigned long long n) {
   if (M == 0 || N == 0) return finish_launch("matmul(empty)");
 
   if (out.dtype == KG_DTYPE_F32) {
-    if (f32_mfma_ok) return launch_gemm_f32_mfma(out, lhs, rhs, bias, m, nn, k);
+    if (f32_mfma_ok) return launch_gemm_f32_mfma(out, lhs, rhs, bias, m, nn, k, (int)stages_f32);
+    if (staged)
+      return fail(kUnsupported, "matmul: memory_stage sets the LDS ring depth of the MFMA kernels; this fp32 call takes "
+                                "a kernel that loads its operands straight into registers");
     if (gemm_f32_splitk_ok(out, lhs, rhs, M, N, K) && (!bias.present || bias.stride[0] == 1))
       return launch_gemm_f32_splitk(out, lhs, rhs, bias, m, nn, k);
     return launch_gemm_simt<float, float>(out, lhs, rhs, bias, m, nn, k);
   }
+  if (staged && !mfma_ok)
+    return fail(kUnsupported, "matmul: memory_stage sets the LDS ring depth of the MFMA kernels; this call takes the "
+                              "SIMT kernel, which stages nothing through an LDS ring");
   if (out.dtype == KG_DTYPE_BF16) {
     if (mfma_ok) return launch_gemm_mfma<Bf16Tag>(out, lhs, rhs, bias, m, nn, k, (int)stages);
     if (bias.present && bias.dtype == KG_DTYPE_F32) return launch_gemm_simt<__bf16, float>(out, lhs, rhs, bias, m, nn, k);
@@ -531,7 +570,7 @@ int launch_conv_direct(const Mem& out, const Mem& x, const Mem& w, const Mem& bi
 
 int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
   if (args == nullptr) return fail(kInvalid, "ordered_args is null");
-  if (n != 12 && n != 17) return fail(kInvalid, "conv2d expects 12 or 17 slots, got %llu", n);
+  if (n != 12 && n != 17 && n != 18) return fail(kInvalid, "conv2d expects 12, 17 or 18 slots, got %llu", n);
   Mem out, x, w, bias;
   int rc;
   if ((rc = read_mem(args, 0, 4, false, "out", &out))) return rc;
@@ -546,13 +585,20 @@ int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
     if (p[i] <= 0) return fail(kInvalid, "conv2d: %s must be positive, got %lld", names[i], p[i]);
   for (int i = 4; i < 8; ++i)
     if (p[i] < 0) return fail(kInvalid, "conv2d: %s must be non-negative, got %lld", names[i], p[i]);
-  if (n == 17) {
+  if (n >= 17) {
     const char* tnames[5] = {"tile_f", "tile_c", "tile_n", "tile_ho", "tile_wo"};
     for (int i = 0; i < 5; ++i) {
       long long t;
       if ((rc = read_int(args, 12 + i, tnames[i], &t))) return rc;
       if (t <= 0) return fail(kInvalid, "conv2d: %s must be positive, got %lld", tnames[i], t);
     }
+  }
+  // slot 17: memory_stage, the LDS stage count of the row-piece and implicit-GEMM kernels
+  long long stages = 2;
+  const bool staged = n == 18;
+  if (staged) {
+    if ((rc = read_int(args, 17, "memory_stage", &stages))) return rc;
+    if (stages < 2 || stages > 4) return fail(kInvalid, "conv2d: memory_stage must be 2, 3 or 4, got %lld", stages);
   }
   if (!x.contiguous() || !w.contiguous() || !out.contiguous() || (bias.present && bias.stride[0] != 1))
     return fail(kInvalid, "conv2d: memory args must be contiguous");
@@ -588,7 +634,7 @@ int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
   if (bias.present && bias.shape[0] != w.shape[0]) return fail(kInvalid, "conv2d: bias extent != F");
   if (g_cost) {
     long long mfma = 0;
-    if (out.dtype != KG_DTYPE_F32 && conv_mfma_supported(s)) {  // live waves x 252 MFMAs per 7-row block
+    if (!staged && out.dtype != KG_DTYPE_F32 && conv_mfma_supported(s)) {  // live waves x 252 MFMAs per 7-row block
       mfma = (long long)s.n * ((s.h + convk::kRows - 1) / convk::kRows) * (s.w > 32 ? 4 : 2) * 252;
     } else if (conv_rowvec_supported(s, out.dtype == KG_DTYPE_F32)) {
       mfma = conv_rowvec_mfma(s, out.dtype == KG_DTYPE_F32);
@@ -607,7 +653,9 @@ int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
   }
   if (out.numel() == 0) return finish_launch("conv2d(empty)");
 
-  if (out.dtype == KG_DTYPE_F16 && conv_mfma_supported(s) && aligned16(x.data) && aligned16(w.data) && aligned16(out.data)) {
+  // The row-phase kernel stages its input rows in two fixed parts: a call that sets the
+  // stage count takes the row-piece kernel (which supports every shape the row-phase one does)
+  if (!staged && out.dtype == KG_DTYPE_F16 && conv_mfma_supported(s) && aligned16(x.data) && aligned16(w.data) && aligned16(out.data)) {
     const int bias_kind = !bias.present ? 0 : (bias.dtype == KG_DTYPE_F32 ? 1 : 2);
     hipError_t e = launch_conv2d_mfma<F16Tag>(static_cast<const uint16_t*>(x.data), static_cast<const uint16_t*>(w.data),
                                               static_cast<uint16_t*>(out.data), bias.present ? bias.data : nullptr,
@@ -615,7 +663,7 @@ int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
     if (e != hipSuccess) return fail(kHipFailure, "conv2d(mfma): %s", hipGetErrorString(e));
     return finish_launch("conv2d(mfma)");
   }
-  if (out.dtype == KG_DTYPE_BF16 && conv_mfma_supported(s) && aligned16(x.data) && aligned16(w.data) && aligned16(out.data)) {
+  if (!staged && out.dtype == KG_DTYPE_BF16 && conv_mfma_supported(s) && aligned16(x.data) && aligned16(w.data) && aligned16(out.data)) {
     const int bias_kind = !bias.present ? 0 : (bias.dtype == KG_DTYPE_F32 ? 1 : 2);
     hipError_t e = launch_conv2d_mfma<Bf16Tag>(static_cast<const uint16_t*>(x.data), static_cast<const uint16_t*>(w.data),
                                                static_cast<uint16_t*>(out.data), bias.present ? bias.data : nullptr,
@@ -625,9 +673,11 @@ int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
   }
   // split-K for conv grids of fewer than two workgroups per CU: fp32 partials in the
   // matmul's per-stream split-K workspace (no workspace: the whole K range in one pass)
+  SplitLease lease;  // held until both kernels of a split call are enqueued (this function's return)
   auto conv_partials = [&](int& splits) -> float* {
     if (splits <= 1) return nullptr;
-    float* ws = static_cast<float*>(split_workspace((size_t)splits * out.numel() * sizeof(float), g_stream));
+    lease = split_workspace((size_t)splits * out.numel() * sizeof(float), g_stream);
+    float* ws = static_cast<float*>(lease.ptr);
     if (ws == nullptr) splits = 1;
     return ws;
   };
@@ -639,7 +689,7 @@ int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
     hipError_t e = launch_conv2d_rowvec_f32(static_cast<const float*>(x.data), static_cast<const float*>(w.data),
                                             static_cast<float*>(out.data),
                                             bias.present ? static_cast<const float*>(bias.data) : nullptr,
-                                            bias.present ? 1 : 0, s, g_stream, partial, splits, kcs);
+                                            bias.present ? 1 : 0, s, g_stream, partial, splits, kcs, (int)stages);
     if (e != hipSuccess) return fail(kHipFailure, "conv2d(rowvec f32): %s", hipGetErrorString(e));
     return finish_launch("conv2d(rowvec f32)");
   }
@@ -654,8 +704,10 @@ int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
     int splits = conv_rowvec_splits(s, false, kSplitMaxWorkspace, &kcs);
     float* partial = conv_partials(splits);
     hipError_t e = out.dtype == KG_DTYPE_BF16
-                       ? launch_conv2d_rowvec<Bf16Tag>(xp, wp, yp, bp, bias_kind, s, g_stream, partial, splits, kcs)
-                       : launch_conv2d_rowvec<F16Tag>(xp, wp, yp, bp, bias_kind, s, g_stream, partial, splits, kcs);
+                       ? launch_conv2d_rowvec<Bf16Tag>(xp, wp, yp, bp, bias_kind, s, g_stream, partial, splits, kcs,
+                                                       (int)stages)
+                       : launch_conv2d_rowvec<F16Tag>(xp, wp, yp, bp, bias_kind, s, g_stream, partial, splits, kcs,
+                                                      (int)stages);
     if (e != hipSuccess) return fail(kHipFailure, "conv2d(rowvec): %s", hipGetErrorString(e));
     return finish_launch("conv2d(rowvec)");
   }
@@ -679,13 +731,19 @@ int conv2d_impl(const KgArgSlot* args, unsigned long long n) {
     float* partial = conv_partials(splits);
     hipError_t e =
         out.dtype == KG_DTYPE_F32
-            ? launch_conv2d_igemm<F32Tag>(x.data, w.data, out.data, bp, bias_kind, order, w_vec, s, g_stream, partial, splits, kcs)
+            ? launch_conv2d_igemm<F32Tag>(x.data, w.data, out.data, bp, bias_kind, order, w_vec, s, g_stream, partial,
+                                          splits, kcs, (int)stages)
         : out.dtype == KG_DTYPE_BF16
-            ? launch_conv2d_igemm<Bf16Tag>(x.data, w.data, out.data, bp, bias_kind, order, w_vec, s, g_stream, partial, splits, kcs)
-            : launch_conv2d_igemm<F16Tag>(x.data, w.data, out.data, bp, bias_kind, order, w_vec, s, g_stream, partial, splits, kcs);
+            ? launch_conv2d_igemm<Bf16Tag>(x.data, w.data, out.data, bp, bias_kind, order, w_vec, s, g_stream, partial,
+                                           splits, kcs, (int)stages)
+            : launch_conv2d_igemm<F16Tag>(x.data, w.data, out.data, bp, bias_kind, order, w_vec, s, g_stream, partial,
+                                          splits, kcs, (int)stages);
     if (e != hipSuccess) return fail(kHipFailure, "conv2d(igemm): %s", hipGetErrorString(e));
     return finish_launch("conv2d(igemm)");
   }
+  if (staged)
+    return fail(kUnsupported, "conv2d: memory_stage sets the LDS stage count of the row-piece and implicit-GEMM kernels; "
+                              "this shape takes the direct kernel, which stages nothing through LDS");
   const bool f32_bias = bias.present && bias.dtype == KG_DTYPE_F32;
   switch (out.dtype) {
     case KG_DTYPE_F32: return launch_conv_direct<float, float>(out, x, w, bias, s);
@@ -713,7 +771,8 @@ int launch_fa_simt(const Mem& out, const Mem& q, const Mem& k, const Mem& v, con
 
 int flash_attention_impl(const KgArgSlot* args, unsigned long long n) {
   if (args == nullptr) return fail(kInvalid, "ordered_args is null");
-  if (n != 4 && n != 6 && n != 8) return fail(kInvalid, "flash_attention expects 4, 6 or 8 slots, got %llu", n);
+  if (n != 4 && n != 6 && n != 8 && n != 9)
+    return fail(kInvalid, "flash_attention expects 4, 6, 8 or 9 slots, got %llu", n);
   Mem out, q, k, v;
   int rc;
   if ((rc = read_mem(args, 0, 4, false, "out", &out))) return rc;
@@ -728,7 +787,14 @@ int flash_attention_impl(const KgArgSlot* args, unsigned long long n) {
     if ((rc = read_int(args, 5, "bc", &bc))) return rc;
     if (br <= 0 || bc <= 0) return fail(kInvalid, "flash_attention: br/bc must be positive");
   }
-  if (n == 8) {
+  // slot 8: memory_stage, the K/V ring depth of the 16-bit MFMA kernel
+  long long stages = fa::kDefaultStages;
+  const bool staged = n == 9;
+  if (staged) {
+    if ((rc = read_int(args, 8, "memory_stage", &stages))) return rc;
+    if (stages < 2 || stages > 4) return fail(kInvalid, "flash_attention: memory_stage must be 2, 3 or 4, got %lld", stages);
+  }
+  if (n >= 8) {
     if ((rc = read_float(args, 6, "scale", &scale))) return rc;
     if ((rc = read_int(args, 7, "causal", &causal))) return rc;
     if (causal != 0 && causal != 1) return fail(kInvalid, "flash_attention: causal must be 0 or 1");
@@ -800,20 +866,26 @@ int flash_attention_impl(const KgArgSlot* args, unsigned long long n) {
     hipError_t e = out.dtype == KG_DTYPE_BF16
                        ? launch_fa_fwd_mfma<Bf16Tag>(static_cast<const uint16_t*>(q.data), static_cast<const uint16_t*>(k.data),
                                                      static_cast<const uint16_t*>(v.data), static_cast<uint16_t*>(out.data), s,
-                                                     g_stream)
+                                                     g_stream, (int)stages)
                        : launch_fa_fwd_mfma<F16Tag>(static_cast<const uint16_t*>(q.data), static_cast<const uint16_t*>(k.data),
                                                     static_cast<const uint16_t*>(v.data), static_cast<uint16_t*>(out.data), s,
-                                                    g_stream);
+                                                    g_stream, (int)stages);
     if (e != hipSuccess) return fail(kHipFailure, "flash_attention(mfma): %s", hipGetErrorString(e));
     return finish_launch("flash_attention(mfma)");
   }
   if (out.dtype == KG_DTYPE_F32 && fa_f32_mfma_supported(s) && aligned16(q.data) && aligned16(k.data) &&
       aligned16(v.data) && aligned16(out.data)) {
+    if (staged && stages != 2)
+      return fail(kUnsupported, "flash_attention: the fp32 MFMA kernel keeps two K and two V buffers, so memory_stage "
+                                "must be 2 for it, got %lld", stages);
     hipError_t e = launch_fa_fwd_f32_mfma(static_cast<const float*>(q.data), static_cast<const float*>(k.data),
                                           static_cast<const float*>(v.data), static_cast<float*>(out.data), s, g_stream);
     if (e != hipSuccess) return fail(kHipFailure, "flash_attention(f32-mfma): %s", hipGetErrorString(e));
     return finish_launch("flash_attention(f32-mfma)");
   }
+  if (staged)
+    return fail(kUnsupported, "flash_attention: memory_stage sets the K/V ring depth of the MFMA kernels; this call "
+                              "takes the SIMT kernel, which stages nothing through LDS");
   switch (out.dtype) {
     case KG_DTYPE_F32: return launch_fa_simt<float>(out, q, k, v, s);
     case KG_DTYPE_BF16: return launch_fa_simt<__bf16>(out, q, k, v, s);
@@ -884,84 +956,7 @@ int kg_gfx950_cost(int op, const KgArgSlot* ordered_args, unsigned long long arg
   return rc;
 }
 
-int kg_gfx950_abi_version(void) { return 2; }
+int kg_gfx950_abi_version(void) { return 3; }
 
-int kg_gfx950_mfma_rate(int dtype_code, int mfma_m, int zero_operands, int iterations, int workgroups, double* tflops,
-                        double* clock_ghz) {
-  if (dtype_code != KG_DTYPE_BF16 && dtype_code != KG_DTYPE_F16)
-    return fail(kInvalid, "mfma_rate: dtype must be bf16 or f16, got %s", dtype_name(dtype_code));
-  if (mfma_m != 32 && mfma_m != 16)
-    return fail(kInvalid, "mfma_rate: mfma_m must be 32 (32x32x16) or 16 (16x16x32), got %d", mfma_m);
-  if (iterations < 1 || iterations > (1 << 20) || workgroups < 1 || workgroups > (1 << 16))
-    return fail(kInvalid, "mfma_rate: iterations must be in [1, 2^20] and workgroups in [1, 65536]");
-  if (tflops == nullptr || clock_ghz == nullptr) return fail(kInvalid, "mfma_rate: null output");
-  // operands: N(0,1)*0.02 (Box-Muller on a fixed 64-bit LCG) rounded to the 16-bit format, or zeros
-  std::vector<uint16_t> host(kMfmaRateOperands * 8, 0);
-  if (!zero_operands) {
-    unsigned long long st = 0x9E3779B97F4A7C15ull;
-    auto uni = [&]() {
-      st = st * 6364136223846793005ull + 1442695040888963407ull;
-      return ((st >> 11) + 0.5) * (1.0 / 9007199254740992.0);
-    };
-    for (size_t i = 0; i < host.size(); ++i) {
-      const float v = (float)(0.02 * std::sqrt(-2.0 * std::log(uni())) * std::cos(6.283185307179586 * uni()));
-      uint32_t bits;
-      std::memcpy(&bits, &v, 4);
-      if (dtype_code == KG_DTYPE_BF16) {
-        host[i] = (uint16_t)((bits + 0x7fffu + ((bits >> 16) & 1u)) >> 16);
-      } else {
-        const _Float16 hv = (_Float16)v;
-        std::memcpy(&host[i], &hv, 2);
-      }
-    }
-  }
-  u32x4* d_ops = nullptr;
-  unsigned long long* d_times = nullptr;
-  float* d_sink = nullptr;
-  hipEvent_t e0 = nullptr, e1 = nullptr;
-  int rc = kOk;
-  auto check = [&](hipError_t e, const char* what) {
-    if (e != hipSuccess && rc == kOk) rc = fail(kHipFailure, "mfma_rate: %s: %s", what, hipGetErrorString(e));
-    return e == hipSuccess;
-  };
-  const size_t sink_n = (size_t)workgroups * kMfmaRateThreads;
-  if (check(hipMalloc(&d_ops, host.size() * 2), "hipMalloc") && check(hipMalloc(&d_times, (size_t)workgroups * 16), "hipMalloc") &&
-      check(hipMalloc(&d_sink, sink_n * 4), "hipMalloc") &&
-      check(hipMemcpy(d_ops, host.data(), host.size() * 2, hipMemcpyHostToDevice), "hipMemcpy") &&
-      check(hipEventCreate(&e0), "hipEventCreate") && check(hipEventCreate(&e1), "hipEventCreate")) {
-    auto launch = [&]() {
-      const bool bf = dtype_code == KG_DTYPE_BF16;
-      auto kernel = mfma_m == 32 ? (bf ? mfma_rate_kernel<Bf16Tag, 32> : mfma_rate_kernel<F16Tag, 32>)
-                                 : (bf ? mfma_rate_kernel<Bf16Tag, 16> : mfma_rate_kernel<F16Tag, 16>);
-      hipLaunchKernelGGL(kernel, dim3(workgroups), dim3(kMfmaRateThreads), 0, nullptr, d_ops, d_times, d_sink,
-                         iterations);
-      return hipGetLastError();
-    };
-    float ms = 0.f;
-    // two untimed launches (the clock settles under the load), then one timed
-    if (check(launch(), "launch") && check(launch(), "launch") && check(hipEventRecord(e0, nullptr), "hipEventRecord") &&
-        check(launch(), "launch") && check(hipEventRecord(e1, nullptr), "hipEventRecord") &&
-        check(hipEventSynchronize(e1), "hipEventSynchronize") && check(hipEventElapsedTime(&ms, e0, e1), "hipEventElapsedTime")) {
-      std::vector<unsigned long long> times((size_t)workgroups * 2);
-      if (check(hipMemcpy(times.data(), d_times, times.size() * 8, hipMemcpyDeviceToHost), "hipMemcpy")) {
-        std::vector<double> ghz;
-        for (int b = 0; b < workgroups; ++b)
-          if (times[2 * b + 1] > 0) ghz.push_back((double)times[2 * b] / (double)times[2 * b + 1] * 0.1);
-        std::sort(ghz.begin(), ghz.end());
-        *clock_ghz = ghz.empty() ? 0.0 : ghz[ghz.size() / 2];
-        const double flop_per_mfma = mfma_m == 32 ? 32768.0 : 16384.0;
-        const double flop = (double)workgroups * (kMfmaRateThreads / 64) * iterations * 8 * flop_per_mfma;
-        *tflops = ms > 0.f ? flop / (ms * 1e-3) / 1e12 : 0.0;
-      }
-    }
-  }
-  if (e0) (void)hipEventDestroy(e0);
-  if (e1) (void)hipEventDestroy(e1);
-  if (d_ops) (void)hipFree(d_ops);
-  if (d_times) (void)hipFree(d_times);
-  if (d_sink) (void)hipFree(d_sink);
-  if (rc == kOk) g_last_error[0] = '\0';
-  return rc;
-}
 
 }  // extern "C"

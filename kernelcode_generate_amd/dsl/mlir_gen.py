@@ -583,6 +583,17 @@ class _Builder:
             mem = self.new_mem((count,), src.dtype, src.space, "reshape", src)
             self.emit("dma.reshape", [src], {"shape": mem.shape}, mem)
             return mem
+        if name == "arch.barrier":
+            # each DSL block runs one DSL thread, and every operation ends with a workgroup
+            # barrier: the request is kept in the IR and costs one more barrier
+            unknown = set(kwargs) - {"visibility", "scope"}
+            if args or unknown:
+                raise _error("arch.barrier takes the keyword arguments visibility= and scope=", node)
+            self.emit("arch.barrier", [])
+            return None
+        if name in ("arch.get_dynamic_memory", "arch.launch_kernel"):
+            raise _error(f"{name} is not supported by the gfx950 front end: tiles are dma.alloc allocations in the "
+                         f"workgroup's workspace and a kernel is launched by its entry point", node)
         if name.startswith("arch.get_"):
             take(())
             query = name[len("arch.get_"):]

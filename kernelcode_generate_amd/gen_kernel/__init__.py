@@ -45,17 +45,24 @@ def _error(message: str) -> KernelCodeError:
 
 def library_slots(call: FusedCall, memory_stage: int | None = None) -> list:
     """The library entry's slot list as (kind, value): ("mem", param | None), ("int", Sym),
-    ("float", FVal). Matmul calls carry the loop tiles only when a memory_stage slot
-    follows (the entry's 8-slot form)."""
+    ("float", FVal). A memory_stage becomes the entry's trailing ring-depth slot: matmul
+    (out, lhs, rhs, bias, 3 tiles, stage), conv2d (out, x, w, bias, 8 geometry ints,
+    5 tiles, stage), flash attention (out, q, k, v, br, bc, scale, causal, stage); without
+    it matmul takes the 4-slot form and conv2d the 12-slot one."""
 
     slots: list = [("mem", name) for name in call.memory]
-    if call.family == "matmul" and memory_stage is not None:
-        tiles = call.ints if call.ints else (Sym.const(1),) * 3
-        slots += [("int", t) for t in tiles] + [("int", Sym.const(memory_stage))]
-    elif call.family != "matmul":
-        slots += [("int", e) for e in call.ints]
-        slots += [("float", v) for v in call.floats]
-        slots += [("int", e) for e in call.trailing_ints]
+    if call.family == "matmul":
+        if memory_stage is not None:
+            tiles = call.tiles or (Sym.const(1),) * 3
+            slots += [("int", t) for t in tiles] + [("int", Sym.const(memory_stage))]
+        return slots
+    slots += [("int", e) for e in call.ints]
+    if call.family == "conv2d" and memory_stage is not None:
+        slots += [("int", t) for t in (call.tiles or (Sym.const(1),) * 5)]
+    slots += [("float", v) for v in call.floats]
+    slots += [("int", e) for e in call.trailing_ints]
+    if memory_stage is not None:
+        slots.append(("int", Sym.const(memory_stage)))
     return slots
 
 

@@ -256,6 +256,9 @@ class _Emitter:
             # whole-tile copy; a cast rounds each element to the target type (to nearest even)
             L(f"{ind}kg_tile::copy({self.var(op.operands[0])}, {self.var(op.operands[1])}, {err});")
             return
+        if n == "arch.barrier":
+            L(f"{ind}kg_tile::sync();")
+            return
         if n == "dma.free":
             L(f"{ind}// dma.free({self.var(op.operands[0])}): workspace tiles live for the whole launch")
             return

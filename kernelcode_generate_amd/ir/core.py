@@ -12,6 +12,12 @@ tiles. Operation names and operand orders are the reference dialects' --
   dma.reshape       -> source with a new (contiguous) shape          (dma.py:1046)
   dma.slice         target <- source[offsets/sizes/strides]          (dma.py:945)
   dma.deslice       target[offsets/sizes/strides] <- source          (dma.py:978)
+  dma.load          target <- source[offsets/sizes/strides]          (dma.py:856)
+  dma.store         target[offsets/sizes/strides] <- source          (dma.py:894)
+  dma.copy          target <- source (whole tile)                    (dma.py:722)
+  dma.cast          target <- source rounded to target's element type (dma.py:1119)
+  dma.free          end of a tile's lifetime (no data effect)        (dma.py:198)
+  arch.barrier      block-level barrier request                      (arch.py:803)
   dma.broadcast     target <- source expanded along size-1 axes      (dma.py:833)
   dma.transpose     target <- permute(source)                        (nn/transpose.py:95)
   kernel.matmul     out (+)= lhs @ rhs, acc flag / condition          (structured.py:188-218)

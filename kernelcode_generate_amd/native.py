@@ -49,7 +49,6 @@ CONTROL_SYMBOLS = (
     "kg_gfx950_launch_stream",
     "kg_gfx950_launch_synchronous",
     "kg_gfx950_finish_launch",
-    "kg_gfx950_mfma_rate",
 )
 
 # kg_gfx950_cost: op codes (KG_OP_*) and the order of its output array (KG_COST_*).
@@ -120,9 +119,6 @@ def load_library() -> ctypes.CDLL:
     lib.kg_gfx950_cost.argtypes = [ctypes.c_int, ctypes.POINTER(KgArgSlot), ctypes.c_ulonglong,
                                    ctypes.POINTER(ctypes.c_longlong)]
     lib.kg_gfx950_cost.restype = ctypes.c_int
-    lib.kg_gfx950_mfma_rate.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                        ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
-    lib.kg_gfx950_mfma_rate.restype = ctypes.c_int
     _LIBRARY = lib
     return lib
 
@@ -247,29 +243,24 @@ def set_launch_mode(synchronous: bool, stream: int | None = None) -> None:
     load_library().kg_gfx950_set_launch_mode(1 if synchronous else 0, ctypes.c_void_p(stream or 0))
 
 
-def mfma_rate(dtype: str = "bf16", zero_operands: bool = False, iterations: int = 20000,
-              workgroups: int = 2048, mfma_m: int = 16) -> dict[str, float]:
-    """Sustained rate of v_mfma_f32_16x16x32 (mfma_m=16) or v_mfma_f32_32x32x16 (mfma_m=32)
-    with no operand movement (kg_gfx950_mfma_rate)."""
-
-    code = {"bf16": DTYPE_CODES["bfloat16"], "f16": DTYPE_CODES["float16"]}[dtype]
-    tf, ghz = ctypes.c_double(0.0), ctypes.c_double(0.0)
-    rc = load_library().kg_gfx950_mfma_rate(code, int(mfma_m), int(bool(zero_operands)), int(iterations),
-                                            int(workgroups), ctypes.byref(tf), ctypes.byref(ghz))
-    if rc != 0:
-        raise NativeLibraryError(f"kg_gfx950_mfma_rate failed: {last_error()}", rc)
-    return {"tflops": tf.value, "clock_ghz": ghz.value}
-
-
 def matmul(out, lhs, rhs, bias=None, *tiles: int) -> None:
     call_entry("kg_gfx950_matmul_entry", (out, lhs, rhs, bias, *tiles))
 
 
-def conv2d(out, x, weight, bias, stride=(1, 1), dilation=(1, 1), padding=(0, 0, 0, 0), tiles=()) -> None:
-    """padding = (top, bottom, left, right)."""
+def conv2d(out, x, weight, bias, stride=(1, 1), dilation=(1, 1), padding=(0, 0, 0, 0), tiles=(),
+           memory_stage: int | None = None) -> None:
+    """padding = (top, bottom, left, right); memory_stage: the LDS stage count (with 5 tiles)."""
 
-    call_entry("kg_gfx950_conv2d_entry", (out, x, weight, bias, *stride, *dilation, *padding, *tiles))
+    if memory_stage is not None and len(tiles) != 5:
+        tiles = (1, 1, 1, 1, 1)
+    stage = () if memory_stage is None else (int(memory_stage),)
+    call_entry("kg_gfx950_conv2d_entry", (out, x, weight, bias, *stride, *dilation, *padding, *tiles, *stage))
 
 
-def flash_attention(out, q, k, v, br: int = 64, bc: int = 64, scale: float = 1.0, causal: bool = False) -> None:
-    call_entry("kg_gfx950_flash_attention_entry", (out, q, k, v, int(br), int(bc), float(scale), int(bool(causal))))
+def flash_attention(out, q, k, v, br: int = 64, bc: int = 64, scale: float = 1.0, causal: bool = False,
+                    memory_stage: int | None = None) -> None:
+    """memory_stage: the K/V ring depth of the MFMA kernel (2, 3 or 4)."""
+
+    stage = () if memory_stage is None else (int(memory_stage),)
+    call_entry("kg_gfx950_flash_attention_entry",
+               (out, q, k, v, int(br), int(bc), float(scale), int(bool(causal)), *stage))

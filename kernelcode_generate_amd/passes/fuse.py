@@ -54,6 +54,7 @@ class FusedCall:
     floats: tuple[FVal, ...] = ()        # FLOAT slots (attention scale)
     trailing_ints: tuple[Sym, ...] = ()  # INT slots after the floats (attention causal flag)
     notes: tuple[str, ...] = field(default_factory=tuple)
+    tiles: tuple[Sym, ...] = ()          # the nest's tile steps (the entry's optional tile slots)
 
 
 class _NoMatch(Exception):
@@ -132,7 +133,7 @@ class _Output:
 
 
 def _destination(op: Op) -> Mem | None:
-    if op.name in ("dma.alloc", "dma.view", "dma.reshape", "dma.free", "symbol.for", "scf.if"):
+    if op.name in ("dma.alloc", "dma.view", "dma.reshape", "dma.free", "arch.barrier", "symbol.for", "scf.if"):
         return None
     return op.operands[0] if op.operands else None
 
@@ -208,7 +209,7 @@ class _Tracer:
         n, a = op.name, op.attrs
         if n == "dma.alloc":
             env[id(op.result)] = Val("undef", shape=op.result.shape)
-        elif n in ("dma.view", "dma.reshape", "dma.free"):
+        elif n in ("dma.view", "dma.reshape", "dma.free", "arch.barrier"):
             pass
         elif n == "dma.fill":
             t = op.operands[0]
@@ -713,8 +714,8 @@ def match_matmul(tracer: _Tracer) -> FusedCall:
                         _req(_is_const(ra, 0.0) or _is_const(rb, 0.0), "zero-padded K tail")
 
     m.verify(check, "matmul")
-    return FusedCall("matmul", (out.arg.name, a_arg, b_arg, bias),
-                     ints=(mloop.attrs["step"], nloop.attrs["step"], kloop.attrs["step"]))
+    steps = (mloop.attrs["step"], nloop.attrs["step"], kloop.attrs["step"])
+    return FusedCall("matmul", (out.arg.name, a_arg, b_arg, bias), ints=steps, tiles=steps)
 
 
 # ---------------------------------------------------------------------------------------
@@ -838,7 +839,9 @@ def match_conv2d(tracer: _Tracer) -> FusedCall:
     # bottom / right pads: the least that give the loops' Ho / Wo (larger ones change nothing)
     pad_b = smax((Ho - 1) * sh + dh * (kh - 1) + 1 - H - pad_t, 0)
     pad_r = smax((Wo - 1) * sw + dw * (kw - 1) + 1 - W - pad_l, 0)
-    return FusedCall("conv2d", (out.arg.name, x_arg, w_arg, bias), ints=(sh, sw, dh, dw, pad_t, pad_b, pad_l, pad_r))
+    tile_n = img_loops[0].attrs["step"] if len(img_loops) == 2 else one
+    return FusedCall("conv2d", (out.arg.name, x_arg, w_arg, bias), ints=(sh, sw, dh, dw, pad_t, pad_b, pad_l, pad_r),
+                     tiles=(floop.attrs["step"], cloop.attrs["step"], tile_n, hloop.attrs["step"], wloop.attrs["step"]))
 
 
 # ---------------------------------------------------------------------------------------
@@ -1012,7 +1015,7 @@ def match_flash_attention(tracer: _Tracer) -> FusedCall:
     _req(full_kv or causal is True, "keys past the query block are skipped only under a causal mask")
     return FusedCall("flash_attention", (out.arg.name, qa, ka, va), ints=(br, bc), floats=(scale,),
                      trailing_ints=(Sym.const(1 if causal else 0),),
-                     notes=("causal lower-triangular mask" if causal else "no mask",))
+                     notes=("causal lower-triangular mask" if causal else "no mask",), tiles=(br, bc))
 
 
 MATCHERS = (("matmul", match_matmul), ("conv2d", match_conv2d), ("flash_attention", match_flash_attention))

@@ -8,9 +8,13 @@ It runs on the kernel IR the front end builds (dsl.mlir_gen) and applies, in ord
                                        (kernel_gen/passes/kernel/kernel_aggregate.py:292)
   kernel-pattern-fuse                  map a recognised loop nest onto a hand-written
                                        gfx950 kernel (passes/fuse.py)
-  multi-buffer{memory-stage=N}         (option) the LDS ring depth of the fused GEMM, the
-                                       gfx950 reading of MultiBufferAnalysisPass's
-                                       memory_stage (kernel_gen/passes/memory/multi_buffer.py)
+  multi-buffer{memory-stage=N}         (option) the LDS ring depth of the fused kernel (the
+                                       GEMMs' operand rings, attention's K/V rings, the
+                                       conv kernels' stage count), the gfx950 reading of
+                                       MultiBufferAnalysisPass's memory_stage
+                                       (kernel_gen/passes/memory/multi_buffer.py); a kernel
+                                       the call selects that cannot take it fails with an
+                                       error naming it
   arch-parallelize{target=gfx950}      the per-operation path's grid: the leading
                                        perfectly nested loops (arch_parallelize.py:637-680)
   attach-arch-information{target=gfx950}  the target's hardware description
@@ -20,7 +24,7 @@ registers itself, and the per-operation path sizes its tiles' workspace in the e
 LoopSoftPipelinePass's prologue / steady loop / epilogue is what every hand-written
 kernel already does, so that pass has no knob here.
 
-Options: ``target`` (gfx950), ``memory_stage`` (2, 3 or 4; fused matmul only) and
+Options: ``target`` (gfx950), ``memory_stage`` (2, 3 or 4; fused kernels) and
 ``fuse`` (default true; false keeps every kernel on the per-operation path).
 """
 
@@ -98,8 +102,10 @@ def _pattern_fuse(state: LoweredKernel) -> LoweredKernel:
 
 def _multi_buffer(stage: int) -> Callable[[LoweredKernel], LoweredKernel]:
     def run(state: LoweredKernel) -> LoweredKernel:
-        if state.fused is None or state.fused.family != "matmul":
-            return state  # like the reference pass on IR it cannot ring: left alone
+        if state.fused is None:
+            # per-operation kernels stage nothing through LDS: like the reference pass on
+            # IR it cannot ring, left alone
+            return state
         return replace(state, memory_stage=stage)
 
     return run

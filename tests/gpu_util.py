@@ -94,10 +94,12 @@ def attention_h16_tolerance(q, k, v, scale=None, causal=False, dtype_name="bfloa
     of the output's own: P is rounded to the 16-bit format (P_j (1 + d_j), |d_j| <= u, the
     unit roundoff of round-to-nearest: 2^-8 for bf16's 8-bit significand, 2^-11 for f16's 11
     bits) before the P V product, and the row sum uses the same rounded P, so
-    O_i = sum_j w~_j V_j moves by exactly sum_j w_j (d_j - mean d) V_j =
-    sum_j w_j d_j (V_j - O_i) to first order: at most u ((W |V|)_id + |O_id|). The rms
-    term alone is too tight for short causal rows (row i averages i + 1 keys with large
-    weights), where this term dominates. Float64 from the inputs."""
+    O_i = sum_j w~_j V_j moves by sum_j w_j d_j (V_j - O_i) to first order. The d_j are
+    rounding errors of different values, taken as independent with mean 0 (|d_j| <= u,
+    variance at most u^2 / 3): the probabilistic bound with the usual factor of 4 standard
+    deviations is 4 u sqrt(sum_j w_j^2 (V_j - O_i)^2). That term covers short causal rows
+    (row i averages i + 1 keys with large weights, where the rms term alone is too tight)
+    and shrinks on long rows like 1 / sqrt(keys). Float64 from the inputs."""
 
     q = np.asarray(q, np.float64)
     k = np.asarray(k, np.float64)
@@ -112,7 +114,10 @@ def attention_h16_tolerance(q, k, v, scale=None, causal=False, dtype_name="bfloa
     o = w @ v
     rms = float(np.sqrt(np.mean(o * o))) if o.size else 0.0
     u = {"bfloat16": 2.0 ** -8, "float16": 2.0 ** -11}[dtype_name]
-    return H16_ATOL_RMS * rms + H16_RTOL * np.abs(o) + u * (w @ np.abs(v) + np.abs(o))
+    w2 = w * w
+    # sum_j w_j^2 (V_j - O)^2 = W2 V^2 - 2 O (W2 V) + O^2 (W2 1), clipped at 0 against cancellation
+    spread = np.maximum(w2 @ (v * v) - 2 * o * (w2 @ v) + o * o * w2.sum(-1, keepdims=True), 0.0)
+    return H16_ATOL_RMS * rms + H16_RTOL * np.abs(o) + 4 * u * np.sqrt(spread)
 
 
 def assert_within(out, ref, atol, what: str = "") -> None:

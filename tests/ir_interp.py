@@ -124,7 +124,7 @@ def _run(block: list[Op], env: _Env) -> None:
             if n == "dma.cast" and op.operands[0].dtype == "bf16":
                 v = bf16_round(v)
             _store(mems[0], v)
-        elif n == "dma.free":
+        elif n in ("dma.free", "arch.barrier"):
             pass
         elif n in ("dma.deslice", "dma.store"):
             region = _region(mems[0], [env.sym(x) for x in a["offsets"]], [env.sym(x) for x in a["sizes"]],

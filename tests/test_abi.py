@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
     lib = native.load_library()
     for name in declared_functions():
         assert hasattr(lib, name), name
-    assert lib.kg_gfx950_abi_version() == 2
+    assert lib.kg_gfx950_abi_version() == 3
 
 
 def test_slot_layout_matches_reference():
@@ -72,17 +72,20 @@ def test_wrong_slot_kind_is_rejected_without_gpu():
     assert "expected memory slot" in native.last_error()
 
 
-def test_mfma_rate_rejects_bad_arguments():
-    """kg_gfx950_mfma_rate validates before touching the GPU: no device is needed here."""
+def test_mfma_rate_probe_rejects_bad_arguments():
+    """bench.py's probe library (libkg_gfx950_probe.so, not the product library) validates
+    before touching the GPU: no device is needed here."""
     import ctypes
 
-    from kernelcode_generate_amd import native
+    import bench
 
-    lib = native.load_library()
+    lib = bench.probe_library()
     tf, ghz = ctypes.c_double(0.0), ctypes.c_double(0.0)
-    assert lib.kg_gfx950_mfma_rate(1, 16, 0, 10, 4, ctypes.byref(tf), ctypes.byref(ghz)) == -1  # fp32: not 16-bit
-    assert "bf16 or f16" in native.last_error()
-    assert lib.kg_gfx950_mfma_rate(6, 8, 0, 10, 4, ctypes.byref(tf), ctypes.byref(ghz)) == -1
-    assert "mfma_m" in native.last_error()
-    assert lib.kg_gfx950_mfma_rate(6, 32, 0, 0, 4, ctypes.byref(tf), ctypes.byref(ghz)) == -1
-    assert lib.kg_gfx950_mfma_rate(6, 16, 0, 10, 1 << 17, ctypes.byref(tf), ctypes.byref(ghz)) == -1
+    rate = lib.kg_gfx950_probe_mfma_rate
+    assert rate(1, 16, 0, 10, 4, ctypes.byref(tf), ctypes.byref(ghz)) == -1  # fp32: not 16-bit
+    assert b"bf16" in lib.kg_gfx950_probe_last_error()
+    assert rate(6, 8, 0, 10, 4, ctypes.byref(tf), ctypes.byref(ghz)) == -1
+    assert b"mfma_m" in lib.kg_gfx950_probe_last_error()
+    assert rate(6, 32, 0, 0, 4, ctypes.byref(tf), ctypes.byref(ghz)) == -1
+    assert rate(6, 16, 0, 10, 1 << 17, ctypes.byref(tf), ctypes.byref(ghz)) == -1
+    assert not hasattr(native.load_library(), "kg_gfx950_mfma_rate")

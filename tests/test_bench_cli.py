@@ -21,7 +21,10 @@ def test_more_than_one_gpu_is_refused_with_a_message():
     assert r.stdout == ""
 
 
-def test_zero_operands_only_for_analysis_runs():
-    r = _run("--operands", "zeros")
-    assert r.returncode == 2
-    assert "analysis mode" in r.stderr
+def test_analysis_modes_are_not_part_of_the_bench():
+    """The bench measures the BASELINE workloads only: the operand and library-comparison
+    analysis switches are not accepted (argparse refuses unknown options with status 2)."""
+
+    for flag in ("--operands", "--vs-library", "--mfma-ceiling"):
+        r = _run(flag)
+        assert r.returncode == 2 and "unrecognized arguments" in r.stderr, flag

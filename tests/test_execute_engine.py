@@ -252,9 +252,11 @@ def test_dsl_run_contract_checks():
         restore_config(snap)
 
 
-def test_memory_stage_option_drives_matmul_ring_depth():
+def test_memory_stage_option_drives_every_fused_ring_depth():
     """memory_stage (MultiBufferAnalysisPass's option, kernel_gen/passes/memory/multi_buffer.py)
-    reaches the matmul entry as a trailing INT slot; conv2d and attention are left alone."""
+    reaches each fused entry as its trailing INT slot: matmul slot 7, attention slot 8 (after
+    the causal flag), conv2d slot 17 (after the nest's five tile steps); a per-operation
+    kernel, which stages nothing through LDS, is left alone."""
 
     pm = get_pipeline("gfx950-lowering", {"memory_stage": "3"})
     b16 = T((256, 256), "bfloat16")
@@ -265,9 +267,16 @@ def test_memory_stage_option_drives_matmul_ring_depth():
         assert "slots[7].int_value = 3LL;" in src and "kg_gfx950_matmul_entry(slots, 8ULL)" in src
     x = T((1, 2, 64, 64), "bfloat16")
     fa = pm.run(mlir_gen(flash_attention_scaled_causal_kernel, (x, x, x, x, 64, 64, 0.1)))
-    assert fa.memory_stage is None
+    assert fa.memory_stage == 3
+    src = gen_kernel(fa)
+    assert "slots[8].int_value = 3LL;" in src and "kg_gfx950_flash_attention_entry(slots, 9ULL)" in src
     conv = pm.run(mlir_gen(conv2d_inputs_static_tile_static_kernel, (_X4, _X4, _X4, None)))
-    assert conv.memory_stage is None
+    assert conv.memory_stage == 3
+    src = gen_kernel(conv)
+    assert "slots[17].int_value = 3LL;" in src and "kg_gfx950_conv2d_entry(slots, 18ULL)" in src
+    assert "slots[12].int_value = 7LL;" in src  # the static demo's filter tile step
+    per_op = get_pipeline("gfx950-lowering", {"memory_stage": "3", "fuse": "false"})
+    assert per_op.run(mlir_gen(flash_attention_scaled_causal_kernel, (x, x, x, x, 64, 64, 0.1))).memory_stage is None
     for bad in ("1", "5", "two"):
         with pytest.raises(KernelCodeError):
             build_gfx950_lowering_pipeline({"memory_stage": bad})
@@ -279,9 +288,15 @@ def test_memory_stage_slot_validated_without_gpu():
 
     base = [T((256, 256), "bfloat16"), T((256, 64), "bfloat16"), T((64, 256), "bfloat16"), None, 64, 64, 64]
     assert native.cost("matmul", base + [2])["MAC"] == 256 * 256 * 64
-    for bad in (1, 5):
-        with pytest.raises(native.NativeLibraryError, match="memory_stage"):
-            native.cost("matmul", base + [bad])
+    x = T((1, 2, 128, 64), "bfloat16")
+    fa = [x, x, x, x, 64, 64, 0.125, 0]
+    c = T((1, 8, 16, 16), "float16")
+    conv = [c, c, T((8, 8, 3, 3), "float16"), None, 1, 1, 1, 1, 1, 1, 1, 1, 8, 8, 1, 8, 8]
+    for family, args in (("matmul", base), ("flash_attention", fa), ("conv2d", conv)):
+        assert native.cost(family, args + [4])["MAC"] > 0
+        for bad in (1, 5):
+            with pytest.raises(native.NativeLibraryError, match="memory_stage"):
+                native.cost(family, args + [bad])
     assert lib is not None
 
 

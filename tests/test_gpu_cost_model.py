@@ -66,11 +66,14 @@ def test_cost_model_against_the_gpu(device, case):
 
 @pytest.mark.gpu
 def test_mfma_rate_measures_the_matrix_cores(device):
-    """kg_gfx950_mfma_rate: a short run gives a rate below the nominal dense peak and above a
-    tenth of it, for both MFMA shapes and both operand kinds, and a clock within the part's range."""
+    """bench.py's MFMA-rate probe (its own library, not the product's): a short run gives a
+    rate below the nominal dense peak and above a tenth of it, for both MFMA shapes and both
+    operand kinds, and a clock within the part's range."""
+    import bench
+
     for mfma_m in (16, 32):
         for zeros in (False, True):
-            r = native.mfma_rate("bf16", zeros, iterations=2000, workgroups=1024, mfma_m=mfma_m)
+            r = bench.mfma_rate("bf16", zeros, iterations=2000, workgroups=1024, mfma_m=mfma_m)
             print(f"[mfma_rate] m={mfma_m} zeros={zeros}: {r['tflops']:.0f} TFLOP/s at {r['clock_ghz']:.2f} GHz",
                   flush=True)
             assert 0.1 * 2516.6 < r["tflops"] < 2516.6
