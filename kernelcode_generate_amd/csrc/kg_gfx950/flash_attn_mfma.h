@@ -384,9 +384,12 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
     constexpr bool kNext = decltype(next_tag)::value != 0;
     const bool copy_k2 = j + kStages < ntiles;      // K(j+S) exists (only if kNext)
     const bool copy_v1 = kStages == 2 || j + kStages - 1 < ntiles;  // V(j+S-1) exists
-    const uint32_t kb_next = (kStages == 2 ? (par ^ 1) : (j + 1) % kStages) * TB;  // K(j+1)
+    // ring buffers: with two they are immediates; deeper rings keep the fragment addresses
+    // k_rd / v_rd on K(j+1)'s and V(j)'s buffers (advanced at the end of each iteration),
+    // and only the copies' destinations (wave-uniform) are computed here
+    const uint32_t kb_next = kStages == 2 ? (par ^ 1) * TB : 0;                    // K(j+1)
     const uint32_t kb_copy = (kStages == 2 ? par : j % kStages) * TB;              // K(j+S): where K(j) was
-    const uint32_t vb_cur = (kStages == 2 ? par : j % kStages) * TB;               // V(j)
+    const uint32_t vb_cur = kStages == 2 ? par * TB : 0;                            // V(j)
     const uint32_t vb_copy = (kStages == 2 ? (par ^ 1) : (j + kStages - 1) % kStages) * TB;  // V(j+S-1)
     rescale(tail_tag);
     if constexpr (!kNext) {
@@ -473,6 +476,15 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
         for (int k = 0; k < 16; ++k) max_op(sn, k >> 3, k & 7, mx[k >> 3]);
       }
       tile_max(mx);
+      if constexpr (kStages != 2) {
+        // next iteration reads K(j+2) and V(j+1): one buffer on, wrapping at the ring's end
+        const uint32_t k_step = (j + 2) % kStages == 0 ? (uint32_t)(-(kStages - 1) * TB) : (uint32_t)TB;
+        const uint32_t v_step = (j + 1) % kStages == 0 ? (uint32_t)(-(kStages - 1) * TB) : (uint32_t)TB;
+#pragma unroll
+        for (int s = 0; s < NDS; ++s) k_rd[s] += k_step;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) v_rd[db] += v_step;
+      }
       if constexpr (kStages == 2) {
         wait_and_barrier<0>();
       } else {
@@ -503,6 +515,10 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
 #pragma unroll
     for (int k = 0; k < 16; ++k) max_op(sa, k >> 3, k & 7, mx[k >> 3]);
     tile_max(mx);
+  }
+  if constexpr (kStages != 2) {
+#pragma unroll
+    for (int s = 0; s < NDS; ++s) k_rd[s] += TB;  // iteration 0 reads K(1) from buffer 1
   }
   wait_and_barrier<0>();  // every wave is done with K(0) before K(S) replaces it
 
