@@ -1,0 +1,272 @@
+// gemm_quad_kernel: bf16/f16 GEMM for whole 256 x 256 tiles (M % 256 == 0, N % 256 == 0,
+// K % 32 == 0), four waves per workgroup, one per SIMD, each computing a 128 x 128 quarter
+// of the tile with v_mfma_f32_16x16x32 and its 256 fp32 accumulators per lane held in the
+// accumulation registers.
+//
+// Against gemm_pipe_kernel (eight waves of 128 x 64) a wave reads 16 KiB of fragments per
+// 64 MFMAs instead of 12 KiB per 32: two thirds of the LDS read bytes per MFMA. The LDS
+// ring, the copy path (global_load_lds_dwordx4, 1 KiB per wave per copy), the operand
+// layouts and the chunk swizzles are gemm_pipe_kernel's (gemmp::a_slot / gemmp::b_slot).
+// With one wave per SIMD no second wave covers a stall, so the slice is software-pipelined
+// in full: slice kt's 64 MFMAs run from registers while slice kt+1's 24 fragment reads and
+// slice kt+kStages's 8 copies are slotted between them; one barrier per slice, at its start,
+// publishes slice kt+1's copies and frees slice kt's stage for its refill.
+#pragma once
+
+#include "common.h"
+#include "gemm.h"
+#include "lds_dma.h"
+
+namespace kg_gfx950 {
+
+// f(Int<0>{}), f(Int<1>{}), ..., f(Int<N-1>{}), expanded at compile time.
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(Int<I>{});
+    static_for<N, I + 1>(f);
+  }
+}
+
+namespace gemmq {
+// acc += a * b on one 16 x 16 block, the accumulator tied to one register tuple of the
+// accumulation file for the whole kernel (with the intrinsic, the register allocator
+// rotates the 256 live accumulators through the full file with moves at every loop edge).
+// Being opaque to the compiler's hazard tracking, the caller waits for the last one to
+// finish before reading any accumulator (mfma_drain).
+template <typename Tag>
+__device__ __forceinline__ void mfma16_tied(f32x4& acc, u32x4 a, u32x4 b) {
+  if constexpr (__is_same(Tag, Bf16Tag))
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+  else
+    asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+// 32 wait states: more than the 16x16x32 MFMA's result latency, before VALU reads of its result.
+__device__ __forceinline__ void mfma_drain() { asm volatile("s_nop 15\n\ts_nop 15" ::: "memory"); }
+constexpr int kT = 256;        // tile rows and columns
+constexpr int kBK = 32;        // K slice
+constexpr int kThreads = 256;  // 4 waves
+constexpr int kVecs = kT * kBK / 8;  // u32x4 per operand per stage (16 KiB)
+constexpr int kPieces = 8;     // copies per wave per slice: 4 lhs (16 rows each), 4 rhs (2 k-rows each)
+constexpr int kDefaultStages = 4;
+}  // namespace gemmq
+
+template <typename Tag, int kBias, int kStages>
+__global__ __launch_bounds__(gemmq::kThreads, 1) void gemm_quad_kernel(
+    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, uint16_t* __restrict__ C,
+    const void* __restrict__ bias, int M, int N, int K, long long lda, long long ldb, long long ldc) {
+  using namespace gemmq;
+  using gemmp::a_mask;
+  using gemmp::a_slot;
+  using gemmp::b_mask;
+  using gemmp::b_slot;
+  using H = Half16<Tag>;
+  static_assert(kStages >= 2 && kStages <= 5, "ring depth");
+  __shared__ u32x4 lds_a[kStages][kVecs];
+  __shared__ u32x4 lds_b[kStages][kVecs];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1;  // 128-row half of the tile
+  const int wn = wave & 1;   // 128-column half
+
+  const int tiles_n = N / kT;
+  const int tiles_m = M / kT;
+  const int logical = xcd_logical_id(blockIdx.x, gridDim.x);
+  constexpr int kGroupM = 4;
+  const int group_size = kGroupM * tiles_n;
+  const int group = logical / group_size;
+  const int first_m = group * kGroupM;
+  const int gm = min(tiles_m - first_m, kGroupM);
+  const int in_group = logical - group * group_size;
+  const int m0 = (first_m + in_group % gm) * kT;
+  const int n0 = (in_group / gm) * kT;
+
+  // ---- HBM -> LDS copies: piece p < 4 is lhs rows (wave*4+p)*16 + lane/4 (the swizzle
+  // depends on lane/16 only), piece 4+i is rhs k-rows (wave*4+i)*2 + lane/32 ----
+  const int a_row0 = wave * 64 + (lane >> 2);
+  const uint32_t a_goff = (uint32_t)((a_row0 * lda + 8 * ((lane & 3) ^ a_mask(a_row0))) * 2);
+  uint32_t b_goff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int k = (wave * 4 + i) * 2 + (lane >> 5);
+    b_goff[i] = (uint32_t)((k * ldb + 8 * ((lane & 31) ^ b_mask(k))) * 2);
+  }
+  const char* a_tile = reinterpret_cast<const char*>(A + (long long)m0 * lda);
+  const char* b_tile = reinterpret_cast<const char*>(B + n0);
+  const long long a_piece = 16 * lda * 2;
+  const long long b_step = (long long)kBK * ldb * 2;
+  const uint32_t lds_a0 = lds_addr(&lds_a[0][0]);
+  const uint32_t lds_b0 = lds_addr(&lds_b[0][0]);
+  constexpr uint32_t kStage = kVecs * 16;
+
+  auto issue_piece = [&](int kt, int s, int piece) {
+    if (piece < 4) {
+      g2lds16_s(a_goff, a_tile + (long long)kt * kBK * 2 + piece * a_piece,
+                lds_a0 + s * kStage + (wave * 4 + piece) * 1024);
+    } else {
+      const int i = piece - 4;
+      g2lds16_s(b_goff[i], b_tile + kt * b_step, lds_b0 + s * kStage + (wave * 4 + i) * 1024);
+    }
+  };
+
+  // ---- fragments: lhs block ib = rows wm*128 + 16 ib + lane%16, chunk lane/16 (one
+  // ds_read_b128; +1024 bytes per block); rhs block nb = columns wn*128 + 16 nb + lane%16,
+  // k-rows 8(lane/16) + 0..7 in two ds_read_b64_tr_b16 (+2048 bytes for k-rows +4) ----
+  const int l16 = lane & 15;
+  const int lg = lane >> 4;
+  const uint32_t a_rd = lds_a0 + a_slot(wm * 128 + l16, lg) * 16;
+  uint32_t b_rd[8];
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) {
+    const int n = wn * 128 + nb * 16 + 4 * (l16 & 3);
+    b_rd[nb] = lds_b0 + b_slot(8 * lg + (l16 >> 2), n >> 3) * 16 + (n & 7) * 2;
+  }
+  struct Frags {
+    u32x4 a[8];
+    u32x4 b[8];
+  };
+  auto read_b = [&](int s, u32x4& f, int nb) {
+    const uint32_t ad = b_rd[nb] + s * kStage;
+    const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(uintptr_t)ad);
+    const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4*)(uintptr_t)(ad + 2048));
+    const u32x2 w0 = __builtin_bit_cast(u32x2, v0), w1 = __builtin_bit_cast(u32x2, v1);
+    f = u32x4{w0[0], w0[1], w1[0], w1[1]};
+  };
+  auto read_a = [&](int s, int ib) -> u32x4 {
+    return *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(a_rd + s * kStage + ib * 1024);
+  };
+  // read step r (0..15): the rhs blocks first (the next slice's first eight MFMAs use lhs
+  // block 0 with rhs blocks 0..7), then the lhs blocks
+  auto read_step = [&](int s, Frags& f, int r) {
+    if (r < 8) read_b(s, f.b[r], r);
+    else f.a[r - 8] = read_a(s, r - 8);
+  };
+
+  f32x4 acc[8][8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[i][j][e] = 0.f;
+
+  const int ktiles = K / kBK;
+#pragma unroll
+  for (int st = 0; st < kStages; ++st)
+    if (st < ktiles)
+#pragma unroll
+      for (int piece = 0; piece < kPieces; ++piece) issue_piece(st, st, piece);
+  {
+    const int younger = min(kStages - 1, ktiles - 1);
+    if (younger >= 4) wait_and_barrier<4 * kPieces>();
+    else if (younger == 3) wait_and_barrier<3 * kPieces>();
+    else if (younger == 2) wait_and_barrier<2 * kPieces>();
+    else if (younger == 1) wait_and_barrier<kPieces>();
+    else wait_and_barrier<0>();
+  }
+  Frags fr[2];  // slice kt's fragments are fr[kt & 1]; the next slice's are read into the other
+#pragma unroll
+  for (int r = 0; r < 16; ++r) read_step(0, fr[0], r);
+
+  // One slice in stage S: wait for slice kt+1's copies and meet the other waves (slice kt's
+  // stage is then free), then the 64 MFMAs with slice kt+1's 16 fragment reads (24 LDS
+  // instructions) on the even steps up to 32 and slice kt+kStages's 8 copies on every
+  // eighth step. kSteady: more slices follow and a refill is due.
+  auto slice = [&](int kt, auto stage_tag, auto par_tag, auto steady_tag) {
+    constexpr int S = decltype(stage_tag)::value;
+    constexpr int P = decltype(par_tag)::value;
+    constexpr bool kSteady = decltype(steady_tag)::value != 0;
+    Frags& fx = fr[P];
+    Frags& fn = fr[P ^ 1];
+    const bool more = kSteady || kt + 1 < ktiles;
+    const bool refill = kSteady || kt + kStages < ktiles;
+    if (kSteady) {
+      wait_and_barrier<(kStages - 2) * kPieces>();
+    } else if (more) {
+      const int younger = min(kStages - 2, ktiles - 2 - kt);
+      if (younger >= 3) wait_and_barrier<3 * kPieces>();
+      else if (younger == 2) wait_and_barrier<2 * kPieces>();
+      else if (younger == 1) wait_and_barrier<kPieces>();
+      else wait_and_barrier<0>();
+    }
+#pragma unroll
+    for (int idx = 0; idx < 64; ++idx) {
+      const int i = idx >> 3, j = idx & 7;
+      mfma16_tied<Tag>(acc[i][j], fx.b[j], fx.a[i]);  // C^T blocks: lane-contiguous columns
+      if (kSteady) {
+        if ((idx & 1) == 0 && idx < 32) read_step((S + 1) % kStages, fn, idx >> 1);
+        if ((idx & 7) == 3) issue_piece(kt + kStages, S, idx >> 3);
+      } else {
+        if ((idx & 1) == 0 && idx < 32 && more) read_step((S + 1) % kStages, fn, idx >> 1);
+        if ((idx & 7) == 3 && refill) issue_piece(kt + kStages, S, idx >> 3);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // Slices are unrolled U at a time (a compile-time loop: `#pragma unroll` gives up on the
+  // larger bodies) so that each one's stage (kt % kStages) and register set (kt & 1) are
+  // constants.
+  constexpr int U = kStages % 2 == 0 ? kStages : 2 * kStages;
+  auto unrolled = [&](int kt0, auto steady_tag) {
+    static_for<U>([&](auto u_tag) {
+      constexpr int u = decltype(u_tag)::value;
+      if (decltype(steady_tag)::value || kt0 + u < ktiles)
+        slice(kt0 + u, gemmp::StageIdx<u % kStages>{}, gemmp::StageIdx<u & 1>{}, steady_tag);
+    });
+  };
+  int kt = 0;
+  for (; kt + U + kStages <= ktiles; kt += U) unrolled(kt, gemmp::StageIdx<1>{});
+  for (; kt < ktiles; kt += U) unrolled(kt, gemmp::StageIdx<0>{});
+
+  // Epilogue: lane l holds C[m][n .. n+3] of block (i, j): m = row block + l % 16,
+  // n = column block + 4 (l / 16).
+  mfma_drain();
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int m = m0 + wm * 128 + i * 16 + l16;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int n = n0 + wn * 128 + j * 16 + 4 * lg;
+      float v0 = acc[i][j][0], v1 = acc[i][j][1], v2 = acc[i][j][2], v3 = acc[i][j][3];
+      if constexpr (kBias == 1) {
+        const float* bp = static_cast<const float*>(bias);
+        v0 += bp[n];
+        v1 += bp[n + 1];
+        v2 += bp[n + 2];
+        v3 += bp[n + 3];
+      } else if constexpr (kBias == 2) {
+        const uint16_t* bp = static_cast<const uint16_t*>(bias);
+        v0 += H::to_float(bp[n]);
+        v1 += H::to_float(bp[n + 1]);
+        v2 += H::to_float(bp[n + 2]);
+        v3 += H::to_float(bp[n + 3]);
+      }
+      u32x2 packed;
+      packed[0] = H::pack2(v0, v1);
+      packed[1] = H::pack2(v2, v3);
+      st8(C + (long long)m * ldc + n, packed);
+    }
+  }
+}
+
+// One launch of gemm_quad_kernel over (M/256) x (N/256) workgroups. bias_kind: 0 none,
+// 1 fp32, 2 16-bit.
+template <typename Tag, int kStages>
+hipError_t launch_gemm_quad(const uint16_t* A, const uint16_t* B, uint16_t* C, const void* bias, int bias_kind, int M,
+                            int N, int K, long long lda, long long ldb, long long ldc, hipStream_t stream) {
+  const int grid = (M / gemmq::kT) * (N / gemmq::kT);
+#define KG_GEMM_QUAD(BIAS)                                                                                   \
+  hipLaunchKernelGGL((gemm_quad_kernel<Tag, BIAS, kStages>), dim3(grid), dim3(gemmq::kThreads), 0, stream, A, B, C, \
+                     bias, M, N, K, lda, ldb, ldc)
+  if (bias_kind == 0) KG_GEMM_QUAD(0);
+  else if (bias_kind == 1) KG_GEMM_QUAD(1);
+  else KG_GEMM_QUAD(2);
+#undef KG_GEMM_QUAD
+  return hipGetLastError();
+}
+
+}  // namespace kg_gfx950

@@ -10,6 +10,7 @@
 #include "conv2d_rowvec.h"
 #include "flash_attn_mfma.h"
 #include "gemm.h"
+#include "gemm_quad.h"
 
 #ifdef KG_INSTANTIATE
 #define KG_INSTANCE template
@@ -36,6 +37,16 @@ KG_GEMM_PIPE_INSTANCES(F16Tag, 256, false)
 KG_GEMM_PIPE_INSTANCES(F16Tag, 256, true)
 #undef KG_GEMM_PIPE_INSTANCES
 #undef KG_GEMM_PIPE_INSTANCE
+#define KG_GEMM_QUAD_INSTANCE(TAG, ST)                                                                                  \
+  KG_INSTANCE hipError_t launch_gemm_quad<TAG, ST>(const uint16_t*, const uint16_t*, uint16_t*, const void*, int, int, int, \
+                                                   int, long long, long long, long long, hipStream_t);
+KG_GEMM_QUAD_INSTANCE(Bf16Tag, 2)
+KG_GEMM_QUAD_INSTANCE(Bf16Tag, 3)
+KG_GEMM_QUAD_INSTANCE(Bf16Tag, 4)
+KG_GEMM_QUAD_INSTANCE(F16Tag, 2)
+KG_GEMM_QUAD_INSTANCE(F16Tag, 3)
+KG_GEMM_QUAD_INSTANCE(F16Tag, 4)
+#undef KG_GEMM_QUAD_INSTANCE
 #endif
 
 #if !defined(KG_INSTANTIATE) || defined(KG_INSTANTIATE_FA)

@@ -129,6 +129,34 @@ def test_pipe_256_row_tiles_with_bias(device, oracle_mod, bias_kind):
     assert_h16_close(to_numpy(out), ref, what=f"4096x64x4096 bias={bias_kind}")
 
 
+@pytest.mark.parametrize("dtype_name,bias_kind", [("bfloat16", None), ("float16", "same"), ("bfloat16", "f32")])
+def test_four_wave_tiles_match_eight_wave_kernel(device, dtype_name, bias_kind):
+    """Whole 256 x 256 tiles that fill the chip run on four waves of 128 x 128; the same rows
+    computed as a 1024-row matmul of their own (64 tiles of 256 x 256, too few for the chip:
+    the eight-wave kernel's 128-row tiles, K = 1024 not split) must give the same bits: both
+    issue one 16x16x32 MFMA per 32-deep slice and output block, in k order, and round once."""
+
+    import torch
+
+    tdt = getattr(torch, dtype_name)
+    m, k, n = 4096, 1024, 4096
+    g = torch.Generator(device=device).manual_seed(77)
+    a = (torch.randn(m, k, generator=g, device=device) * 0.1).to(tdt)
+    b = (torch.randn(k, n, generator=g, device=device) * 0.1).to(tdt)
+    bias = None
+    if bias_kind == "f32":
+        bias = torch.randn(n, generator=g, device=device)
+    elif bias_kind == "same":
+        bias = torch.randn(n, generator=g, device=device).to(tdt)
+    full = torch.full((m, n), float("nan"), dtype=tdt, device=device)
+    native.matmul(full, a, b, bias)
+    for r0 in (0, 3072):
+        part = torch.full((1024, n), float("nan"), dtype=tdt, device=device)
+        print(f"[matmul] four-wave vs eight-wave rows {r0}:{r0 + 1024} {dtype_name} bias={bias_kind}", flush=True)
+        native.matmul(part, a[r0:r0 + 1024].contiguous(), b, bias)
+        assert torch.equal(full[r0:r0 + 1024], part), f"rows {r0}:{r0 + 1024}"
+
+
 @pytest.mark.parametrize(
     "shape,dtype_name,bias_kind,rows",
     [
