@@ -222,33 +222,56 @@ __global__ __launch_bounds__(gemmq::kThreads, 1) void gemm_quad_kernel(
   for (; kt + U + kStages <= ktiles; kt += U) unrolled(kt, gemmp::StageIdx<1>{});
   for (; kt < ktiles; kt += U) unrolled(kt, gemmp::StageIdx<0>{});
 
-  // Epilogue: lane l holds C[m][n .. n+3] of block (i, j): m = row block + l % 16,
-  // n = column block + 4 (l / 16).
+  // Epilogue: lane l holds C[m][n .. n+3] of block (i, j) (m = row block + l % 16, n = column
+  // block + 4 (l / 16)). Stored as is, every store instruction would write 32-byte pieces of
+  // 16 rows; instead each wave packs P row blocks at a time (bias added, rounded once) into an
+  // LDS region of its own, [16P rows][128 columns], and writes them back as whole 256-byte row
+  // segments, 16 bytes per lane and 4 rows per instruction (the chip-wide store burst at the
+  // end of the kernel drains faster). 16-byte chunk c of region row r sits at slot
+  // c ^ (r % 16): the packing writes of 16 rows and the row reads both spread over all banks.
+  // A wave reads back only what it wrote itself, so no barrier separates the two; one barrier
+  // first retires the ring (every wave is past its last fragment read).
   mfma_drain();
+  wait_and_barrier<0>();
+  constexpr int P = kStages >= 4 ? 8 : 4;  // row blocks per pass: 2 regions of 4P KiB per ring half
+  static_assert(2 * P * 4096 <= kStages * kStage, "two epilogue regions fit in each half of the ring");
+  const uint32_t region = (wave < 2 ? lds_a0 : lds_b0) + (wave & 1) * P * 4096;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int m = m0 + wm * 128 + i * 16 + l16;
+  for (int i0 = 0; i0 < 8; i0 += P) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int n = n0 + wn * 128 + j * 16 + 4 * lg;
-      float v0 = acc[i][j][0], v1 = acc[i][j][1], v2 = acc[i][j][2], v3 = acc[i][j][3];
-      if constexpr (kBias == 1) {
-        const float* bp = static_cast<const float*>(bias);
-        v0 += bp[n];
-        v1 += bp[n + 1];
-        v2 += bp[n + 2];
-        v3 += bp[n + 3];
-      } else if constexpr (kBias == 2) {
-        const uint16_t* bp = static_cast<const uint16_t*>(bias);
-        v0 += H::to_float(bp[n]);
-        v1 += H::to_float(bp[n + 1]);
-        v2 += H::to_float(bp[n + 2]);
-        v3 += H::to_float(bp[n + 3]);
+    for (int i = i0; i < i0 + P; ++i) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int n = n0 + wn * 128 + j * 16 + 4 * lg;
+        float v0 = acc[i][j][0], v1 = acc[i][j][1], v2 = acc[i][j][2], v3 = acc[i][j][3];
+        if constexpr (kBias == 1) {
+          const float* bp = static_cast<const float*>(bias);
+          v0 += bp[n];
+          v1 += bp[n + 1];
+          v2 += bp[n + 2];
+          v3 += bp[n + 3];
+        } else if constexpr (kBias == 2) {
+          const uint16_t* bp = static_cast<const uint16_t*>(bias);
+          v0 += H::to_float(bp[n]);
+          v1 += H::to_float(bp[n + 1]);
+          v2 += H::to_float(bp[n + 2]);
+          v3 += H::to_float(bp[n + 3]);
+        }
+        u32x2 packed;
+        packed[0] = H::pack2(v0, v1);
+        packed[1] = H::pack2(v2, v3);
+        const int r = 16 * (i - i0) + l16;  // region row; r % 16 == l16
+        const uint32_t ad = region + r * 256 + (((2 * j + (lg >> 1)) ^ l16) * 16) + (lg & 1) * 8;
+        *(__attribute__((address_space(3))) u32x2*)(uintptr_t)ad = packed;
       }
-      u32x2 packed;
-      packed[0] = H::pack2(v0, v1);
-      packed[1] = H::pack2(v2, v3);
-      st8(C + (long long)m * ldc + n, packed);
+    }
+#pragma unroll
+    for (int q = 0; q < 4 * P; ++q) {
+      const int r = 4 * q + (lane >> 4);
+      const int c = lane & 15;
+      const u32x4 v = *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(region + r * 256 + ((c ^ (r & 15)) * 16));
+      const int m = m0 + wm * 128 + 16 * i0 + r;
+      *reinterpret_cast<u32x4*>(C + (long long)m * ldc + n0 + wn * 128 + 8 * c) = v;
     }
   }
 }
