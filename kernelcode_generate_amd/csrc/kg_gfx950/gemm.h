@@ -301,6 +301,60 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
 
   // Epilogue: lane l holds C[m][n .. n+3] of block (ib, nb): m = row block + l % 16, n = column
   // block + 4 (l / 16).
+  auto out_value = [&](int i, int j, int n) -> u32x2 {  // bias added, rounded once
+    float v0 = acc[i][j][0], v1 = acc[i][j][1], v2 = acc[i][j][2], v3 = acc[i][j][3];
+    if constexpr (kBias == 1) {
+      const float* bp = static_cast<const float*>(bias);
+      v0 += bp[n];
+      v1 += bp[n + 1];
+      v2 += bp[n + 2];
+      v3 += bp[n + 3];
+    } else if constexpr (kBias == 2) {
+      const uint16_t* bp = static_cast<const uint16_t*>(bias);
+      v0 += H::to_float(bp[n]);
+      v1 += H::to_float(bp[n + 1]);
+      v2 += H::to_float(bp[n + 2]);
+      v3 += H::to_float(bp[n + 3]);
+    }
+    u32x2 packed;
+    packed[0] = H::pack2(v0, v1);
+    packed[1] = H::pack2(v2, v3);
+    return packed;
+  };
+  if (!kRagged && k_chunk == 0) {
+    // Whole tiles: each wave packs P row blocks at a time into an LDS region of its own,
+    // [16P rows][64 columns], and writes them back as whole 128-byte row segments (16 bytes
+    // per lane, 8 rows per instruction) instead of 32-byte pieces of 16 rows. 16-byte chunk c
+    // of region row r sits at slot c ^ (r % 8): two lanes per bank for the packing writes,
+    // none shared for the row reads. One barrier retires the ring first; a wave reads back
+    // only what it wrote itself.
+    constexpr int kRingHalf = kStages * (kAVecs * 16 < kBVecs * 16 ? kAVecs * 16 : kBVecs * 16);
+    constexpr int P = MB * 8192 <= kRingHalf ? MB : (MB / 2) * 8192 <= kRingHalf ? MB / 2 : MB / 4;
+    static_assert(P >= 1 && MB % P == 0 && P * 8192 <= kRingHalf, "four epilogue regions fit in each half of the ring");
+    wait_and_barrier<0>();
+    const uint32_t region = (wave < 4 ? lds_a0 : lds_b0) + (wave & 3) * P * 2048;
+#pragma unroll
+    for (int i0 = 0; i0 < MB; i0 += P) {
+#pragma unroll
+      for (int i = i0; i < i0 + P; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const u32x2 packed = out_value(i, j, n0 + wn * 64 + j * 16 + 4 * lg);
+          const int r = 16 * (i - i0) + l16;
+          const uint32_t ad = region + r * 128 + (((2 * j + (lg >> 1)) ^ (r & 7)) * 16) + (lg & 1) * 8;
+          *(__attribute__((address_space(3))) u32x2*)(uintptr_t)ad = packed;
+        }
+#pragma unroll
+      for (int q = 0; q < 2 * P; ++q) {
+        const int r = 8 * q + (lane >> 3);
+        const int c = lane & 7;
+        const u32x4 v = *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(region + r * 128 + ((c ^ (r & 7)) * 16));
+        const int m = m0 + wm * (kTM / 2) + 16 * i0 + r;
+        *reinterpret_cast<u32x4*>(C + (long long)m * ldc + n0 + wn * 64 + 8 * c) = v;
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < MB; ++i) {
     const int m = m0 + wm * (kTM / 2) + i * 16 + l16;
@@ -309,28 +363,11 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
       {
         const int n = n0 + wn * 64 + j * 16 + 4 * lg;
         if (kRagged && (m >= M || n >= N)) continue;  // N % 8 == 0: n < N covers n .. n+3
-        float v0 = acc[i][j][0], v1 = acc[i][j][1], v2 = acc[i][j][2], v3 = acc[i][j][3];
         if (k_chunk > 0) {
-          *reinterpret_cast<f32x4*>(partial + (long long)m * N + n) = f32x4{v0, v1, v2, v3};
+          *reinterpret_cast<f32x4*>(partial + (long long)m * N + n) = acc[i][j];
           continue;
         }
-        if constexpr (kBias == 1) {
-          const float* bp = static_cast<const float*>(bias);
-          v0 += bp[n];
-          v1 += bp[n + 1];
-          v2 += bp[n + 2];
-          v3 += bp[n + 3];
-        } else if constexpr (kBias == 2) {
-          const uint16_t* bp = static_cast<const uint16_t*>(bias);
-          v0 += H::to_float(bp[n]);
-          v1 += H::to_float(bp[n + 1]);
-          v2 += H::to_float(bp[n + 2]);
-          v3 += H::to_float(bp[n + 3]);
-        }
-        u32x2 packed;
-        packed[0] = H::pack2(v0, v1);
-        packed[1] = H::pack2(v2, v3);
-        st8(C + (long long)m * ldc + n, packed);
+        st8(C + (long long)m * ldc + n, out_value(i, j, n));
       }
     }
   }
