@@ -36,7 +36,7 @@ DTYPE_CODES = {"f32": 1, "f16": 5, "bf16": 6}
 BINARY_KIND = {"add": 0, "sub": 1, "mul": 2, "truediv": 3, "max": 4}
 ENUM_LIMIT = 4_000_000
 MAX_GRID = 2048
-SCRATCH_BYTES = 32 << 20  # scratch of the allocation-free entry, per GPU
+SCRATCH_BYTES = 32 << 20  # cap of the allocation-free entry's scratch, per GPU (scratch_bytes)
 MAX_DEVICES = 64
 QUERY_GRID = 256  # workgroups of a kernel that distributes work with arch.get_block_id / get_block_num
 
@@ -441,16 +441,35 @@ class _Emitter:
         L += self.entry(function)
         return "\n".join(L) + "\n"
 
+    def scratch_bytes(self) -> int:
+        """Size of the allocation-free entry's __device__ scratch. When every dma.alloc has a
+        static extent the workspace per workgroup is a constant, and the scratch holds exactly
+        the largest grid's slices plus the error word; kernels whose allocations depend on the
+        runtime arguments get the SCRATCH_BYTES cap (a larger workspace per workgroup runs
+        fewer workgroups, or fails with -3)."""
+
+        per_block = 0
+        for m in self.plan.allocs:
+            count = 1
+            for e in m.shape:
+                if not e.is_const:
+                    return SCRATCH_BYTES
+                count *= max(int(e.value), 0)
+            per_block += (count * ELEMENT_BYTES[m.dtype] + 255) // 256 * 256
+        grid = QUERY_GRID if uses_block_queries(self.func) else MAX_GRID
+        return min(SCRATCH_BYTES, per_block * grid + 256)
+
     def entry(self, function: str) -> list[str]:
         f = self.func
+        scratch = self.scratch_bytes()
         L = ["}  // namespace", "",
              "// Scratch of kg_execute_entry_noalloc: device memory the library never allocates.",
              "// Every GPU holds its own copy until the process ends; every call on a GPU shares it",
              "// (so calls that overlap on one GPU race), and it keeps the last call's contents.",
-             f"static __device__ __align__(256) char scratch[{SCRATCH_BYTES}];",
+             f"static __device__ __align__(256) char scratch[{scratch}];",
              "",
              "namespace {",
-             f"constexpr long long kScratchBytes = {SCRATCH_BYTES}LL;",
+             f"constexpr long long kScratchBytes = {scratch}LL;",
              "std::mutex g_scratch_mutex;",
              "char* g_scratch[kMaxDevices] = {};",
              "",
@@ -534,7 +553,7 @@ class _Emitter:
             f'scratch of the allocation-free entry", a.ws_per_block, kScratchBytes - 256);',
             "      return kg_gfx950_fail(-3, msg);",
             "    }",
-            "    const long long fit = (kScratchBytes - 256) / (a.ws_per_block > 0 ? a.ws_per_block : 1);",
+            "    const long long fit = a.ws_per_block > 0 ? (kScratchBytes - 256) / a.ws_per_block : grid;",
             ("    if (grid > fit) grid = fit;" if not uses_block_queries(f) else
              f'    if (grid > fit) return kg_gfx950_fail(-3, "{function}: the {QUERY_GRID} workgroups the kernel\'s '
              f'block queries assume do not fit the scratch of the allocation-free entry");'),

@@ -82,3 +82,24 @@ def test_unsupported_operations_are_named():
         mlir_gen(free_argument, (a,))
     with pytest.raises(KernelCodeError, match="element type"):
         mlir_gen(bad_cast, (a,))
+
+
+def _lower_per_op(fn, args):
+    from kernelcode_generate_amd.pipeline import get_pipeline
+
+    return get_pipeline("gfx950-lowering", {"fuse": "false"}).run(mlir_gen(fn, args))
+
+
+def test_noalloc_scratch_is_bounded_by_static_workspace():
+    """The allocation-free entry's __device__ scratch: exact for kernels whose allocations all
+    have constant extents, the 32 MiB cap otherwise (extents that depend on the arguments)."""
+
+    from kernelcode_generate_amd.gen_kernel import per_op
+    from tests.test_zz_no_alloc import fixed_tile_rows
+
+    x = np.zeros((64, 8), np.float32)
+    fixed = per_op._Emitter(_lower_per_op(fixed_tile_rows, (x, x)).func)
+    assert fixed.scratch_bytes() == 256 * per_op.MAX_GRID + 256
+    assert f"char scratch[{256 * per_op.MAX_GRID + 256}];" in fixed.source("fixed_tile_rows")
+    dynamic = per_op._Emitter(_lower_per_op(cast_rows, (np.zeros((64, 8), np.float16), x, 4)).func)
+    assert dynamic.scratch_bytes() == per_op.SCRATCH_BYTES == 32 << 20

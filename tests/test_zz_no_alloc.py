@@ -20,7 +20,7 @@ from kernelcode_generate_amd.execute_engine import ExecutionEngine
 from kernelcode_generate_amd.gen_kernel import gen_kernel
 from kernelcode_generate_amd.kernel.flash_attention.scaled import flash_attention_scaled_causal_kernel
 from kernelcode_generate_amd.operation import kernel as dsl_kernel
-from kernelcode_generate_amd.operation.dma import alloc, broadcast, deslice, view
+from kernelcode_generate_amd.operation.dma import alloc, broadcast, deslice, load, store, view
 from kernelcode_generate_amd.operation.scf import loop
 from kernelcode_generate_amd.pipeline import get_pipeline
 from kernelcode_generate_amd.symbol_variable import MemorySpace, NumericType, SymbolDim
@@ -106,5 +106,40 @@ def test_noalloc_rejects_oversized_workspace(device):
         assert torch.equal(out, small)
         ref = x - x.max(dim=1, keepdim=True).values
         assert torch.equal(out, ref)
+    finally:
+        compiled.close()
+
+
+def fixed_tile_rows(out: "Tensor[f32, R, C]", x: "Tensor[f32, R, C]") -> None:
+    # every allocation has a constant extent: the generated library's scratch is sized exactly
+    rows, cols = x.get_shape()
+    for r0 in loop(0, rows, 4):
+        t = load(x, [r0, 0], [4, 8], space=MemorySpace.TSM)
+        dsl_kernel.add(t, t, t)
+        store(out, t, [r0, 0], [4, 8])
+
+
+def test_noalloc_exactly_sized_scratch(device):
+    """A kernel whose allocations all have constant extents gets a scratch of exactly the
+    largest grid's workspace plus the error word (4 x 8 fp32 = one 256-byte slice per
+    workgroup, 2048 workgroups: 524,544 bytes, not the 32 MiB cap); two calls in a row, the
+    second smaller, match the allocating entry."""
+
+    import torch
+
+    from kernelcode_generate_amd.gen_kernel import per_op
+
+    x = torch.randn(4096, 8, device=device)
+    lowered = get_pipeline("gfx950-lowering", {"fuse": "false"}).run(mlir_gen(fixed_tile_rows, (x, x)))
+    assert per_op._Emitter(lowered.func).scratch_bytes() == 256 * per_op.MAX_GRID + 256
+    compiled, lib, (alloc_entry, noalloc_entry) = _compile_per_op(fixed_tile_rows, (x, x))
+    try:
+        for rows in (4096, 64):  # 1024 workgroups, then 16
+            xi = torch.randn(rows, 8, device=device)
+            want, got = torch.full_like(xi, float("nan")), torch.full_like(xi, float("nan"))
+            print(f"[no-alloc] exact scratch rows={rows}", flush=True)
+            assert _call(alloc_entry, (want, xi)) == 0, native.last_error()
+            assert _call(noalloc_entry, (got, xi)) == 0, native.last_error()
+            assert torch.equal(got, want) and torch.equal(want, xi + xi)
     finally:
         compiled.close()
