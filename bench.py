@@ -479,7 +479,9 @@ def main() -> int:
         "data": "synthetic: A,B ~ N(0,1)*0.02 (seeded torch generator on the device), resident in HBM",
         "config": {
             "workload": "bf16 matmul M=N=K=4096, row-major A[M,K] B[K,N], fp32 accumulate, bf16 out (BASELINE configs[1])",
-            "M": m, "N": n, "K": k, "kernel": "gemm_pipe_kernel 256x256 tiles, 8 waves, 4-stage HBM->LDS ring, v_mfma_f32_16x16x32_bf16",
+            "M": m, "N": n, "K": k,
+            "kernel": "gemm_quad_kernel: 256x256 tiles, 4 waves of 128x128 (fp32 accumulators in AGPRs), "
+                      "4-stage HBM->LDS ring, v_mfma_f32_16x16x32_bf16, C stored through LDS as whole row segments",
         },
         "roofline": {
             "bound": "mfma",

@@ -18,10 +18,15 @@
  * "runtime_throw_or_abort") is unchanged.
  *
  * Memory slots carry DEVICE pointers (torch ROCm tensor .data_ptr()), element shapes
- * and element strides. Kernels allocate nothing per call. Calls are synchronous by
- * default (the reference's cuda_sm89 launch ends with a device synchronize,
- * include/cuda_sm89/Arch.h:166-168); kg_gfx950_set_launch_mode() switches to
- * asynchronous launches on a caller-chosen stream for benchmarking.
+ * and element strides. Kernels allocate nothing per call, with one exception: matmul and
+ * conv2d calls that split K over workgroups keep their fp32 partial sums in a workspace
+ * held per (device, stream) for the life of the process, allocated on the first such call
+ * on that stream and reallocated when a later one needs more. Those calls are therefore
+ * not safe under HIP graph capture unless an earlier call of at least the same size ran on
+ * that stream uncaptured. Calls are synchronous by default (the reference's cuda_sm89
+ * launch ends with a device synchronize, include/cuda_sm89/Arch.h:166-168);
+ * kg_gfx950_set_launch_mode() switches to asynchronous launches on a caller-chosen stream
+ * for benchmarking.
  *
  * Return codes: 0 ok; -1 slot/shape/dtype validation failure; -2 HIP runtime error;
  * -3 unsupported configuration. kg_gfx950_last_error() describes the last failure.

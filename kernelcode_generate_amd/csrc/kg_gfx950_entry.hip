@@ -531,8 +531,8 @@ int matmul_impl(const KgArgSlot* args, unsigned long long n) {
              (!bias.present || bias.stride[0] == 1))  // 8 MFMAs (32x32x2) per 32 x 32 block and 16-deep slice
       mfma = (M / 32) * (N / 32) * (K / 16) * 8;
     if (mfma_ok && M > 0 && N > 0) {
-      // 8 waves x tm/8 MFMAs (16x16x32) per 32-deep slice of a tm x 256 tile; ragged edges
-      // are covered by whole tiles and slices
+      // tm MFMAs (16x16x32) per 32-deep slice of a tm x 256 tile: 8 waves x tm/8, or for
+      // whole 256 x 256 tiles 4 waves x 64; ragged edges are covered by whole tiles and slices
       const long long tm = pipe_tile_m(M, N);
       mfma = cdiv(M, tm) * cdiv(N, gemmp::kBN) * cdiv(K, gemmp::kBK) * tm;
       cyc = 16;
