@@ -19,15 +19,6 @@
 
 namespace kg_gfx950 {
 
-// f(Int<0>{}), f(Int<1>{}), ..., f(Int<N-1>{}), expanded at compile time.
-template <int N, int I = 0, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (I < N) {
-    f(Int<I>{});
-    static_for<N, I + 1>(f);
-  }
-}
-
 namespace gemmq {
 // acc += a * b on one 16 x 16 block, the accumulator tied to one register tuple of the
 // accumulation file for the whole kernel (with the intrinsic, the register allocator
@@ -41,8 +32,13 @@ __device__ __forceinline__ void mfma16_tied(f32x4& acc, u32x4 a, u32x4 b) {
   else
     asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
-// 32 wait states: more than the 16x16x32 MFMA's result latency, before VALU reads of its result.
+// 32 wait states: more than the 16x16x32 MFMA's result latency, before VALU reads of its
+// result. The caller then passes every accumulator through mfma_order (an empty asm that
+// redefines it), so the compiler cannot move a read of one above the wait.
 __device__ __forceinline__ void mfma_drain() { asm volatile("s_nop 15\n\ts_nop 15" ::: "memory"); }
+__device__ __forceinline__ void mfma_order(f32x4 (&a)[8]) {
+  asm volatile("" : "+a"(a[0]), "+a"(a[1]), "+a"(a[2]), "+a"(a[3]), "+a"(a[4]), "+a"(a[5]), "+a"(a[6]), "+a"(a[7]));
+}
 constexpr int kT = 256;        // tile rows and columns
 constexpr int kBK = 32;        // K slice
 constexpr int kThreads = 256;  // 4 waves
@@ -232,6 +228,8 @@ __global__ __launch_bounds__(gemmq::kThreads, 1) void gemm_quad_kernel(
   // A wave reads back only what it wrote itself, so no barrier separates the two; one barrier
   // first retires the ring (every wave is past its last fragment read).
   mfma_drain();
+#pragma unroll
+  for (int i = 0; i < 8; ++i) mfma_order(acc[i]);
   wait_and_barrier<0>();
   constexpr int P = kStages >= 4 ? 8 : 4;  // row blocks per pass: 2 regions of 4P KiB per ring half
   static_assert(2 * P * 4096 <= kStages * kStage, "two epilogue regions fit in each half of the ring");

@@ -112,4 +112,14 @@ template <int N>
 struct Int {
   static constexpr int value = N;
 };
+
+// f(Int<0>{}), f(Int<1>{}), ..., f(Int<N-1>{}), expanded at compile time (`#pragma unroll`
+// gives up on large bodies and leaves a runtime index).
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(Int<I>{});
+    static_for<N, I + 1>(f);
+  }
+}
 }  // namespace kg_gfx950
