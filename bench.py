@@ -296,7 +296,7 @@ def cpu_model() -> str:
     return "unknown"
 
 
-SECONDARY_KEYS = ("c1", "c2s", "c3", "c4", "c5d128", "c5d64", "f32gemm", "f32fa")
+SECONDARY_KEYS = ("c1", "c2s", "c3", "c4", "c5d128", "c5d64", "f32gemm", "f32fa", "perop")
 PROFILE_KEYS = ("c2",) + SECONDARY_KEYS  # --only also takes the headline GEMM, for counter runs
 
 
@@ -327,7 +327,7 @@ def secondary(dev, steps: int, warmup: int, only=None):
     runs = {"c1": lambda: c1(dev, add, steps), "c2": lambda: c2(dev, add, steps), "c2s": lambda: c2s(dev, add, steps), "c3": lambda: c3(dev, add, steps),
             "c4": lambda: c4(dev, add, steps), "c5d128": lambda: c5(dev, add, steps, 128),
             "c5d64": lambda: c5(dev, add, steps, 64), "f32gemm": lambda: f32_gemm(dev, add, steps),
-            "f32fa": lambda: f32_fa(dev, add, steps)}
+            "f32fa": lambda: f32_fa(dev, add, steps), "perop": lambda: perop_matmul(dev, add, steps)}
     for key in PROFILE_KEYS:
         if key in keys:
             current[0] = key
@@ -393,6 +393,54 @@ def c5(dev, add, steps, d):
     add(f"C5 bf16 flash-attn fwd B=1 H=32 S=16384 D={d} causal", 4 * 32 * 16384 * 16384 * d // 2,
         PreparedCall("kg_gfx950_flash_attention_entry", (o, q, k, v, 128, 64, 1.0 / math.sqrt(d), 1)),
         PEAK_BF16_TFLOPS, max(20, steps // 4))
+
+
+def perop_matmul(dev, add, steps):
+    """The per-operation path, what a kernel the fuse pass does not recognise runs on: this
+    package's tiled matmul program lowered with fuse=false (one HIP kernel executing the IR's
+    operations on tiles, the reference's sequential-k fp32 arithmetic), compiled by the
+    execution engine and called through its kg_execute_entry (workspace allocation included),
+    fp32 1024^3 with 64 x 64 x 64 tiles; the fused library kernel on the same call follows."""
+
+    import ctypes
+
+    import torch
+
+    from kernelcode_generate_amd import native
+    from kernelcode_generate_amd.dsl import mlir_gen
+    from kernelcode_generate_amd.execute_engine import ExecutionEngine
+    from kernelcode_generate_amd.gen_kernel import gen_kernel
+    from kernelcode_generate_amd.kernel.matmul.inputs_static_tile_dynamic import (
+        matmul_inputs_static_tile_dynamic_kernel as program,
+    )
+    from kernelcode_generate_amd.pipeline import get_pipeline
+
+    m = n = k = 1024
+    g = torch.Generator(device=dev).manual_seed(20261206)
+    a = torch.rand(m, k, generator=g, device=dev) * 2 - 1
+    b = torch.rand(k, n, generator=g, device=dev) * 2 - 1
+    c = torch.empty(m, n, device=dev)
+    args = (c, a, b, None, 64, 64, 64)
+    lowered = get_pipeline("gfx950-lowering", {"fuse": "false"}).run(mlir_gen(program, args))
+    compiled = ExecutionEngine("gfx950").compile(source=gen_kernel(lowered), function=program.__name__)
+    try:
+        lib = ctypes.CDLL(compiled.soname_path)
+        entry = lib.kg_execute_entry
+        entry.argtypes = [ctypes.POINTER(native.KgArgSlot), ctypes.c_ulonglong]
+        entry.restype = ctypes.c_int
+        slots, keep = native.marshal_slots(args)
+
+        def call():
+            if entry(slots, len(args)) != 0:
+                raise RuntimeError(f"per-operation kg_execute_entry failed: {native.last_error()}")
+
+        add("per-operation path: fp32 matmul 1024^3, tiles 64 (unfused DSL program)", 2.0 * m * n * k, call,
+            PEAK_FP32_TFLOPS, max(10, steps // 10))
+        add("fused library kernel on the same call (fp32 matmul 1024^3)", 2.0 * m * n * k,
+            PreparedCall("kg_gfx950_matmul_entry", args), PEAK_FP32_TFLOPS, max(20, steps // 4))
+        del keep
+    finally:
+        compiled.close()
 
 
 def f32_gemm(dev, add, steps):
@@ -525,6 +573,7 @@ def main() -> int:
             keys = {r["key"] for r in result["secondary"]}
             baselines = cpu_baselines(keys | ({"c4"} if "f32fa" in keys else set()))
             baselines["f32gemm"] = dict(cb, note="the headline's sample: the same 4096^3 loop nest in fp32")
+            baselines["perop"] = dict(cb, note="the headline's sample: the same matmul loop nest in fp32")
             if "c4" in baselines:
                 baselines["f32fa"] = dict(baselines["c4"], note="C4's sample: the same loop nest in fp32")
             for r in result["secondary"]:
