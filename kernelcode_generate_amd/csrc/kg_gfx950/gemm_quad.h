@@ -11,6 +11,13 @@
 // in full: slice kt's 64 MFMAs run from registers while slice kt+1's 24 fragment reads and
 // slice kt+kStages's 8 copies are slotted between them; one barrier per slice, at its start,
 // publishes slice kt+1's copies and frees slice kt's stage for its refill.
+//
+// kExact (even ring depths, K / 32 a multiple of the depth and at least twice it): the last
+// kStages slices are a compile-time group, so their waits and fragment reads carry no runtime
+// conditions (with the runtime conditions those slices took 1.3-1.5x a steady slice's
+// cycles). C is written with nontemporal stores: whole 256-byte row segments stream past
+// the L2, so less dirty data is left to write back when the kernel ends (measured 1-1.5 %
+// shorter launches than write-back stores at C2's shape).
 #pragma once
 
 #include "common.h"
@@ -47,7 +54,7 @@ constexpr int kPieces = 8;     // copies per wave per slice: 4 lhs (16 rows each
 constexpr int kDefaultStages = 4;
 }  // namespace gemmq
 
-template <typename Tag, int kBias, int kStages>
+template <typename Tag, int kBias, int kStages, bool kExact>
 __global__ __launch_bounds__(gemmq::kThreads, 1) void gemm_quad_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, uint16_t* __restrict__ C,
     const void* __restrict__ bias, int M, int N, int K, long long lda, long long ldb, long long ldc) {
@@ -58,6 +65,7 @@ __global__ __launch_bounds__(gemmq::kThreads, 1) void gemm_quad_kernel(
   using gemmp::b_slot;
   using H = Half16<Tag>;
   static_assert(kStages >= 2 && kStages <= 5, "ring depth");
+  static_assert(!kExact || kStages % 2 == 0, "the exact-K form unrolls one ring turn per group");
   __shared__ u32x4 lds_a[kStages][kVecs];
   __shared__ u32x4 lds_b[kStages][kVecs];
 
@@ -97,7 +105,9 @@ __global__ __launch_bounds__(gemmq::kThreads, 1) void gemm_quad_kernel(
   const uint32_t lds_b0 = lds_addr(&lds_b[0][0]);
   constexpr uint32_t kStage = kVecs * 16;
 
-  auto issue_piece = [&](int kt, int s, int piece) {
+  // (the lambdas are forced inline: if one were left a call, the fragment and accumulator
+  // arrays it takes by reference would move to scratch memory)
+  auto issue_piece = [&](int kt, int s, int piece) __attribute__((always_inline)) {
     if (piece < 4) {
       g2lds16_s(a_goff, a_tile + (long long)kt * kBK * 2 + piece * a_piece,
                 lds_a0 + s * kStage + (wave * 4 + piece) * 1024);
@@ -123,7 +133,7 @@ __global__ __launch_bounds__(gemmq::kThreads, 1) void gemm_quad_kernel(
     u32x4 a[8];
     u32x4 b[8];
   };
-  auto read_b = [&](int s, u32x4& f, int nb) {
+  auto read_b = [&](int s, u32x4& f, int nb) __attribute__((always_inline)) {
     const uint32_t ad = b_rd[nb] + s * kStage;
     const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(uintptr_t)ad);
     const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -131,12 +141,12 @@ __global__ __launch_bounds__(gemmq::kThreads, 1) void gemm_quad_kernel(
     const u32x2 w0 = __builtin_bit_cast(u32x2, v0), w1 = __builtin_bit_cast(u32x2, v1);
     f = u32x4{w0[0], w0[1], w1[0], w1[1]};
   };
-  auto read_a = [&](int s, int ib) -> u32x4 {
+  auto read_a = [&](int s, int ib) __attribute__((always_inline)) -> u32x4 {
     return *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(a_rd + s * kStage + ib * 1024);
   };
   // read step r (0..15): the rhs blocks first (the next slice's first eight MFMAs use lhs
   // block 0 with rhs blocks 0..7), then the lhs blocks
-  auto read_step = [&](int s, Frags& f, int r) {
+  auto read_step = [&](int s, Frags& f, int r) __attribute__((always_inline)) {
     if (r < 8) read_b(s, f.b[r], r);
     else f.a[r - 8] = read_a(s, r - 8);
   };
@@ -148,6 +158,11 @@ __global__ __launch_bounds__(gemmq::kThreads, 1) void gemm_quad_kernel(
     for (int j = 0; j < 8; ++j)
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc[i][j][e] = 0.f;
+  // opaque from here on: the compiler must not rematerialise the zeros (with accumulator
+  // copies) right before the first MFMAs, which would read them without the wait states
+  // a VALU write before an MFMA needs
+#pragma unroll
+  for (int i = 0; i < 8; ++i) mfma_order(acc[i]);
 
   const int ktiles = K / kBK;
 #pragma unroll
@@ -170,16 +185,23 @@ __global__ __launch_bounds__(gemmq::kThreads, 1) void gemm_quad_kernel(
   // One slice in stage S: wait for slice kt+1's copies and meet the other waves (slice kt's
   // stage is then free), then the 64 MFMAs with slice kt+1's 16 fragment reads (24 LDS
   // instructions) on the even steps up to 32 and slice kt+kStages's 8 copies on every
-  // eighth step. kSteady: more slices follow and a refill is due.
-  auto slice = [&](int kt, auto stage_tag, auto par_tag, auto steady_tag) {
+  // eighth step. Mode: 1 steady (more slices follow and a refill is due); 2 one of the last
+  // kStages slices of the exact-K form, with kFollow = decltype(follow_tag)::value slices
+  // after it, all of them copied already; 0 any slice, with runtime conditions.
+  auto slice = [&](int kt, auto stage_tag, auto par_tag, auto mode_tag, auto follow_tag) __attribute__((always_inline)) {
     constexpr int S = decltype(stage_tag)::value;
     constexpr int P = decltype(par_tag)::value;
-    constexpr bool kSteady = decltype(steady_tag)::value != 0;
+    constexpr int kMode = decltype(mode_tag)::value;
+    constexpr int kFollow = decltype(follow_tag)::value;
+    constexpr bool kSteady = kMode == 1;
     Frags& fx = fr[P];
     Frags& fn = fr[P ^ 1];
     const bool more = kSteady || kt + 1 < ktiles;
     const bool refill = kSteady || kt + kStages < ktiles;
-    if (kSteady) {
+    if constexpr (kMode == 2) {
+      // the copies of the kFollow later slices are this wave's only outstanding ones
+      if constexpr (kFollow >= 1) wait_and_barrier<(kFollow - 1) * kPieces>();
+    } else if (kSteady) {
       wait_and_barrier<(kStages - 2) * kPieces>();
     } else if (more) {
       const int younger = min(kStages - 2, ktiles - 2 - kt);
@@ -188,35 +210,47 @@ __global__ __launch_bounds__(gemmq::kThreads, 1) void gemm_quad_kernel(
       else if (younger == 1) wait_and_barrier<kPieces>();
       else wait_and_barrier<0>();
     }
-#pragma unroll
-    for (int idx = 0; idx < 64; ++idx) {
-      const int i = idx >> 3, j = idx & 7;
+    static_for<64>([&](auto idx_tag) __attribute__((always_inline)) {
+      constexpr int idx = decltype(idx_tag)::value;
+      constexpr int i = idx >> 3, j = idx & 7;
       mfma16_tied<Tag>(acc[i][j], fx.b[j], fx.a[i]);  // C^T blocks: lane-contiguous columns
-      if (kSteady) {
-        if ((idx & 1) == 0 && idx < 32) read_step((S + 1) % kStages, fn, idx >> 1);
-        if ((idx & 7) == 3) issue_piece(kt + kStages, S, idx >> 3);
+      if constexpr (kMode == 2) {
+        if constexpr (kFollow >= 1 && (idx & 1) == 0 && idx < 32) read_step((S + 1) % kStages, fn, idx >> 1);
+      } else if constexpr (kSteady) {
+        if constexpr ((idx & 1) == 0 && idx < 32) read_step((S + 1) % kStages, fn, idx >> 1);
+        if constexpr ((idx & 7) == 3) issue_piece(kt + kStages, S, idx >> 3);
       } else {
         if ((idx & 1) == 0 && idx < 32 && more) read_step((S + 1) % kStages, fn, idx >> 1);
         if ((idx & 7) == 3 && refill) issue_piece(kt + kStages, S, idx >> 3);
       }
       __builtin_amdgcn_sched_barrier(0);
-    }
+    });
   };
 
   // Slices are unrolled U at a time (a compile-time loop: `#pragma unroll` gives up on the
   // larger bodies) so that each one's stage (kt % kStages) and register set (kt & 1) are
   // constants.
   constexpr int U = kStages % 2 == 0 ? kStages : 2 * kStages;
-  auto unrolled = [&](int kt0, auto steady_tag) {
-    static_for<U>([&](auto u_tag) {
+  auto unrolled = [&](int kt0, auto mode_tag) __attribute__((always_inline)) {
+    static_for<U>([&](auto u_tag) __attribute__((always_inline)) {
       constexpr int u = decltype(u_tag)::value;
-      if (decltype(steady_tag)::value || kt0 + u < ktiles)
-        slice(kt0 + u, gemmp::StageIdx<u % kStages>{}, gemmp::StageIdx<u & 1>{}, steady_tag);
+      if (decltype(mode_tag)::value == 1 || kt0 + u < ktiles)
+        slice(kt0 + u, gemmp::StageIdx<u % kStages>{}, gemmp::StageIdx<u & 1>{}, mode_tag, Int<0>{});
     });
   };
   int kt = 0;
-  for (; kt + U + kStages <= ktiles; kt += U) unrolled(kt, gemmp::StageIdx<1>{});
-  for (; kt < ktiles; kt += U) unrolled(kt, gemmp::StageIdx<0>{});
+  if constexpr (kExact) {
+    // ktiles % kStages == 0 and ktiles >= 2 kStages (the launcher checks): steady groups up to
+    // the last kStages slices, which run as one compile-time group
+    for (; kt + U < ktiles; kt += U) unrolled(kt, Int<1>{});
+    static_for<U>([&](auto u_tag) __attribute__((always_inline)) {
+      constexpr int u = decltype(u_tag)::value;
+      slice(kt + u, gemmp::StageIdx<u % kStages>{}, gemmp::StageIdx<u & 1>{}, Int<2>{}, Int<U - 1 - u>{});
+    });
+  } else {
+    for (; kt + U + kStages <= ktiles; kt += U) unrolled(kt, Int<1>{});
+    for (; kt < ktiles; kt += U) unrolled(kt, Int<0>{});
+  }
 
   // Epilogue: lane l holds C[m][n .. n+3] of block (i, j) (m = row block + l % 16, n = column
   // block + 4 (l / 16)). Stored as is, every store instruction would write 32-byte pieces of
@@ -269,7 +303,7 @@ __global__ __launch_bounds__(gemmq::kThreads, 1) void gemm_quad_kernel(
       const int c = lane & 15;
       const u32x4 v = *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(region + r * 256 + ((c ^ (r & 15)) * 16));
       const int m = m0 + wm * 128 + 16 * i0 + r;
-      *reinterpret_cast<u32x4*>(C + (long long)m * ldc + n0 + wn * 128 + 8 * c) = v;
+      __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(C + (long long)m * ldc + n0 + wn * 128 + 8 * c));
     }
   }
 }
@@ -280,12 +314,22 @@ template <typename Tag, int kStages>
 hipError_t launch_gemm_quad(const uint16_t* A, const uint16_t* B, uint16_t* C, const void* bias, int bias_kind, int M,
                             int N, int K, long long lda, long long ldb, long long ldc, hipStream_t stream) {
   const int grid = (M / gemmq::kT) * (N / gemmq::kT);
-#define KG_GEMM_QUAD(BIAS)                                                                                   \
-  hipLaunchKernelGGL((gemm_quad_kernel<Tag, BIAS, kStages>), dim3(grid), dim3(gemmq::kThreads), 0, stream, A, B, C, \
-                     bias, M, N, K, lda, ldb, ldc)
-  if (bias_kind == 0) KG_GEMM_QUAD(0);
-  else if (bias_kind == 1) KG_GEMM_QUAD(1);
-  else KG_GEMM_QUAD(2);
+  const int ktiles = K / gemmq::kBK;
+  const bool exact = kStages % 2 == 0 && ktiles % kStages == 0 && ktiles >= 2 * kStages;
+#define KG_GEMM_QUAD(BIAS, EXACT)                                                                                   \
+  hipLaunchKernelGGL((gemm_quad_kernel<Tag, BIAS, kStages, EXACT>), dim3(grid), dim3(gemmq::kThreads), 0, stream, A, B, \
+                     C, bias, M, N, K, lda, ldb, ldc)
+  if constexpr (kStages % 2 == 0) {
+    if (exact) {
+      if (bias_kind == 0) KG_GEMM_QUAD(0, true);
+      else if (bias_kind == 1) KG_GEMM_QUAD(1, true);
+      else KG_GEMM_QUAD(2, true);
+      return hipGetLastError();
+    }
+  }
+  if (bias_kind == 0) KG_GEMM_QUAD(0, false);
+  else if (bias_kind == 1) KG_GEMM_QUAD(1, false);
+  else KG_GEMM_QUAD(2, false);
 #undef KG_GEMM_QUAD
   return hipGetLastError();
 }

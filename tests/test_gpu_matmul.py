@@ -129,17 +129,23 @@ def test_pipe_256_row_tiles_with_bias(device, oracle_mod, bias_kind):
     assert_h16_close(to_numpy(out), ref, what=f"4096x64x4096 bias={bias_kind}")
 
 
-@pytest.mark.parametrize("dtype_name,bias_kind", [("bfloat16", None), ("float16", "same"), ("bfloat16", "f32")])
-def test_four_wave_tiles_match_eight_wave_kernel(device, dtype_name, bias_kind):
+@pytest.mark.parametrize(
+    "dtype_name,bias_kind,k",
+    [("bfloat16", None, 1024), ("float16", "same", 1024), ("bfloat16", "f32", 1024), ("bfloat16", None, 256),
+     ("float16", None, 1056)],
+    ids=["bf16-k1024", "f16-bias16-k1024", "bf16-bias32-k1024", "bf16-k256", "f16-k1056"])
+def test_four_wave_tiles_match_eight_wave_kernel(device, dtype_name, bias_kind, k):
     """Whole 256 x 256 tiles that fill the chip run on four waves of 128 x 128; the same rows
     computed as a 1024-row matmul of their own (64 tiles of 256 x 256, too few for the chip:
-    the eight-wave kernel's 128-row tiles, K = 1024 not split) must give the same bits: both
-    issue one 16x16x32 MFMA per 32-deep slice and output block, in k order, and round once."""
+    the eight-wave kernel's 128-row tiles, K not split) must give the same bits: both issue
+    one 16x16x32 MFMA per 32-deep slice and output block, in k order, and round once.
+    K = 1024 and 256 (32 and 8 slices: the exact-K form, whose last four slices are one
+    compile-time group; 8 is the fewest it takes) and 1056 (33 slices: the general loop)."""
 
     import torch
 
     tdt = getattr(torch, dtype_name)
-    m, k, n = 4096, 1024, 4096
+    m, n = 4096, 4096
     g = torch.Generator(device=device).manual_seed(77)
     a = (torch.randn(m, k, generator=g, device=device) * 0.1).to(tdt)
     b = (torch.randn(k, n, generator=g, device=device) * 0.1).to(tdt)
@@ -152,7 +158,7 @@ def test_four_wave_tiles_match_eight_wave_kernel(device, dtype_name, bias_kind):
     native.matmul(full, a, b, bias)
     for r0 in (0, 3072):
         part = torch.full((1024, n), float("nan"), dtype=tdt, device=device)
-        print(f"[matmul] four-wave vs eight-wave rows {r0}:{r0 + 1024} {dtype_name} bias={bias_kind}", flush=True)
+        print(f"[matmul] four-wave vs eight-wave rows {r0}:{r0 + 1024} {dtype_name} bias={bias_kind} k={k}", flush=True)
         native.matmul(part, a[r0:r0 + 1024].contiguous(), b, bias)
         assert torch.equal(full[r0:r0 + 1024], part), f"rows {r0}:{r0 + 1024}"
 
