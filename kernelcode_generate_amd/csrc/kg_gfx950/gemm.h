@@ -350,7 +350,7 @@ __global__ __launch_bounds__(gemmp::kThreads, 1) void gemm_pipe_kernel(
         const int c = lane & 7;
         const u32x4 v = *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(region + r * 128 + ((c ^ (r & 7)) * 16));
         const int m = m0 + wm * (kTM / 2) + 16 * i0 + r;
-        *reinterpret_cast<u32x4*>(C + (long long)m * ldc + n0 + wn * 64 + 8 * c) = v;
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(C + (long long)m * ldc + n0 + wn * 64 + 8 * c));
       }
     }
     return;
