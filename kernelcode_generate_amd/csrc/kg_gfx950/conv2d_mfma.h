@@ -152,7 +152,7 @@ __global__ __launch_bounds__(convk::kThreads, 1) void conv2d_3x3s1p1_mfma_kernel
       for (int i = 0; i < 8; ++i) {
         const int f2 = (wave - 4) * 16 + 2 * i + (lane >> 5);
         const u32x4 v = *reinterpret_cast<const u32x4*>(ob + f2 * stride + 16 * k);
-        st16(y + ((long long)n * kF + f2) * hw + (long long)ho0 * W + 8 * k, v);
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(y + ((long long)n * kF + f2) * hw + (long long)ho0 * W + 8 * k));
       }
     };
 
