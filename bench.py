@@ -477,8 +477,6 @@ def main() -> int:
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--only", nargs="+", choices=PROFILE_KEYS,
                     help="profiling aid: run only these secondary workloads (no headline GEMM, no CPU baseline)")
-    ap.add_argument("--copy-calibration", action="store_true",
-                    help="also run a plain 1 GiB device copy (reference point for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(
@@ -553,14 +551,6 @@ def main() -> int:
     result["roofline"]["frac_of_mfma_ceiling"] = round(achieved / ceiling["tflops"], 4)
     log(f"[bench] mfma ceiling (random bf16 operands): {ceiling['tflops']:.1f} TFLOP/s at {ceiling['clock_ghz']:.3f} GHz; "
         f"headline {achieved / ceiling['tflops']:.3f} of it")
-    if args.copy_calibration:
-        src = torch.empty(1 << 29, dtype=torch.bfloat16, device=dev).fill_(1.0)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        log("[bench] copy calibration: 3 x 1 GiB device-to-device copies")
-        del src, dst
     if not args.no_secondary:
         result["secondary"] = secondary(dev, max(5, args.steps // 2), args.warmup)
     native.set_launch_mode(True, None)
