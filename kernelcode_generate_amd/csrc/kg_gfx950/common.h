@@ -28,6 +28,7 @@ struct Half16;
 
 template <>
 struct Half16<Bf16Tag> {
+  static constexpr uint32_t kOnePair = 0x3F803F80u;  // two bf16 1.0
   // D(16x16,f32) += A(16x32) * B(32x16); lane l supplies A[l%16][8*(l/16)+0..7] and
   // B[8*(l/16)+0..7][l%16]; D[4*(l/16)+i][l%16] lands in element i.
   static __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
@@ -62,6 +63,7 @@ struct Half16<Bf16Tag> {
 
 template <>
 struct Half16<F16Tag> {
+  static constexpr uint32_t kOnePair = 0x3C003C00u;  // two fp16 1.0
   static __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);

@@ -837,7 +837,7 @@ int flash_attention_impl(const KgArgSlot* args, unsigned long long n) {
     const long long pairs = s.causal ? (long long)s.s_q * (s.s_q + 1) / 2 : (long long)s.s_q * s.s_kv;
     long long mfma = 0;
     if ((out.dtype == KG_DTYPE_BF16 || out.dtype == KG_DTYPE_F16) && fa_mfma_supported(s) && out.numel() > 0) {
-      // per workgroup: waves x key tiles x (D/4 16x16x32 MFMAs for S^T + D/4 for PV)
+      // per workgroup: waves x key tiles x (D/4 16x16x32 MFMAs for S^T + D/4 for PV + 4 row sums)
       const int waves = fa_mfma_waves(s);
       const int bm = 32 * waves;
       const int nmb = (s.s_q + bm - 1) / bm;
@@ -846,7 +846,7 @@ int flash_attention_impl(const KgArgSlot* args, unsigned long long n) {
         const int n_end = s.causal ? std::min(s.s_kv, (mb + 1) * bm) : s.s_kv;
         tiles += (n_end + fa::kBC - 1) / fa::kBC;
       }
-      mfma = B_H * tiles * waves * (s.d / 2);
+      mfma = B_H * tiles * waves * (s.d / 2 + 4);
     }
     if (out.dtype == KG_DTYPE_F32 && fa_f32_mfma_supported(s) && out.numel() > 0) {
       // per workgroup and key tile: D MFMAs (32x32x2: D/2 for S^T, D/2 for PV) per wave that

@@ -181,9 +181,13 @@ def test_attention_macs_count_mask(shape, causal):
 
 
 def test_attention_mfma_exact_tiles():
+    """Exact tiles: the S^T and PV MFMAs (D/2 per wave and key tile) carry exactly the MACs;
+    the kernel adds 4 row-sum MFMAs (P against ones) per wave and tile."""
+
     shape = (4, 32, 2048, 128)
+    d = shape[3]
     c = costs(flash_attention_scaled_kernel, (T(shape, "bfloat16"),) * 4 + (128, 64, 0.088))
-    assert c["MFMA"] * GEMM_MFMA_MACS == c["MAC"] and c["MFMA_CYCLES"] == 16 * c["MFMA"]
+    assert c["MFMA"] * (d // 2) * GEMM_MFMA_MACS == c["MAC"] * (d // 2 + 4) and c["MFMA_CYCLES"] == 16 * c["MFMA"]
     static = costs(flash_attention_inputs_static_tile_static_kernel, (T(shape, "bfloat16"),) * 4)
     assert static["MAC"] == c["MAC"] and static["MFMA"] == c["MFMA"]
 
@@ -193,9 +197,12 @@ def test_attention_causal_mfma_bounds():
     pairs and the full square."""
 
     shape = (1, 32, 16384, 128)
+    d = shape[3]
     c = costs(flash_attention_scaled_causal_kernel, (T(shape, "bfloat16"),) * 4 + (128, 64, 0.088))
     full = 2 * 32 * 16384 * 16384 * 128
-    assert c["MAC"] <= c["MFMA"] * GEMM_MFMA_MACS < 0.51 * full
+    assert c["MFMA"] % (d // 2 + 4) == 0
+    product_mfma = c["MFMA"] // (d // 2 + 4) * (d // 2)  # without the 4 row-sum MFMAs per wave and tile
+    assert c["MAC"] <= product_mfma * GEMM_MFMA_MACS < 0.51 * full
 
 
 def _read_profile():

@@ -23,7 +23,7 @@ from tests.cost_cases import CASES, modelled, prepare
 pytestmark = pytest.mark.gpu
 FLOP_PER_MFMA_CYCLE = {"float32": 64, "bfloat16": 1024, "float16": 1024}
 EXACT = {"gemm_bf16_4096", "gemm_bf16_c2s_8192x1024x4096", "gemm_f16_512x768x256", "gemm_f32_256",
-         "gemm_f32_splitk_512x512x4096", "gemm_f32_mfma_1024x256x1024", "fa_bf16_c4"}
+         "gemm_f32_splitk_512x512x4096", "gemm_f32_mfma_1024x256x1024"}
 
 
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
