@@ -122,6 +122,13 @@ __device__ __forceinline__ void transpose8x8_b16(const u32x4 in[8], u32x4 out[8]
 }
 
 // Global -> register 16-byte load/store helpers (plain vector memory ops).
+// The lane id from an asm statement the compiler may not move or merge: values computed from
+// it inside a loop are not hoisted out of that loop (and held in registers across it).
+__device__ __forceinline__ int lane_id_volatile() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 __device__ __forceinline__ void st8(void* p, u32x2 v) { *reinterpret_cast<u32x2*>(p) = v; }

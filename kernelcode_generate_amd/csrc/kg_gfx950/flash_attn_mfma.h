@@ -51,6 +51,8 @@
 // at c ^ v_mask(r). Each copy lane fetches the HBM chunk that belongs at its LDS slot.
 #pragma once
 
+#include <atomic>
+
 #include "flash_attn.h"
 #include "lds_dma.h"
 
@@ -142,9 +144,51 @@ __device__ __forceinline__ void rows4_combine(float& a, float& b) {
   b = f(r31);
 }
 
+// Whole query blocks: a wave packs its 32 output rows (o: O^T accumulators, lane holding
+// O^T[16db + 4lr + i][query l16 of block qb]; inv: the row sums' inverses) into an LDS region of
+// its own and writes them back as whole 2D-byte rows, 16 bytes per lane, with nontemporal
+// stores, instead of 32-byte pieces of 16 rows (measured on C4: shorter launches, as for the
+// GEMMs' C). 16-byte chunk c of region row r sits at slot c ^ (r % CPR): the packing writes of
+// 16 rows at one chunk pair and the row reads both spread over the bank groups.
+template <typename H, int D, int NDB>
+__device__ __forceinline__ void write_rows(const f32x4 (&o)[NDB][2], const float (&inv)[2], uint32_t region, int lane,
+                                           uint16_t* rows) {
+  constexpr int RB = 2 * D;
+  constexpr int CPR = RB / 16;  // 16-byte chunks per output row
+  constexpr int RPI = 64 / CPR;  // rows per read instruction
+  const int l16 = lane & 15, lr = lane >> 4;
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      u32x2 packed;
+      packed[0] = H::pack2(o[db][qb][0] * inv[qb], o[db][qb][1] * inv[qb]);
+      packed[1] = H::pack2(o[db][qb][2] * inv[qb], o[db][qb][3] * inv[qb]);
+      const int r = 16 * qb + l16;
+      const int c = 2 * db + (lr >> 1);
+      const uint32_t ad = region + r * RB + 16 * (c ^ (r & (CPR - 1))) + 8 * (lr & 1);
+      *(__attribute__((address_space(3))) u32x2*)(uintptr_t)ad = packed;
+    }
+#pragma unroll
+  for (int t = 0; t < 32 / RPI; ++t) {
+    const int r = RPI * t + lane / CPR;
+    const int c = lane % CPR;
+    const u32x4 v = *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(region + r * RB + 16 * (c ^ (r & (CPR - 1))));
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(rows + (long long)r * D + 8 * c));
+  }
+}
+
 }  // namespace fa
 
-template <typename Tag, int D, bool kCausal, bool kMasked, int W, int kStages>
+// kPersist: a grid of kPerCU workgroups per CU walks the work items (query blocks) blockIdx.x,
+// blockIdx.x + gridDim.x, ... as one sequence of key tiles: each wave copies its rows of the
+// next item's Q into a staging region of its own during tiles nt-4 and nt-3 and reads them
+// into its Q registers in tile nt-2, the next item's K tiles 0-1 and V tile 0 take the ring
+// slots of the tiles that would follow this item's last, and the last tile's S MFMAs compute
+// the next item's first S tile. An item boundary then costs only the output write, where a
+// new workgroup waits for its launch and its first tiles (non-causal whole tiles, an even
+// tile count of at least 4 and a two-deep ring).
+template <typename Tag, int D, bool kCausal, bool kMasked, int W, int kStages, bool kPersist = false>
 __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU)) void fa_fwd_mfma_kernel(const uint16_t* __restrict__ Q,
                                                                       const uint16_t* __restrict__ K,
                                                                       const uint16_t* __restrict__ V,
@@ -168,8 +212,12 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
   constexpr int RPP = 1024 / RB;     // rows per copy instruction
   constexpr int kKAhead = 3;         // K fragments read ahead of their MFMAs
   static_assert(kStages >= 2 && kStages <= 4, "K/V ring depth");
+  static_assert(!kPersist || (!kCausal && !kMasked && kStages == 2), "persistent form: whole non-causal tiles");
+  // persistent form: each wave's output staging region of 32 rows follows the ring (the ring
+  // holds the next item's first tiles while the outputs leave)
+  constexpr int kOutBytes = kPersist ? kWaves * 32 * RB : 0;
 
-  __shared__ __attribute__((aligned(1024))) u32x4 lds[2 * kStages * TB / 16];  // K ring, then V ring
+  __shared__ __attribute__((aligned(1024))) u32x4 lds[(2 * kStages * TB + kOutBytes) / 16];  // K ring, V ring, outputs
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -178,16 +226,39 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
   const int lr = lane >> 4;  // lane row (16 lanes)
 
   const int nmb = (s_q + kBM - 1) / kBM;
-  const int lin = xcd_block(blockIdx.x, nmb * bh_count);
+  const int items = nmb * bh_count;
+  int item = blockIdx.x;  // work item (query block): the workgroup id, or for kPersist the first
+  const int lin = xcd_block(item, items);
   const int bh = lin / nmb;
   int mb = lin - bh * nmb;
   if (kCausal) mb = nmb - 1 - mb;  // longest query blocks of a (b,h) first
-  const int m0 = mb * kBM;
+  int m0 = mb * kBM;
   const long long kv_base = (long long)bh * s_kv * D;
   const uint16_t* Qh = Q + (long long)bh * s_q * D;
   const char* Kb = reinterpret_cast<const char*>(K + kv_base);
   const char* Vb = reinterpret_cast<const char*>(V + kv_base);
   uint16_t* Oh = O + (long long)bh * s_q * D;
+  // the next item of a persistent workgroup (has_next false: none, or not persistent)
+  bool has_next = false;
+  int m0_next = 0;
+  const uint16_t* Qn = Q;
+  const char* Kn = nullptr;
+  const char* Vn = nullptr;
+  uint16_t* On = O;
+  auto find_next = [&]() {
+    const int it = item + (int)gridDim.x;
+    has_next = it < items;
+    if (has_next) {
+      const int lin_n = xcd_block(it, items);
+      const long long bhn = lin_n / nmb;
+      m0_next = (lin_n - (int)bhn * nmb) * kBM;
+      Qn = Q + bhn * s_q * D;
+      Kn = reinterpret_cast<const char*>(K + bhn * s_kv * D);
+      Vn = reinterpret_cast<const char*>(V + bhn * s_kv * D);
+      On = O + bhn * s_q * D;
+    }
+  };
+  if constexpr (kPersist) find_next();
 
   const int wave_q_lo = m0 + 32 * wave;
   const int q_row0 = wave_q_lo + l16;  // query of block qb: q_row0 + 16 qb
@@ -237,6 +308,19 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
 #pragma unroll
     for (int p = 0; p < PW; ++p) copy_piece(Vb, t, lds0 + (kStages + buf) * TB, true, p);
   };
+  // Persistent form: this wave's 32 rows of the next item's Q into its staging region (after
+  // the ring), laid out like a K tile (chunk c of row r at slot c ^ k_mask(r)), so that the Q
+  // fragments are read at the K fragment offsets; QPW copies of RPP rows. The lane id is taken
+  // afresh: offsets derived from a value that lives through the item loop would be hoisted out
+  // of it and held in registers across the main loop.
+  constexpr int QPW = 32 * RB / 1024;
+  const uint32_t q_stage = lds0 + 2 * kStages * TB + wave * 32 * RB;
+  auto copy_q = [&](int p) {
+    const int ln = lane_id_volatile();
+    const int row = p * RPP + ln / DCH;
+    const uint32_t voff = (uint32_t)(row * RB + 16 * ((ln % DCH) ^ k_mask<D>(row)));
+    g2lds16_s(voff, reinterpret_cast<const char*>(Qn + (long long)(m0_next + 32 * wave) * D), q_stage + p * 1024);
+  };
 
   // ---- fragment reads ----
   // K fragment f = kb*NDS + s: key row 16kb + l16, chunk 4s + lr; k_mask(16kb + l16) ==
@@ -264,6 +348,11 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
   auto read_k = [&](uint32_t boff, int f) -> u32x4 {
     const int kb = f / NDS, s = f % NDS;
     return *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(k_rd[s] + boff + kb * 16 * RB);
+  };
+  // Q fragment (query block qb, d step s) of the staged next item: row 16qb + l16, chunk 4s + lr,
+  // whose slot is the K fragment's (k_mask(16qb + l16) == k_mask(l16))
+  auto read_q = [&](int qb, int s) -> u32x4 {
+    return *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)(k_rd[s] + (q_stage - lds0) + qb * 16 * RB);
   };
   auto read_v = [&](uint32_t boff, int f) -> u32x4 {
     const int c = f / NDB, db = f % NDB;
@@ -386,6 +475,9 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
   auto iteration = [&](int j, auto par_tag, auto next_tag, Scores& sc, Scores& sn, auto tail_tag) {
     constexpr int par = decltype(par_tag)::value;
     constexpr bool kNext = decltype(next_tag)::value != 0;
+    // tail_tag: 0 main loop, 1 the last two tiles, 2 (persistent form) tiles nt-4 and nt-3
+    constexpr bool kTailIt = decltype(tail_tag)::value == 1;
+    constexpr bool kQStage = kPersist && decltype(tail_tag)::value == 2;
     const bool copy_k2 = j + kStages < ntiles;      // K(j+S) exists (only if kNext)
     const bool copy_v1 = kStages == 2 || j + kStages - 1 < ntiles;  // V(j+S-1) exists
     // ring buffers: with two they are immediates; deeper rings keep the fragment addresses
@@ -429,10 +521,26 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
         if (i % kGap == kGap - 1) {
           const int c = i / kGap;
           if (c < PW) {
-            if (copy_k2) copy_piece(Kb, j + kStages, lds0 + kb_copy, false, c);
+            if constexpr (kPersist && kTailIt) {
+              // the last two tiles copy the next item's K tiles 0 and 1, into the buffers of
+              // their position in the sequence of tiles (the tile count is even)
+              if (has_next) copy_piece(Kn, par, lds0 + kb_copy, false, c);
+            } else {
+              if (copy_k2) copy_piece(Kb, j + kStages, lds0 + kb_copy, false, c);
+            }
           } else {
-            if (copy_v1) copy_piece(Vb, j + kStages - 1, lds0 + kStages * TB + vb_copy, true, c - PW);
+            if constexpr (kPersist && kTailIt && par == 1) {
+              copy_piece(Vn, 0, lds0 + kStages * TB + vb_copy, true, c - PW);  // (a next item exists here)
+            } else {
+              if (copy_v1) copy_piece(Vb, j + kStages - 1, lds0 + kStages * TB + vb_copy, true, c - PW);
+            }
           }
+        }
+        if constexpr (kQStage) {
+          // tiles nt-4 and nt-3 copy this wave's rows of the next item's Q into its staging
+          // region, half in each (unconditionally: without a next item Qn and m0_next still
+          // address valid rows, this item's or the first one's)
+          if (i % kGap == kGap / 2 - 1 && i / kGap < QPW / 2) copy_q(par * (QPW / 2) + i / kGap);
         }
         if ((i & 1) == 0 && (i >> 1) + kKAhead < NKF) kf[(i >> 1) + kKAhead] = read_k(kb_next, (i >> 1) + kKAhead);
         if (i == NS - 2) vf[0] = read_v(vb_cur, 0);
@@ -450,6 +558,12 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
       for (int i = 0; i < NP / 2; ++i) {
         pv(i, vf[i >> 1]);
         if ((i & 1) == 0) vf[(i >> 1) + 2] = read_v(vb_cur, (i >> 1) + 2);
+        if constexpr (kPersist && kTailIt && par == 0) {
+          // the second-to-last tile is done with Q after block 1: the next item's Q comes in
+          // from the staging region (unconditionally: without a next item it is not used)
+          static_assert(2 * NDS <= NP / 4, "Q read slots");
+          if ((i & 1) == 1 && (i >> 1) < 2 * NDS) qf[(i >> 1) / NDS][(i >> 1) % NDS] = read_q((i >> 1) / NDS, (i >> 1) % NDS);
+        }
         const int lo = 24 + 8 * i / (NP / 2), hi = 24 + 8 * (i + 1) / (NP / 2);
 #pragma unroll
         for (int e = lo; e < hi; ++e) sm_elem(sc, e);
@@ -526,6 +640,50 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
   }
   wait_and_barrier<0>();  // every wave is done with K(0) before K(S) replaces it
 
+  if constexpr (kPersist) {
+    for (;;) {  // work items
+      int j = 0;
+      for (; j + 4 < ntiles; j += 2) {
+        iteration(j, Int<0>{}, Int<1>{}, sa, sb, Int<0>{});
+        iteration(j + 1, Int<1>{}, Int<1>{}, sb, sa, Int<0>{});
+      }
+      // An even tile count of at least 4: tiles nt-4 and nt-3 stage the next item's Q, then
+      // the last two. With a next item the last one runs as a middle tile of one sequence of
+      // tiles: its S MFMAs compute the next item's first S tile (into sa, with the Q read from
+      // the staging region in the tile before) and its copies bring the next item's K tile 1
+      // and V tile 0, so the next item starts at its first iteration once this one's outputs
+      // are written.
+      iteration(j, Int<0>{}, Int<1>{}, sa, sb, Int<2>{});
+      iteration(j + 1, Int<1>{}, Int<1>{}, sb, sa, Int<2>{});
+      j += 2;
+      iteration(j, Int<0>{}, Int<1>{}, sa, sb, Int<1>{});
+      if (!has_next) break;
+      iteration(j + 1, Int<1>{}, Int<1>{}, sb, sa, Int<1>{});
+      {
+        // the lane id afresh (see copy_q); the staging region is free again (the Q read of
+        // the tile before has completed: LDS ops of one wave complete in order)
+        const float inv[2] = {1.f / l_run[0][0], 1.f / l_run[1][0]};
+        fa::write_rows<H, D>(o, inv, q_stage, lane_id_volatile(), Oh + (long long)(m0 + 32 * wave) * D);
+      }
+      item += (int)gridDim.x;
+      m0 = m0_next;
+      Kb = Kn;
+      Vb = Vn;
+      Oh = On;
+      find_next();
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) o[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      m_run[0] = m_run[1] = -INFINITY;
+      l_run[0] = l_run[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    iteration(ntiles - 1, Int<1>{}, Int<0>{}, sb, sa, Int<1>{});
+    const float inv[2] = {1.f / l_run[0][0], 1.f / l_run[1][0]};
+    fa::write_rows<H, D>(o, inv, q_stage, lane_id_volatile(), Oh + (long long)(m0 + 32 * wave) * D);
+    return;
+  }
+
   int j = 0;
   for (; j + 2 < ntiles; j += 2) {
     iteration(j, Int<0>{}, Int<1>{}, sa, sb, Int<0>{});
@@ -540,12 +698,9 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
 
   const float inv[2] = {1.f / l_run[0][0], 1.f / l_run[1][0]};
   if constexpr (!kMasked) {
-    // Whole query blocks: each wave packs its 32 output rows into an LDS region of its own
-    // (the K/V ring is free once every wave is past its last fragment read) and writes them
-    // back as whole 2D-byte rows, 16 bytes per lane, with nontemporal stores, instead of
-    // 32-byte pieces of 16 rows (measured on C4: shorter launches, as for the GEMMs' C).
-    // 16-byte chunk c of region row r sits at slot c ^ (r % CPR): the packing writes of 16
-    // rows at one chunk pair and the row reads both spread over the bank groups.
+    // Whole query blocks: fa::write_rows's packing and row stores, written out here (the call
+    // changed the register allocation of these kernels), through the wave's part of the K/V
+    // ring (free once every wave is past its last fragment read).
     constexpr int CPR = RB / 16;       // 16-byte chunks per output row
     constexpr int RPI = 64 / CPR;      // rows per read instruction
     static_assert(kWaves * 32 * RB <= 2 * kStages * TB, "the output regions fit in the ring");
@@ -601,6 +756,31 @@ inline bool fa_mfma_supported(const FaShape& s) {
          (long long)((s.s_q + fa::Cfg<64>::kBM - 1) / fa::Cfg<64>::kBM) * s.bh < (1ll << 31);
 }
 
+// Compute units of the current device, read once per device.
+inline int fa_device_cus() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cached[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 0;
+    cached[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// The persistent form (kPerCU workgroups per CU for `slots` workgroups in all). Compiled in a
+// translation unit of its own: next to the other instantiations it changed their register
+// allocation (spills in the causal D=128 kernels).
+template <typename Tag, int D, int W>
+hipError_t launch_fa_fwd_mfma_persist(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
+                                      const FaShape& s, int slots, hipStream_t stream) {
+  hipLaunchKernelGGL((fa_fwd_mfma_kernel<Tag, D, false, false, W, 2, true>), dim3(slots), dim3(fa::Cfg<D, W>::kThreads),
+                     0, stream, q, k, v, o, s.bh, s.s_q, s.s_kv, s.scale * 1.4426950408889634f);
+  return hipGetLastError();
+}
+
 template <typename Tag, int D, int W, int kStages>
 hipError_t launch_fa_fwd_mfma_dw(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, const FaShape& s,
                                  hipStream_t stream) {
@@ -609,6 +789,16 @@ hipError_t launch_fa_fwd_mfma_dw(const uint16_t* q, const uint16_t* k, const uin
   const dim3 grid(nmb * s.bh);
   const bool masked = (s.s_q % C::kBM) != 0 || (s.s_kv % fa::kBC) != 0;
   const float scale_log2 = s.scale * 1.4426950408889634f;
+  if constexpr (kStages == 2 && (D == 64 || W == 8)) {
+    // Non-causal whole tiles, an even tile count of at least 4 and at least two items per
+    // workgroup slot: the persistent form, kPerCU workgroups per CU (a multiple of the 8
+    // XCDs, so an item's XCD is its workgroup's).
+    const long long items = (long long)nmb * s.bh;
+    const int slots = fa_device_cus() * C::kPerCU / 8 * 8;
+    const int ntiles = s.s_kv / fa::kBC;
+    if (!s.causal && !masked && ntiles % 2 == 0 && ntiles >= 4 && slots >= 8 && items >= 2ll * slots)
+      return launch_fa_fwd_mfma_persist<Tag, D, W>(q, k, v, o, s, slots, stream);
+  }
 #define KG_FA(CAUSAL, MASKED)                                                                                    \
   hipLaunchKernelGGL((fa_fwd_mfma_kernel<Tag, D, CAUSAL, MASKED, W, kStages>), grid, dim3(C::kThreads), 0, stream, q, k, v, o, \
                      s.bh, s.s_q, s.s_kv, scale_log2)

@@ -49,6 +49,25 @@ KG_GEMM_QUAD_INSTANCE(F16Tag, 4)
 #undef KG_GEMM_QUAD_INSTANCE
 #endif
 
+// The persistent attention form: its own translation unit; every other one, the attention
+// family's included, sees `extern template` declarations (ahead of the attention launchers
+// that call it).
+#ifdef KG_INSTANTIATE_FA_PERSIST
+#define KG_FA_PERSIST_INSTANCE(TAG, D, W)                                                                          \
+  template hipError_t launch_fa_fwd_mfma_persist<TAG, D, W>(const uint16_t*, const uint16_t*, const uint16_t*,     \
+                                                            uint16_t*, const FaShape&, int, hipStream_t);
+#else
+#define KG_FA_PERSIST_INSTANCE(TAG, D, W)                                                                          \
+  extern template hipError_t launch_fa_fwd_mfma_persist<TAG, D, W>(const uint16_t*, const uint16_t*,              \
+                                                                   const uint16_t*, uint16_t*, const FaShape&, int, \
+                                                                   hipStream_t);
+#endif
+KG_FA_PERSIST_INSTANCE(Bf16Tag, 128, 8)
+KG_FA_PERSIST_INSTANCE(Bf16Tag, 64, 4)
+KG_FA_PERSIST_INSTANCE(F16Tag, 128, 8)
+KG_FA_PERSIST_INSTANCE(F16Tag, 64, 4)
+#undef KG_FA_PERSIST_INSTANCE
+
 #if !defined(KG_INSTANTIATE) || defined(KG_INSTANTIATE_FA)
 #define KG_FA_INSTANCE(TAG, ST)                                                                                      \
   KG_INSTANCE hipError_t launch_fa_fwd_mfma_st<TAG, ST>(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, \

@@ -247,6 +247,57 @@ def test_c5_full_size_causal(device, oracle_mod, d, seed):
     np.testing.assert_allclose(got[0, :, 0, :], v[0, :, 0, :], rtol=1e-2, atol=1e-2)
 
 
+PERSISTENT = [
+    ((1, 65, 2048, 128), 2048, "bfloat16"),  # 520 items on 256 workgroups: 8 of them take a third
+    ((2, 64, 2048, 128), 2048, "float16"),   # 1024 items, 4 per workgroup
+    ((1, 64, 2048, 128), 256, "bfloat16"),   # 4 key tiles per item, the fewest: Q staged in tiles 0-1
+    ((1, 64, 2048, 128), 384, "float16"),    # 6 key tiles per item
+    ((1, 64, 2048, 128), 128, "bfloat16"),   # 2 key tiles: too few, one workgroup per item
+    ((1, 130, 1024, 64), 1024, "bfloat16"),  # D=64: 1040 items on 512 four-wave workgroups
+]
+
+
+@pytest.mark.parametrize("shape,s_kv,dtype", PERSISTENT)
+def test_persistent_form_matches_one_item_per_workgroup(device, oracle_mod, shape, s_kv, dtype):
+    """Non-causal whole-tile attention with an even key-tile count of at least 4 and at least
+    two items (query blocks) per workgroup slot runs persistent workgroups: each walks the
+    items gridDim.x apart as one sequence of key tiles (the next item's Q staged in LDS during
+    tiles nt-4 and nt-3, its K tiles 0-1 and V tile 0 copied and its first S tile computed in
+    this item's last two tiles). A three-deep ring (memory_stage=3) launches one workgroup per
+    item instead.
+    Both do the same arithmetic per item, so the bits must agree; sampled rows of two heads
+    also against the oracle (S_kv = S_q: the demo's loop nest) or the float64 formula."""
+
+    import torch
+
+    tdt = getattr(torch, dtype)
+    b, h, s, d = shape
+    rng = np.random.default_rng(s + h + s_kv)
+    q, qn = round_to(rng.standard_normal(shape, dtype=np.float32), tdt)
+    (k, kn), (v, vn) = (round_to(rng.standard_normal((b, h, s_kv, d), dtype=np.float32), tdt) for _ in range(2))
+    q, k, v = (t.to(device) for t in (q, k, v))
+    scale = 1.0 / np.sqrt(d)
+    outs = []
+    for stages in (2, 3):
+        out = torch.full(shape, float("nan"), dtype=tdt, device=device)
+        print(f"[fa] persistent check {shape} s_kv={s_kv} {dtype} memory_stage={stages}", flush=True)
+        native.flash_attention(out, q, k, v, 64, 64, scale, False, memory_stage=stages)
+        outs.append(out)
+    assert torch.equal(outs[0], outs[1])
+    got = to_numpy(outs[0])
+    assert np.isfinite(got).all()
+    heads, blocks = [(0, 0), (b - 1, h - 1)], [(0, 64), (s - 64, s)]
+    if s_kv == s:
+        _sampled_check(oracle_mod, got, qn, kn, vn, heads, blocks, scale, False, f"{shape}")
+        return
+    for bb, hh in heads:
+        for m0, m1 in blocks:
+            logits = qn[bb, hh, m0:m1].astype(np.float64) @ kn[bb, hh].astype(np.float64).T * scale
+            w = np.exp(logits - logits.max(axis=1, keepdims=True))
+            ref = (w / w.sum(axis=1, keepdims=True)) @ vn[bb, hh].astype(np.float64)
+            assert_h16_close(got[bb, hh, m0:m1], ref, what=f"{shape} s_kv={s_kv} b={bb} h={hh} rows {m0}:{m1}")
+
+
 def test_rejects_bad_args(device):
     import torch
 
