@@ -538,9 +538,8 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
         }
         if constexpr (kQStage) {
           // tiles nt-4 and nt-3 copy this wave's rows of the next item's Q into its staging
-          // region, half in each (unconditionally: without a next item Qn and m0_next still
-          // address valid rows, this item's or the first one's)
-          if (i % kGap == kGap / 2 - 1 && i / kGap < QPW / 2) copy_q(par * (QPW / 2) + i / kGap);
+          // region, half in each
+          if (i % kGap == kGap / 2 - 1 && i / kGap < QPW / 2 && has_next) copy_q(par * (QPW / 2) + i / kGap);
         }
         if ((i & 1) == 0 && (i >> 1) + kKAhead < NKF) kf[(i >> 1) + kKAhead] = read_k(kb_next, (i >> 1) + kKAhead);
         if (i == NS - 2) vf[0] = read_v(vb_cur, 0);
