@@ -264,17 +264,45 @@ __device__ void matmul(const View<TO, 2>& out, const View<TL, 2>& lhs, const Vie
     sync();
     return;
   }
-  for (long long e = threadIdx.x; e < M * N; e += kThreads) {
-    const long long m = e / N, n = e % N;
-    TO* o = out.p + m * out.stride[0] + n * out.stride[1];
-    float a = acc ? ld(o) : 0.0f;
-    const TL* l = lhs.p + m * lhs.stride[0];
-    const TR* r = rhs.p + n * rhs.stride[1];
+  // Each thread owns a block of up to kB x kB outputs, so every lhs and rhs element it loads
+  // feeds kB products instead of one (rows and columns past the output are computed on
+  // clamped indices and not stored). Each output still sums its products in k order.
+  constexpr int kB = 4;
+  const long long mb = (M + kB - 1) / kB, nb = (N + kB - 1) / kB;
+  for (long long blk = threadIdx.x; blk < mb * nb; blk += kThreads) {
+    const long long m0 = (blk / nb) * kB, n0 = (blk % nb) * kB;
+    const TL* l[kB];
+    const TR* r[kB];
+    float a[kB][kB];
+#pragma unroll
+    for (int i = 0; i < kB; ++i) l[i] = lhs.p + (m0 + i < M ? m0 + i : M - 1) * lhs.stride[0];
+#pragma unroll
+    for (int j = 0; j < kB; ++j) r[j] = rhs.p + (n0 + j < N ? n0 + j : N - 1) * rhs.stride[1];
+#pragma unroll
+    for (int i = 0; i < kB; ++i)
+#pragma unroll
+      for (int j = 0; j < kB; ++j)
+        a[i][j] = acc && m0 + i < M && n0 + j < N ? ld(out.p + (m0 + i) * out.stride[0] + (n0 + j) * out.stride[1])
+                                                  : 0.0f;
     for (long long k = 0; k < K; ++k) {
-      const float prod = ld(l + k * lhs.stride[1]) * ld(r + k * rhs.stride[0]);
-      a = a + prod;
+      float lv[kB], rv[kB];
+#pragma unroll
+      for (int i = 0; i < kB; ++i) lv[i] = ld(l[i] + k * lhs.stride[1]);
+#pragma unroll
+      for (int j = 0; j < kB; ++j) rv[j] = ld(r[j] + k * rhs.stride[0]);
+#pragma unroll
+      for (int i = 0; i < kB; ++i)
+#pragma unroll
+        for (int j = 0; j < kB; ++j) {
+          const float prod = lv[i] * rv[j];
+          a[i][j] = a[i][j] + prod;
+        }
     }
-    st(o, a);
+#pragma unroll
+    for (int i = 0; i < kB; ++i)
+#pragma unroll
+      for (int j = 0; j < kB; ++j)
+        if (m0 + i < M && n0 + j < N) st(out.p + (m0 + i) * out.stride[0] + (n0 + j) * out.stride[1], a[i][j]);
   }
   sync();
 }
