@@ -3,7 +3,8 @@
 //
 // Work split: a workgroup holds query rows of one (b,h), 32 per wave (Cfg<D>: 8 waves for
 // D=128, 4 for D=64 and for D=128 grids too small to give every CU an 8-wave workgroup;
-// two waves per SIMD either way). Key/value tiles of 64 keys are copied
+// two waves per SIMD either way; large non-causal grids run persistent workgroups, kPersist
+// below). Key/value tiles of 64 keys are copied
 // HBM -> LDS into rings of kStages buffers each for K and V (2 by default; 3 or 4 when the
 // lowering's memory_stage asks for a deeper ring) and shared by the workgroup's waves. Workgroup
 // ids are dealt to the 8 XCDs round-robin; they are remapped so that each XCD runs the query
