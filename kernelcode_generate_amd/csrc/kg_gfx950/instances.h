@@ -37,15 +37,16 @@ KG_GEMM_PIPE_INSTANCES(F16Tag, 256, false)
 KG_GEMM_PIPE_INSTANCES(F16Tag, 256, true)
 #undef KG_GEMM_PIPE_INSTANCES
 #undef KG_GEMM_PIPE_INSTANCE
-#define KG_GEMM_QUAD_INSTANCE(TAG, ST)                                                                                  \
-  KG_INSTANCE hipError_t launch_gemm_quad<TAG, ST>(const uint16_t*, const uint16_t*, uint16_t*, const void*, int, int, int, \
-                                                   int, long long, long long, long long, hipStream_t);
-KG_GEMM_QUAD_INSTANCE(Bf16Tag, 2)
-KG_GEMM_QUAD_INSTANCE(Bf16Tag, 3)
-KG_GEMM_QUAD_INSTANCE(Bf16Tag, 4)
-KG_GEMM_QUAD_INSTANCE(F16Tag, 2)
-KG_GEMM_QUAD_INSTANCE(F16Tag, 3)
-KG_GEMM_QUAD_INSTANCE(F16Tag, 4)
+#define KG_GEMM_QUAD_INSTANCE(TAG, ST, TM)                                                                              \
+  KG_INSTANCE hipError_t launch_gemm_quad<TAG, ST, TM>(const uint16_t*, const uint16_t*, uint16_t*, const void*, int, int, \
+                                                       int, int, long long, long long, long long, hipStream_t);
+#define KG_GEMM_QUAD_INSTANCES(TAG, TM) \
+  KG_GEMM_QUAD_INSTANCE(TAG, 2, TM) KG_GEMM_QUAD_INSTANCE(TAG, 3, TM) KG_GEMM_QUAD_INSTANCE(TAG, 4, TM)
+KG_GEMM_QUAD_INSTANCES(Bf16Tag, 256)
+KG_GEMM_QUAD_INSTANCES(Bf16Tag, 128)
+KG_GEMM_QUAD_INSTANCES(F16Tag, 256)
+KG_GEMM_QUAD_INSTANCES(F16Tag, 128)
+#undef KG_GEMM_QUAD_INSTANCES
 #undef KG_GEMM_QUAD_INSTANCE
 #endif
 

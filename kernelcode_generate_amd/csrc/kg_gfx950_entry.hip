@@ -378,13 +378,16 @@ int launch_gemm_mfma(const Mem& out, const Mem& lhs, const Mem& rhs, const Mem& 
     if (partial == nullptr) splits = 1;  // no workspace: the whole K range in one pass
   }
   const int k_chunk = splits > 1 ? (int)chunk : 0;
-  if (tm == 256 && !ragged && splits == 1) {
-    // whole 256 x 256 tiles that fill the chip: four waves of 128 x 128 (same MFMA sequence
-    // per output block as the eight-wave kernel, so the same bits)
+  if (!ragged && splits == 1 && (tm == 256 || grid >= kNumCUs)) {
+    // whole tiles that fill the chip: four waves of (tm/2) x 128 (same MFMA sequence per
+    // output block as the eight-wave kernel, so the same bits)
     hipError_t e = hipSuccess;
-    if (stages == 2) e = launch_gemm_quad<Tag, 2>(A, B, C, bp, bias_kind, M, N, K, lda, ldb, ldc, g_stream);
-    else if (stages == 3) e = launch_gemm_quad<Tag, 3>(A, B, C, bp, bias_kind, M, N, K, lda, ldb, ldc, g_stream);
-    else e = launch_gemm_quad<Tag, 4>(A, B, C, bp, bias_kind, M, N, K, lda, ldb, ldc, g_stream);
+#define KG_GEMM_QUAD(TM)                                                                                          \
+  if (stages == 2) e = launch_gemm_quad<Tag, 2, TM>(A, B, C, bp, bias_kind, M, N, K, lda, ldb, ldc, g_stream);      \
+  else if (stages == 3) e = launch_gemm_quad<Tag, 3, TM>(A, B, C, bp, bias_kind, M, N, K, lda, ldb, ldc, g_stream); \
+  else e = launch_gemm_quad<Tag, 4, TM>(A, B, C, bp, bias_kind, M, N, K, lda, ldb, ldc, g_stream);
+    if (tm == 256) { KG_GEMM_QUAD(256) } else { KG_GEMM_QUAD(128) }
+#undef KG_GEMM_QUAD
     if (e != hipSuccess) return fail(kHipFailure, "matmul(mfma-quad): %s", hipGetErrorString(e));
     return finish_launch("matmul(mfma-quad)");
   }

@@ -164,6 +164,40 @@ def test_four_wave_tiles_match_eight_wave_kernel(device, dtype_name, bias_kind, 
 
 
 @pytest.mark.parametrize(
+    "dtype_name,bias_kind,k",
+    [("bfloat16", None, 1024), ("float16", "f32", 1024), ("bfloat16", "same", 1056)],
+    ids=["bf16-k1024", "f16-bias32-k1024", "bf16-bias16-k1056"])
+def test_four_wave_128_row_tiles_match_eight_wave_kernel(device, dtype_name, bias_kind, k):
+    """Outputs whose 256 x 256 tiles would leave CUs idle but whose 128 x 256 tiles fill the
+    chip (2048 x 4096: 128 and 256 tiles) run on four waves of 64 x 128; the same rows
+    computed again as a ragged 1000-row matmul (the eight-wave kernel's ragged form, 128
+    tiles, K not split) must give the same bits: both issue one 16x16x32 MFMA per 32-deep
+    slice and output block, in k order, and round once. K = 1024 is the exact-K form, 1056
+    the general loop."""
+
+    import torch
+
+    tdt = getattr(torch, dtype_name)
+    m, n = 2048, 4096
+    g = torch.Generator(device=device).manual_seed(78)
+    a = (torch.randn(m, k, generator=g, device=device) * 0.1).to(tdt)
+    b = (torch.randn(k, n, generator=g, device=device) * 0.1).to(tdt)
+    bias = None
+    if bias_kind == "f32":
+        bias = torch.randn(n, generator=g, device=device)
+    elif bias_kind == "same":
+        bias = torch.randn(n, generator=g, device=device).to(tdt)
+    full = torch.full((m, n), float("nan"), dtype=tdt, device=device)
+    print(f"[matmul] four-wave 128-row tiles {m}x{n}x{k} {dtype_name} bias={bias_kind}", flush=True)
+    native.matmul(full, a, b, bias)
+    for r0 in (0, 1048):
+        part = torch.full((1000, n), float("nan"), dtype=tdt, device=device)
+        print(f"[matmul] eight-wave ragged rows {r0}:{r0 + 1000}", flush=True)
+        native.matmul(part, a[r0:r0 + 1000].contiguous(), b, bias)
+        assert torch.equal(full[r0:r0 + 1000], part), f"rows {r0}:{r0 + 1000}"
+
+
+@pytest.mark.parametrize(
     "shape,dtype_name,bias_kind,rows",
     [
         ((16, 4096, 4096), "bfloat16", "f32", None),  # 16 tiles: 16 K chunks of 256
