@@ -44,8 +44,8 @@ def include_flags() -> list[str]:
     return [f"-I{REPO_ROOT / 'include'}", f"-I{CSRC}"]
 
 
-SOURCES = ("kg_gfx950_entry.hip", "kg_gfx950_gemm.hip", "kg_gfx950_fa.hip", "kg_gfx950_fa_persist.hip",
-           "kg_gfx950_conv_rowvec.hip", "kg_gfx950_conv_igemm.hip")
+SOURCES = ("kg_gfx950_entry.hip", "kg_gfx950_gemm.hip", "kg_gfx950_gemm_quad.hip", "kg_gfx950_fa.hip",
+           "kg_gfx950_fa_persist.hip", "kg_gfx950_conv_rowvec.hip", "kg_gfx950_conv_igemm.hip")
 
 
 def build_library(output: Path = OUTPUT, extra_flags: tuple[str, ...] = (), verbose: bool = False) -> Path:

@@ -37,6 +37,9 @@ KG_GEMM_PIPE_INSTANCES(F16Tag, 256, false)
 KG_GEMM_PIPE_INSTANCES(F16Tag, 256, true)
 #undef KG_GEMM_PIPE_INSTANCES
 #undef KG_GEMM_PIPE_INSTANCE
+#endif
+
+#if !defined(KG_INSTANTIATE) || defined(KG_INSTANTIATE_GEMM_QUAD)
 #define KG_GEMM_QUAD_INSTANCE(TAG, ST, TM)                                                                              \
   KG_INSTANCE hipError_t launch_gemm_quad<TAG, ST, TM>(const uint16_t*, const uint16_t*, uint16_t*, const void*, int, int, \
                                                        int, int, long long, long long, long long, hipStream_t);
