@@ -239,7 +239,10 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
   const char* Kb = reinterpret_cast<const char*>(K + kv_base);
   const char* Vb = reinterpret_cast<const char*>(V + kv_base);
   uint16_t* Oh = O + (long long)bh * s_q * D;
-  // the next item of a persistent workgroup (has_next false: none, or not persistent)
+  // the next item of a persistent workgroup (has_next false: none, or not persistent; the
+  // persistent form is non-causal, so query blocks keep their order). Only the persistent
+  // form's copies and Q staging read these; the masks and the masked epilogue use
+  // wave_q_lo / q_row0 below, which stay those of the first item.
   bool has_next = false;
   int m0_next = 0;
   const uint16_t* Qn = Q;
