@@ -229,6 +229,7 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
   const int nmb = (s_q + kBM - 1) / kBM;
   const int items = nmb * bh_count;
   int item = blockIdx.x;  // work item (query block): the workgroup id, or for kPersist the first
+  if (kPersist && item >= items) return;  // (the launcher gives every workgroup at least two)
   const int lin = xcd_block(item, items);
   const int bh = lin / nmb;
   int mb = lin - bh * nmb;
