@@ -214,11 +214,12 @@ __global__ __launch_bounds__((fa::Cfg<D, W>::kThreads), (fa::Cfg<D, W>::kPerCU))
   constexpr int kKAhead = 3;         // K fragments read ahead of their MFMAs
   static_assert(kStages >= 2 && kStages <= 4, "K/V ring depth");
   static_assert(!kPersist || (!kCausal && !kMasked && kStages == 2), "persistent form: whole non-causal tiles");
-  // persistent form: each wave's output staging region of 32 rows follows the ring (the ring
-  // holds the next item's first tiles while the outputs leave)
-  constexpr int kOutBytes = kPersist ? kWaves * 32 * RB : 0;
+  // persistent form: each wave's staging region of 32 rows follows the ring; it takes the
+  // next item's Q rows, then this item's output rows (the ring holds the next item's first
+  // tiles while the outputs leave)
+  constexpr int kStagingBytes = kPersist ? kWaves * 32 * RB : 0;
 
-  __shared__ __attribute__((aligned(1024))) u32x4 lds[(2 * kStages * TB + kOutBytes) / 16];  // K ring, V ring, outputs
+  __shared__ __attribute__((aligned(1024))) u32x4 lds[(2 * kStages * TB + kStagingBytes) / 16];  // K ring, V ring, staging
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
