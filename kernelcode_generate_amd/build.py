@@ -21,15 +21,15 @@ OUTPUT = PACKAGE_DIR / "libkg_gfx950.so"
 PROBE_OUTPUT = PACKAGE_DIR / "libkg_gfx950_probe.so"  # bench.py's measurement library
 OFFLOAD_ARCH = "gfx950"
 
+# turns off the packed-fp32 target feature: every hipcc line that builds device code carries it
+NO_PACKED_FP32 = ("-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops")
+
 HIP_FLAGS = (
     "-O3",
     "-std=c++17",
     f"--offload-arch={OFFLOAD_ARCH}",
     "-fPIC",
-    "-Xclang",
-    "-target-feature",
-    "-Xclang",
-    "-packed-fp32-ops",
+    *NO_PACKED_FP32,
 )
 
 

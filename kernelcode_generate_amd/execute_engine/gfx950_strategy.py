@@ -5,8 +5,9 @@ introduced by ``// __KG_BUNDLE_FILE__:<relative path>`` lines (the reference's m
 kernel_gen/dsl/gen_kernel/emit/register.py:69; path checks as in
 builtin_strategy/cuda_sm89.py:62-92). The main file is ``kernel.hip``.
 
-Build: ``hipcc -std=c++17 --offload-arch=gfx950 -O2 -shared -fPIC -I<repo>/include
--I<bundle dir> kernel.hip -o libkernel.so`` linked against libkg_gfx950.so (the prebuilt
+Build: ``hipcc -std=c++17 --offload-arch=gfx950 -O2 -shared -fPIC -Xclang -target-feature
+-Xclang -packed-fp32-ops -I<repo>/include -I<bundle dir> kernel.hip -o libkernel.so`` (the
+packed-fp32 feature is always off, whatever flags the request carries) linked against libkg_gfx950.so (the prebuilt
 gfx950 kernels and their C ABI), in a private work directory that
 ``CompiledKernel.close()`` removes (compiler.py:232-246 of the reference). Failures map to
 ``source_empty_or_invalid`` / ``compile_failed``.
@@ -21,7 +22,7 @@ from functools import partial
 from pathlib import Path
 
 from .. import native
-from ..build import OFFLOAD_ARCH, REPO_ROOT, hipcc
+from ..build import NO_PACKED_FP32, OFFLOAD_ARCH, REPO_ROOT, hipcc
 from .compiler import COMPILE_FAILED, SOURCE_EMPTY_OR_INVALID, CompiledKernel, CompileRequest, execute_engine_error
 from .runtime_args import parse_allow_absent
 from .strategy import register_compile_strategy
@@ -87,6 +88,7 @@ class Gfx950CompileStrategy:
             for extra in ("-O2", "-shared", "-fPIC"):
                 if extra not in flags:
                     flags.append(extra)
+            flags.extend(NO_PACKED_FP32)
             cmd = [
                 request.compiler or hipcc(),
                 *flags,

@@ -174,12 +174,25 @@ def test_fake_compiler_command_line(tmp_path):
     argv = (tmp_path / "argv.log").read_text()
     assert "--offload-arch=gfx950" in argv and "-shared" in argv and "-fPIC" in argv and "-std=c++17" in argv
     assert "kernel.hip" in argv and "libkg_gfx950.so" in argv and "-Wl,-rpath," in argv
+    assert "-Xclang -target-feature -Xclang -packed-fp32-ops" in argv
     assert kernel.target == "gfx950" and kernel.entry_point == "kg_execute_entry"
     work = Path(kernel.soname_path).parent
     assert work.is_dir()
     kernel.close()
     assert not work.exists()
     kernel.close()  # idempotent
+
+
+def test_packed_fp32_stays_off_with_caller_flags(tmp_path):
+    """A caller's own flag list replaces the default one, but every device build still
+    turns the packed-fp32 target feature off."""
+
+    fake = _fake_hipcc(tmp_path)
+    kernel = ExecutionEngine("gfx950", compiler=str(fake), compiler_flags=("-std=c++17", "-O1")).compile(
+        source="int x;", function="f")
+    argv = (tmp_path / "argv.log").read_text()
+    assert "-O1" in argv and "-Xclang -target-feature -Xclang -packed-fp32-ops" in argv
+    kernel.close()
 
 
 def test_fake_compiler_failure_phrase(tmp_path):
