@@ -91,16 +91,39 @@ __device__ __forceinline__ long long numel(const View<T, R>& v) {
   return n;
 }
 
+// Row-major multi-index of element i over R extents (none of them 0), with 32-bit divisions
+// where the index and the extents fit: a 64-bit division is a long instruction sequence on
+// the GPU, and this runs once per element of every operation.
+template <int R>
+__device__ __forceinline__ void unravel(long long i, const long long (&shape)[R], long long (&idx)[R]) {
+  bool narrow = i <= 0x7fffffffll;
+#pragma unroll
+  for (int d = 0; d < R; ++d) narrow = narrow && shape[d] <= 0x7fffffffll;
+  if (narrow) {
+    uint32_t u = (uint32_t)i;
+#pragma unroll
+    for (int d = R - 1; d >= 0; --d) {
+      const uint32_t e = (uint32_t)shape[d];
+      idx[d] = u % e;
+      u /= e;
+    }
+    return;
+  }
+#pragma unroll
+  for (int d = R - 1; d >= 0; --d) {
+    idx[d] = i % shape[d];
+    i /= shape[d];
+  }
+}
+
 // element offset of the i-th element (row-major order over the view's shape)
 template <typename T, int R>
 __device__ __forceinline__ long long offset_of(const View<T, R>& v, long long i) {
+  long long idx[R];
+  unravel(i, v.shape, idx);
   long long off = 0;
 #pragma unroll
-  for (int d = R - 1; d >= 0; --d) {
-    const long long e = v.shape[d];
-    off += (i % e) * v.stride[d];
-    i /= e;
-  }
+  for (int d = 0; d < R; ++d) off += idx[d] * v.stride[d];
   return off;
 }
 
@@ -175,6 +198,24 @@ __device__ __forceinline__ View<T, RO> reshape(const View<T, R>& src, const long
 
 __device__ __forceinline__ void sync() { __syncthreads(); }
 
+// Element loop of the element-wise operations: each thread takes i = threadIdx.x,
+// threadIdx.x + kThreads, ... < n, and evaluates kU of its elements (value(i)) before it
+// stores them (store(i, v)), so that their loads are in flight together. Each element is
+// still read before it is written; elements of different threads were never ordered.
+template <typename Value, typename Store>
+__device__ __forceinline__ void each_element(long long n, Value value, Store store) {
+  constexpr int kU = 4;
+  long long i = threadIdx.x;
+  for (; i + (kU - 1) * kThreads < n; i += kU * kThreads) {
+    float v[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) v[u] = value(i + u * kThreads);
+#pragma unroll
+    for (int u = 0; u < kU; ++u) store(i + u * kThreads, v[u]);
+  }
+  for (; i < n; i += kThreads) store(i, value(i));
+}
+
 // ---- dma ----------------------------------------------------------------------------------
 template <typename T, int R>
 __device__ void fill(const View<T, R>& t, float value) {
@@ -193,7 +234,9 @@ __device__ void copy(const View<TD, RD>& dst, const View<TS, RS>& src, int* err)
     sync();
     return;
   }
-  for (long long i = threadIdx.x; i < n; i += kThreads) st(dst.p + offset_of(dst, i), ld(src.p + offset_of(src, i)));
+  each_element(
+      n, [&](long long i) { return ld(src.p + offset_of(src, i)); },
+      [&](long long i, float v) { st(dst.p + offset_of(dst, i), v); });
   sync();
 }
 
@@ -212,19 +255,19 @@ __device__ void broadcast(const View<TD, RD>& dst, const View<TS, RS>& src, int*
     sync();
     return;
   }
-  const long long n = numel(dst);
-  for (long long i = threadIdx.x; i < n; i += kThreads) {
-    long long rem = i, so = 0, doff = 0;
+  each_element(
+      numel(dst),
+      [&](long long i) {
+        long long idx[RD], so = 0;
+        unravel(i, dst.shape, idx);
 #pragma unroll
-    for (int d = RD - 1; d >= 0; --d) {
-      const long long idx = rem % dst.shape[d];
-      rem /= dst.shape[d];
-      doff += idx * dst.stride[d];
-      const int s = d - (RD - RS);
-      if (s >= 0 && src.shape[s] != 1) so += idx * src.stride[s];
-    }
-    st(dst.p + doff, ld(src.p + so));
-  }
+        for (int d = RD - 1; d >= 0; --d) {
+          const int s = d - (RD - RS);
+          if (s >= 0 && src.shape[s] != 1) so += idx[d] * src.stride[s];
+        }
+        return ld(src.p + so);
+      },
+      [&](long long i, float v) { st(dst.p + offset_of(dst, i), v); });
   sync();
 }
 
@@ -240,18 +283,16 @@ __device__ void transpose(const View<TD, R>& dst, const View<TS, R>& src, const 
     sync();
     return;
   }
-  const long long n = numel(dst);
-  for (long long i = threadIdx.x; i < n; i += kThreads) {
-    long long rem = i, so = 0, doff = 0;
+  each_element(
+      numel(dst),
+      [&](long long i) {
+        long long idx[R], so = 0;
+        unravel(i, dst.shape, idx);
 #pragma unroll
-    for (int d = R - 1; d >= 0; --d) {
-      const long long idx = rem % dst.shape[d];
-      rem /= dst.shape[d];
-      doff += idx * dst.stride[d];
-      so += idx * src.stride[perm[d]];
-    }
-    st(dst.p + doff, ld(src.p + so));
-  }
+        for (int d = R - 1; d >= 0; --d) so += idx[d] * src.stride[perm[d]];
+        return ld(src.p + so);
+      },
+      [&](long long i, float v) { st(dst.p + offset_of(dst, i), v); });
   sync();
 }
 
@@ -284,6 +325,9 @@ __device__ void matmul(const View<TO, 2>& out, const View<TL, 2>& lhs, const Vie
       for (int j = 0; j < kB; ++j)
         a[i][j] = acc && m0 + i < M && n0 + j < N ? ld(out.p + (m0 + i) * out.stride[0] + (n0 + j) * out.stride[1])
                                                   : 0.0f;
+    // unrolled so that the loads of several k steps are in flight together (one wave per SIMD
+    // here: the loop is bound by load latency, not by the products)
+#pragma unroll 4
     for (long long k = 0; k < K; ++k) {
       float lv[kB], rv[kB];
 #pragma unroll
@@ -320,21 +364,19 @@ __device__ void img2col2d(const View<TO, 6>& out, const View<TI, 4>& in, long lo
     sync();
     return;
   }
-  const long long n = numel(out);
-  for (long long i = threadIdx.x; i < n; i += kThreads) {
-    long long rem = i;
-    const long long x = rem % out.shape[5]; rem /= out.shape[5];
-    const long long y = rem % out.shape[4]; rem /= out.shape[4];
-    const long long q = rem % kw; rem /= kw;
-    const long long r = rem % kh; rem /= kh;
-    const long long c = rem % out.shape[1]; rem /= out.shape[1];
-    const long long b = rem;
-    const long long sy = y * sh + r * dh - ph, sx = x * sw + q * dw - pl;
-    float v = 0.0f;
-    if (sy >= 0 && sy < H && sx >= 0 && sx < W)
-      v = ld(in.p + b * in.stride[0] + c * in.stride[1] + sy * in.stride[2] + sx * in.stride[3]);
-    st(out.p + offset_of(out, i), v);
-  }
+  each_element(
+      numel(out),
+      [&](long long i) {
+        long long idx[6];  // b, c, r (kh), q (kw), y, x: out.shape[2] == kh and out.shape[3] == kw
+        unravel(i, out.shape, idx);
+        const long long b = idx[0], c = idx[1], r = idx[2], q = idx[3], y = idx[4], x = idx[5];
+        const long long sy = y * sh + r * dh - ph, sx = x * sw + q * dw - pl;
+        float v = 0.0f;
+        if (sy >= 0 && sy < H && sx >= 0 && sx < W)
+          v = ld(in.p + b * in.stride[0] + c * in.stride[1] + sy * in.stride[2] + sx * in.stride[3]);
+        return v;
+      },
+      [&](long long i, float v) { st(out.p + offset_of(out, i), v); });
   sync();
 }
 
@@ -346,8 +388,9 @@ __device__ void exp(const View<TO, R>& out, const View<TI, R>& in, int* err) {
     sync();
     return;
   }
-  for (long long i = threadIdx.x; i < n; i += kThreads)
-    st(out.p + offset_of(out, i), (float)::exp((double)ld(in.p + offset_of(in, i))));
+  each_element(
+      n, [&](long long i) { return ld(in.p + offset_of(in, i)); },
+      [&](long long i, float v) { st(out.p + offset_of(out, i), (float)::exp((double)v)); });
   sync();
 }
 
@@ -390,21 +433,21 @@ __device__ void binary(const View<TO, R>& out, const View<TL, R>& lhs, const Vie
     sync();
     return;
   }
-  const long long n = numel(out);
-  // every thread reads its elements before any is written (out may alias an operand)
-  for (long long i = threadIdx.x; i < n; i += kThreads) {
-    const float a = ld(lhs.p + offset_of(lhs, i));
-    const float b = ld(rhs.p + offset_of(rhs, i));
-    float r;
-    switch (kind) {
-      case 0: r = a + b; break;
-      case 1: r = a - b; break;
-      case 2: r = a * b; break;
-      case 3: r = (float)((double)a / (double)b); break;
-      default: r = a > b ? a : b; break;
-    }
-    st(out.p + offset_of(out, i), r);
-  }
+  // every element is read before it is written (out may alias an operand)
+  each_element(
+      numel(out),
+      [&](long long i) {
+        const float a = ld(lhs.p + offset_of(lhs, i));
+        const float b = ld(rhs.p + offset_of(rhs, i));
+        switch (kind) {
+          case 0: return a + b;
+          case 1: return a - b;
+          case 2: return a * b;
+          case 3: return (float)((double)a / (double)b);
+          default: return a > b ? a : b;
+        }
+      },
+      [&](long long i, float v) { st(out.p + offset_of(out, i), v); });
   sync();
 }
 
