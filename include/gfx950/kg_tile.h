@@ -36,7 +36,7 @@
 
 namespace kg_tile {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 1024;
 
 // ---- elements -------------------------------------------------------------------------
 struct Bf16 {

@@ -11,7 +11,7 @@ headers and runs the whole body on one thread of one block
     workgroup takes iteration `it = blockIdx.x, blockIdx.x + gridDim.x, ...` of their
     product, so any trip count runs on a bounded grid;
   - every other operation becomes a call of include/gfx950/kg_tile.h, executed by the
-    workgroup's 256 threads on strided views, with a barrier after it; loops and
+    workgroup's threads (kg_tile::kThreads) on strided views, with a barrier after it; loops and
     branches inside the body stay loops and branches (uniform across the workgroup);
   - every dma.alloc gets a fixed slice of the workgroup's part of a scratch workspace.
     Its size is the largest the tile can take: each dimension's maximum over the loop
@@ -396,7 +396,7 @@ class _Emitter:
         L.append("  int* err;")
         L.append("};")
         L.append("")
-        L.append("__global__ __launch_bounds__(256) void kg_gfx950_generated_kernel(KgArgs a) {")
+        L.append("__global__ __launch_bounds__(kg_tile::kThreads) void kg_gfx950_generated_kernel(KgArgs a) {")
         L.append("  char* wsb = a.ws + (long long)blockIdx.x * a.ws_per_block;")
         L.append("  (void)wsb;")
         for p in f.params:
@@ -569,7 +569,7 @@ class _Emitter:
             "  a.ws = ws;",
             "  // the error word starts at zero: cleared by a kernel (no memset node if a caller captures the stream)",
             "  hipLaunchKernelGGL(kg_gfx950_clear_word, dim3(1), dim3(64), 0, stream, a.err);",
-            "  hipLaunchKernelGGL(kg_gfx950_generated_kernel, dim3((unsigned)grid), dim3(256), 0, stream, a);",
+            "  hipLaunchKernelGGL(kg_gfx950_generated_kernel, dim3((unsigned)grid), dim3(kg_tile::kThreads), 0, stream, a);",
             "  int err_word = 0;",
             "  const bool sync = kg_gfx950_launch_synchronous() != 0;",
             "  if (sync) (void)hipMemcpyAsync(&err_word, a.err, sizeof(int), hipMemcpyDeviceToHost, stream);",
