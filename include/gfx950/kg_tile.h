@@ -297,6 +297,16 @@ __device__ void transpose(const View<TD, R>& dst, const View<TS, R>& src, const 
 }
 
 // ---- kernel -------------------------------------------------------------------------------
+// Operand staging of matmul: lhs[:, k0:k0+KC] and rhs[k0:k0+KC, :] as fp32 in LDS.
+constexpr int kMatmulStage = 4096;  // floats per operand (16 KiB each)
+
+// out (+)= lhs @ rhs. Each output sums its products in k order, one product and one add
+// at a time (the reference's arithmetic). Each thread owns a block of up to kB x kB outputs,
+// so every operand element it reads feeds kB products (rows and columns past the output are
+// computed on clamped indices and not stored). When max(M, N) <= kMatmulStage the operands
+// are staged through LDS in k chunks (a workspace tile lives in global memory, and with one
+// workgroup per CU its load latency is what the loop waits on); otherwise they are read in
+// place.
 template <typename TO, typename TL, typename TR>
 __device__ void matmul(const View<TO, 2>& out, const View<TL, 2>& lhs, const View<TR, 2>& rhs, bool acc, int* err) {
   const long long M = out.shape[0], N = out.shape[1], K = lhs.shape[1];
@@ -305,48 +315,108 @@ __device__ void matmul(const View<TO, 2>& out, const View<TL, 2>& lhs, const Vie
     sync();
     return;
   }
-  // Each thread owns a block of up to kB x kB outputs, so every lhs and rhs element it loads
-  // feeds kB products instead of one (rows and columns past the output are computed on
-  // clamped indices and not stored). Each output still sums its products in k order.
   constexpr int kB = 4;
-  const long long mb = (M + kB - 1) / kB, nb = (N + kB - 1) / kB;
-  for (long long blk = threadIdx.x; blk < mb * nb; blk += kThreads) {
-    const long long m0 = (blk / nb) * kB, n0 = (blk % nb) * kB;
-    const TL* l[kB];
-    const TR* r[kB];
+  const long long mb = (M + kB - 1) / kB, nb = (N + kB - 1) / kB, blocks = mb * nb;
+  const bool staged = M <= kMatmulStage && N <= kMatmulStage;
+  __shared__ float s_l[kMatmulStage], s_r[kMatmulStage];
+  // k chunk: M x KC and KC x N floats fit the stages (KC >= 1 when staged)
+  const long long mn = M > N ? M : N;
+  const long long KC = staged && mn > 0 ? (kMatmulStage / mn < K ? kMatmulStage / mn : K) : K;
+  // rounds of kThreads blocks, the same count on every thread (the staging is cooperative)
+  for (long long blk0 = 0; blk0 < blocks; blk0 += kThreads) {
+    const long long blk = blk0 + threadIdx.x;
+    const bool active = blk < blocks;
+    const long long m0 = active ? (blk / nb) * kB : 0, n0 = active ? (blk % nb) * kB : 0;
+    long long mi[kB], nj[kB];
+#pragma unroll
+    for (int i = 0; i < kB; ++i) mi[i] = m0 + i < M ? m0 + i : M - 1;
+#pragma unroll
+    for (int j = 0; j < kB; ++j) nj[j] = n0 + j < N ? n0 + j : N - 1;
     float a[kB][kB];
-#pragma unroll
-    for (int i = 0; i < kB; ++i) l[i] = lhs.p + (m0 + i < M ? m0 + i : M - 1) * lhs.stride[0];
-#pragma unroll
-    for (int j = 0; j < kB; ++j) r[j] = rhs.p + (n0 + j < N ? n0 + j : N - 1) * rhs.stride[1];
 #pragma unroll
     for (int i = 0; i < kB; ++i)
 #pragma unroll
       for (int j = 0; j < kB; ++j)
-        a[i][j] = acc && m0 + i < M && n0 + j < N ? ld(out.p + (m0 + i) * out.stride[0] + (n0 + j) * out.stride[1])
-                                                  : 0.0f;
-    // unrolled so that the loads of several k steps are in flight together (one wave per SIMD
-    // here: the loop is bound by load latency, not by the products)
+        a[i][j] = active && acc && m0 + i < M && n0 + j < N
+                      ? ld(out.p + (m0 + i) * out.stride[0] + (n0 + j) * out.stride[1])
+                      : 0.0f;
+    if (staged) {
+      for (long long k0 = 0; k0 < K; k0 += KC) {
+        const int kc = (int)(K - k0 < KC ? K - k0 : KC);
+        // lhs chunk k-major (s_l[k * M + m]: a thread's kB rows are adjacent), rhs row-major;
+        // element e of a chunk is read in the operand's row-major order
+        const uint32_t um = (uint32_t)M, un = (uint32_t)N, uk = (uint32_t)kc;
+        each_element(
+            M * kc,
+            [&](long long e) {
+              const uint32_t m = (uint32_t)e / uk, k = (uint32_t)e % uk;
+              return ld(lhs.p + m * lhs.stride[0] + (k0 + k) * lhs.stride[1]);
+            },
+            [&](long long e, float v) { s_l[((uint32_t)e % uk) * um + (uint32_t)e / uk] = v; });
+        each_element(
+            (long long)kc * N,
+            [&](long long e) {
+              const uint32_t k = (uint32_t)e / un, n = (uint32_t)e % un;
+              return ld(rhs.p + (k0 + k) * rhs.stride[0] + n * rhs.stride[1]);
+            },
+            [&](long long e, float v) { s_r[e] = v; });
+        sync();
+        if (active) {
+          const float* l[kB];
+          const float* r[kB];
+#pragma unroll
+          for (int i = 0; i < kB; ++i) l[i] = s_l + mi[i];
+#pragma unroll
+          for (int j = 0; j < kB; ++j) r[j] = s_r + nj[j];
 #pragma unroll 4
-    for (long long k = 0; k < K; ++k) {
-      float lv[kB], rv[kB];
+          for (int k = 0; k < kc; ++k) {
+            float lv[kB], rv[kB];
 #pragma unroll
-      for (int i = 0; i < kB; ++i) lv[i] = ld(l[i] + k * lhs.stride[1]);
+            for (int i = 0; i < kB; ++i) lv[i] = l[i][(long long)k * M];
 #pragma unroll
-      for (int j = 0; j < kB; ++j) rv[j] = ld(r[j] + k * rhs.stride[0]);
+            for (int j = 0; j < kB; ++j) rv[j] = r[j][(long long)k * N];
+#pragma unroll
+            for (int i = 0; i < kB; ++i)
+#pragma unroll
+              for (int j = 0; j < kB; ++j) {
+                const float prod = lv[i] * rv[j];
+                a[i][j] = a[i][j] + prod;
+              }
+          }
+        }
+        sync();
+      }
+    } else if (active) {
+      const TL* l[kB];
+      const TR* r[kB];
+#pragma unroll
+      for (int i = 0; i < kB; ++i) l[i] = lhs.p + mi[i] * lhs.stride[0];
+#pragma unroll
+      for (int j = 0; j < kB; ++j) r[j] = rhs.p + nj[j] * rhs.stride[1];
+      // unrolled so that the loads of several k steps are in flight together
+#pragma unroll 4
+      for (long long k = 0; k < K; ++k) {
+        float lv[kB], rv[kB];
+#pragma unroll
+        for (int i = 0; i < kB; ++i) lv[i] = ld(l[i] + k * lhs.stride[1]);
+#pragma unroll
+        for (int j = 0; j < kB; ++j) rv[j] = ld(r[j] + k * rhs.stride[0]);
+#pragma unroll
+        for (int i = 0; i < kB; ++i)
+#pragma unroll
+          for (int j = 0; j < kB; ++j) {
+            const float prod = lv[i] * rv[j];
+            a[i][j] = a[i][j] + prod;
+          }
+      }
+    }
+    if (active) {
 #pragma unroll
       for (int i = 0; i < kB; ++i)
 #pragma unroll
-        for (int j = 0; j < kB; ++j) {
-          const float prod = lv[i] * rv[j];
-          a[i][j] = a[i][j] + prod;
-        }
+        for (int j = 0; j < kB; ++j)
+          if (m0 + i < M && n0 + j < N) st(out.p + (m0 + i) * out.stride[0] + (n0 + j) * out.stride[1], a[i][j]);
     }
-#pragma unroll
-    for (int i = 0; i < kB; ++i)
-#pragma unroll
-      for (int j = 0; j < kB; ++j)
-        if (m0 + i < M && n0 + j < N) st(out.p + (m0 + i) * out.stride[0] + (n0 + j) * out.stride[1], a[i][j]);
   }
   sync();
 }
