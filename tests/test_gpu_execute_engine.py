@@ -209,24 +209,28 @@ def _run(fn, args, options=None):
     return dsl_run(fn, tuple(args), pipeline)
 
 
-@pytest.mark.parametrize("variant", ["static", "dyn"])
+@pytest.mark.parametrize("variant", ["static", "dyn", "dyn_chunks", "dyn_wide"])
 def test_per_op_matmul_matches_oracle_bit_for_bit(device, oracle_mod, variant):
     """The per-operation path computes the demo's own loop nest (sequential-k fp32 products
-    and sums, like include/npu_demo/Kernel.h:900-948): it reproduces the oracle exactly."""
+    and sums, like include/npu_demo/Kernel.h:900-948): it reproduces the oracle exactly.
+    The runtime's matmul stages its operands through LDS in k chunks of 4096 // max(M, N):
+    one chunk for 50 x 64 x 17 tiles, three (32, 32, 16) for 96 x 128 x 80 tiles; tiles
+    wider than 4096 read the operands in place."""
 
     from kernelcode_generate_amd.kernel.matmul import inputs_static_tile_static as mod
 
+    m, k, n = (3, 40, 4500) if variant == "dyn_wide" else (97, 130, 75)
     rng = np.random.default_rng(21)
-    lhs = rng.standard_normal((97, 130), dtype=np.float32)
-    rhs = rng.standard_normal((130, 75), dtype=np.float32)
-    bias = rng.standard_normal(75, dtype=np.float32)
-    out = np.zeros((97, 75), np.float32)
+    lhs = rng.standard_normal((m, k), dtype=np.float32)
+    rhs = rng.standard_normal((k, n), dtype=np.float32)
+    bias = rng.standard_normal(n, dtype=np.float32)
+    out = np.zeros((m, n), np.float32)
     if variant == "static":
         r = _run(matmul_inputs_static_tile_static_kernel, (out, lhs, rhs, bias), PER_OP)
         tiles = (mod._TILE_M, mod._TILE_N, mod._TILE_K)
     else:
-        r = _run(matmul_inputs_dynamic_tile_dynamic_kernel, (out, lhs, rhs, bias, 50, 64, 17), PER_OP)
-        tiles = (50, 64, 17)
+        tiles = {"dyn": (50, 64, 17), "dyn_chunks": (96, 128, 80), "dyn_wide": (3, 4500, 40)}[variant]
+        r = _run(matmul_inputs_dynamic_tile_dynamic_kernel, (out, lhs, rhs, bias, *tiles), PER_OP)
     assert r.fused is None and "kg_gfx950_generated_kernel" in r.source
     assert np.array_equal(out, oracle_mod.matmul_demo(lhs, rhs, bias, tiles))
 
