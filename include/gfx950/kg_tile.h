@@ -216,6 +216,66 @@ __device__ __forceinline__ void each_element(long long n, Value value, Store sto
   for (; i < n; i += kThreads) store(i, value(i));
 }
 
+// Multi-index of a thread's elements over one shape: the thread's first element, then the
+// next one kThreads further on, stepped digit by digit with carries (no division per element).
+template <int R>
+struct Walk {
+  long long idx[R], step[R];
+  __device__ __forceinline__ explicit Walk(const long long (&shape)[R]) {
+    unravel(threadIdx.x, shape, idx);
+    long long t = kThreads;
+#pragma unroll
+    for (int d = R - 1; d > 0; --d) {
+      step[d] = t % shape[d];
+      t /= shape[d];
+    }
+    step[0] = t;
+  }
+  // every digit below the first stays under its extent: idx + step + carry < 2 * extent
+  __device__ __forceinline__ void next(const long long (&shape)[R]) {
+    long long c = 0;
+#pragma unroll
+    for (int d = R - 1; d > 0; --d) {
+      idx[d] += step[d] + c;
+      c = idx[d] >= shape[d];
+      if (c) idx[d] -= shape[d];
+    }
+    idx[0] += step[0] + c;
+  }
+  __device__ __forceinline__ long long offset(const long long (&stride)[R]) const {
+    long long off = 0;
+#pragma unroll
+    for (int d = 0; d < R; ++d) off += idx[d] * stride[d];
+    return off;
+  }
+};
+
+// each_element over the n > 0 elements of one shape with a Walk: value(idx) and where(idx)
+// (the element's destination) for kU elements, then store(where, v) for them.
+template <int R, typename Value, typename Where, typename Store>
+__device__ __forceinline__ void each_index(long long n, const long long (&shape)[R], Value value, Where where,
+                                           Store store) {
+  constexpr int kU = 4;
+  Walk<R> w(shape);
+  long long i = threadIdx.x;
+  for (; i + (kU - 1) * kThreads < n; i += kU * kThreads) {
+    float v[kU];
+    long long o[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      v[u] = value(w.idx);
+      o[u] = where(w.idx);
+      w.next(shape);
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) store(o[u], v[u]);
+  }
+  for (; i < n; i += kThreads) {
+    store(where(w.idx), value(w.idx));
+    w.next(shape);
+  }
+}
+
 // ---- dma ----------------------------------------------------------------------------------
 template <typename T, int R>
 __device__ void fill(const View<T, R>& t, float value) {
@@ -233,6 +293,29 @@ __device__ void copy(const View<TD, RD>& dst, const View<TS, RS>& src, int* err)
     if (threadIdx.x == 0 && n > 0) atomicOr(err, 4);
     sync();
     return;
+  }
+  if constexpr (RD == RS) {
+    bool same = n > 0;
+#pragma unroll
+    for (int d = 0; d < RD; ++d) same = same && dst.shape[d] == src.shape[d];
+    if (same) {  // one walk serves both views
+      each_index<RD>(
+          n, dst.shape, [&](const long long (&idx)[RD]) {
+            long long off = 0;
+#pragma unroll
+            for (int d = 0; d < RD; ++d) off += idx[d] * src.stride[d];
+            return ld(src.p + off);
+          },
+          [&](const long long (&idx)[RD]) {
+            long long off = 0;
+#pragma unroll
+            for (int d = 0; d < RD; ++d) off += idx[d] * dst.stride[d];
+            return off;
+          },
+          [&](long long off, float v) { st(dst.p + off, v); });
+      sync();
+      return;
+    }
   }
   each_element(
       n, [&](long long i) { return ld(src.p + offset_of(src, i)); },
@@ -318,10 +401,13 @@ __device__ void matmul(const View<TO, 2>& out, const View<TL, 2>& lhs, const Vie
   constexpr int kB = 4;
   const long long mb = (M + kB - 1) / kB, nb = (N + kB - 1) / kB, blocks = mb * nb;
   const bool staged = M <= kMatmulStage && N <= kMatmulStage;
-  __shared__ float s_l[kMatmulStage], s_r[kMatmulStage];
+  // kB - 1 floats past each stage: the last k step's block may read (and discard) elements
+  // past the chunk's last row or column
+  __shared__ float s_l[kMatmulStage + kB], s_r[kMatmulStage + kB];
   // k chunk: M x KC and KC x N floats fit the stages (KC >= 1 when staged)
   const long long mn = M > N ? M : N;
   const long long KC = staged && mn > 0 ? (kMatmulStage / mn < K ? kMatmulStage / mn : K) : K;
+  const uint32_t um = (uint32_t)M, un = (uint32_t)N;
   // rounds of kThreads blocks, the same count on every thread (the staging is cooperative)
   for (long long blk0 = 0; blk0 < blocks; blk0 += kThreads) {
     const long long blk = blk0 + threadIdx.x;
@@ -345,36 +431,28 @@ __device__ void matmul(const View<TO, 2>& out, const View<TL, 2>& lhs, const Vie
         const int kc = (int)(K - k0 < KC ? K - k0 : KC);
         // lhs chunk k-major (s_l[k * M + m]: a thread's kB rows are adjacent), rhs row-major;
         // element e of a chunk is read in the operand's row-major order
-        const uint32_t um = (uint32_t)M, un = (uint32_t)N, uk = (uint32_t)kc;
-        each_element(
-            M * kc,
-            [&](long long e) {
-              const uint32_t m = (uint32_t)e / uk, k = (uint32_t)e % uk;
-              return ld(lhs.p + m * lhs.stride[0] + (k0 + k) * lhs.stride[1]);
-            },
-            [&](long long e, float v) { s_l[((uint32_t)e % uk) * um + (uint32_t)e / uk] = v; });
-        each_element(
-            (long long)kc * N,
-            [&](long long e) {
-              const uint32_t k = (uint32_t)e / un, n = (uint32_t)e % un;
-              return ld(rhs.p + (k0 + k) * rhs.stride[0] + n * rhs.stride[1]);
-            },
-            [&](long long e, float v) { s_r[e] = v; });
+        const long long lsh[2] = {M, kc}, rsh[2] = {kc, N};
+        each_index<2>(
+            M * kc, lsh, [&](const long long (&x)[2]) { return ld(lhs.p + x[0] * lhs.stride[0] + (k0 + x[1]) * lhs.stride[1]); },
+            [&](const long long (&x)[2]) { return x[1] * M + x[0]; }, [&](long long o, float v) { s_l[(uint32_t)o] = v; });
+        each_index<2>(
+            (long long)kc * N, rsh,
+            [&](const long long (&x)[2]) { return ld(rhs.p + (k0 + x[0]) * rhs.stride[0] + x[1] * rhs.stride[1]); },
+            [&](const long long (&x)[2]) { return x[0] * N + x[1]; }, [&](long long o, float v) { s_r[(uint32_t)o] = v; });
         sync();
         if (active) {
-          const float* l[kB];
-          const float* r[kB];
-#pragma unroll
-          for (int i = 0; i < kB; ++i) l[i] = s_l + mi[i];
-#pragma unroll
-          for (int j = 0; j < kB; ++j) r[j] = s_r + nj[j];
+          // 32-bit LDS indexes with the block's rows and columns as immediate offsets: rows
+          // and columns past the output read neighbouring stage elements, whose products go
+          // to accumulators that are not stored
+          const uint32_t um0 = (uint32_t)m0, un0 = (uint32_t)n0;
 #pragma unroll 4
           for (int k = 0; k < kc; ++k) {
+            const uint32_t lo = (uint32_t)k * um + um0, ro = (uint32_t)k * un + un0;
             float lv[kB], rv[kB];
 #pragma unroll
-            for (int i = 0; i < kB; ++i) lv[i] = l[i][(long long)k * M];
+            for (int i = 0; i < kB; ++i) lv[i] = s_l[lo + i];
 #pragma unroll
-            for (int j = 0; j < kB; ++j) rv[j] = r[j][(long long)k * N];
+            for (int j = 0; j < kB; ++j) rv[j] = s_r[ro + j];
 #pragma unroll
             for (int i = 0; i < kB; ++i)
 #pragma unroll

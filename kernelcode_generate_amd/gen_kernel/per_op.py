@@ -38,6 +38,9 @@ ENUM_LIMIT = 4_000_000
 MAX_GRID = 2048
 SCRATCH_BYTES = 32 << 20  # cap of the allocation-free entry's scratch, per GPU (scratch_bytes)
 MAX_DEVICES = 64
+# largest workspace per workgroup kept in LDS (with the matmul's 32 KiB of operand stages,
+# 128 of the 160 KiB a gfx950 workgroup can hold)
+LDS_WORKSPACE_BYTES = 96 * 1024
 QUERY_GRID = 256  # workgroups of a kernel that distributes work with arch.get_block_id / get_block_num
 
 # Launch queries. Each workgroup is one DSL block; the operations of its body are executed
@@ -380,6 +383,7 @@ class _Emitter:
         L.append("namespace {")
         L.append("using kg_tile::kg_floordiv; using kg_tile::kg_max; using kg_tile::kg_min; using kg_tile::kg_mod;")
         L.append(f"constexpr int kMaxDevices = {MAX_DEVICES};")
+        L.append(f"constexpr long long kLdsWorkspaceBytes = {LDS_WORKSPACE_BYTES};")
         L.append("")
         L.append("struct KgArgs {")
         for p in f.params:
@@ -393,11 +397,13 @@ class _Emitter:
         L.append(f"  long long ws_off[{max(1, len(self.plan.allocs))}];")
         L.append("  long long ws_per_block;")
         L.append("  char* ws;")
+        L.append("  int ws_lds;  // the workspace is the workgroup's dynamic LDS")
         L.append("  int* err;")
         L.append("};")
         L.append("")
         L.append("__global__ __launch_bounds__(kg_tile::kThreads) void kg_gfx950_generated_kernel(KgArgs a) {")
-        L.append("  char* wsb = a.ws + (long long)blockIdx.x * a.ws_per_block;")
+        L.append("  extern __shared__ __attribute__((aligned(16))) char kg_ws_lds[];")
+        L.append("  char* wsb = a.ws_lds ? kg_ws_lds : a.ws + (long long)blockIdx.x * a.ws_per_block;")
         L.append("  (void)wsb;")
         for p in f.params:
             if p.kind == "memory":
@@ -530,6 +536,18 @@ class _Emitter:
             size = " * ".join(dims) if dims else "1LL"
             L.append(f"  a.ws_off[{k}] = off; off += ((({size}) * {ELEMENT_BYTES[m.dtype]}LL) + 255LL) / 256LL * 256LL;")
         L.append("  a.ws_per_block = off;")
+        L += [
+            "  // A workspace of at most kLdsWorkspaceBytes lives in the workgroup's LDS (private to the",
+            "  // workgroup for the launch, like its slice of device memory, at a fraction of the latency);",
+            "  // only the error word is then device memory.",
+            "  a.ws_lds = off > 0 && off <= kLdsWorkspaceBytes;",
+            "  if (a.ws_lds && hipFuncSetAttribute(reinterpret_cast<const void*>(kg_gfx950_generated_kernel),",
+            "                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)off) != hipSuccess) {",
+            "    (void)hipGetLastError();",
+            "    a.ws_lds = 0;",
+            "  }",
+            "  const long long ws_block = a.ws_lds ? 0 : off;  // device-memory workspace per workgroup",
+        ]
         par = self.plan.parallel
         if par:
             trips = " * ".join(
@@ -547,29 +565,30 @@ class _Emitter:
             "  char* ws = nullptr;",
             "  if (no_alloc) {",
             "    // fewer workgroups when the scratch cannot give each its slice (the loop is block-strided)",
-            "    if (a.ws_per_block > kScratchBytes - 256) {",
+            "    if (ws_block > kScratchBytes - 256) {",
             "      char msg[256];",
             f'      snprintf(msg, sizeof(msg), "{function}: %lld bytes of workspace per workgroup exceed the %lld-byte '
-            f'scratch of the allocation-free entry", a.ws_per_block, kScratchBytes - 256);',
+            f'scratch of the allocation-free entry", ws_block, kScratchBytes - 256);',
             "      return kg_gfx950_fail(-3, msg);",
             "    }",
-            "    const long long fit = a.ws_per_block > 0 ? (kScratchBytes - 256) / a.ws_per_block : grid;",
+            "    const long long fit = ws_block > 0 ? (kScratchBytes - 256) / ws_block : grid;",
             ("    if (grid > fit) grid = fit;" if not uses_block_queries(f) else
              f'    if (grid > fit) return kg_gfx950_fail(-3, "{function}: the {QUERY_GRID} workgroups the kernel\'s '
              f'block queries assume do not fit the scratch of the allocation-free entry");'),
             "    if (scratch_of_current_device(&ws) != 0) return -2;",
             "  } else {",
-            "    const size_t bytes = (size_t)(grid * a.ws_per_block) + 256;",
+            "    const size_t bytes = (size_t)(grid * ws_block) + 256;",
             "    if (hipMallocAsync(reinterpret_cast<void**>(&ws), bytes, stream) != hipSuccess) {",
             "      (void)hipGetLastError();",
             f'      return kg_gfx950_fail(-2, "{function}: workspace allocation failed");',
             "    }",
             "  }",
-            "  a.err = reinterpret_cast<int*>(ws + grid * a.ws_per_block);",
+            "  a.err = reinterpret_cast<int*>(ws + grid * ws_block);",
             "  a.ws = ws;",
             "  // the error word starts at zero: cleared by a kernel (no memset node if a caller captures the stream)",
             "  hipLaunchKernelGGL(kg_gfx950_clear_word, dim3(1), dim3(64), 0, stream, a.err);",
-            "  hipLaunchKernelGGL(kg_gfx950_generated_kernel, dim3((unsigned)grid), dim3(kg_tile::kThreads), 0, stream, a);",
+            "  hipLaunchKernelGGL(kg_gfx950_generated_kernel, dim3((unsigned)grid), dim3(kg_tile::kThreads),",
+            "                     a.ws_lds ? (unsigned)off : 0u, stream, a);",
             "  int err_word = 0;",
             "  const bool sync = kg_gfx950_launch_synchronous() != 0;",
             "  if (sync) (void)hipMemcpyAsync(&err_word, a.err, sizeof(int), hipMemcpyDeviceToHost, stream);",
