@@ -280,7 +280,16 @@ __device__ __forceinline__ void each_index(long long n, const long long (&shape)
 template <typename T, int R>
 __device__ void fill(const View<T, R>& t, float value) {
   const long long n = numel(t);
-  for (long long i = threadIdx.x; i < n; i += kThreads) st(t.p + offset_of(t, i), value);
+  if (n > 0)
+    each_index<R>(
+        n, t.shape, [&](const long long (&)[R]) { return value; },
+        [&](const long long (&idx)[R]) {
+          long long off = 0;
+#pragma unroll
+          for (int d = 0; d < R; ++d) off += idx[d] * t.stride[d];
+          return off;
+        },
+        [&](long long off, float v) { st(t.p + off, v); });
   sync();
 }
 
@@ -581,12 +590,21 @@ __device__ void binary(const View<TO, R>& out, const View<TL, R>& lhs, const Vie
     sync();
     return;
   }
-  // every element is read before it is written (out may alias an operand)
-  each_element(
-      numel(out),
-      [&](long long i) {
-        const float a = ld(lhs.p + offset_of(lhs, i));
-        const float b = ld(rhs.p + offset_of(rhs, i));
+  // every element is read before it is written (out may alias an operand); the three views
+  // have one shape, so one walk over it serves them all
+  const long long n = numel(out);
+  if (n > 0)
+    each_index<R>(
+      n, out.shape,
+      [&](const long long (&idx)[R]) {
+        long long lo = 0, ro = 0;
+#pragma unroll
+        for (int d = 0; d < R; ++d) {
+          lo += idx[d] * lhs.stride[d];
+          ro += idx[d] * rhs.stride[d];
+        }
+        const float a = ld(lhs.p + lo);
+        const float b = ld(rhs.p + ro);
         switch (kind) {
           case 0: return a + b;
           case 1: return a - b;
@@ -595,7 +613,13 @@ __device__ void binary(const View<TO, R>& out, const View<TL, R>& lhs, const Vie
           default: return a > b ? a : b;
         }
       },
-      [&](long long i, float v) { st(out.p + offset_of(out, i), v); });
+      [&](const long long (&idx)[R]) {
+        long long off = 0;
+#pragma unroll
+        for (int d = 0; d < R; ++d) off += idx[d] * out.stride[d];
+        return off;
+      },
+      [&](long long off, float v) { st(out.p + off, v); });
   sync();
 }
 
