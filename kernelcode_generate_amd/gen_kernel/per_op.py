@@ -539,13 +539,9 @@ class _Emitter:
         L += [
             "  // A workspace of at most kLdsWorkspaceBytes lives in the workgroup's LDS (private to the",
             "  // workgroup for the launch, like its slice of device memory, at a fraction of the latency);",
-            "  // only the error word is then device memory.",
+            "  // only the error word is then device memory. (A gfx950 workgroup holds up to 160 KiB of LDS,",
+            "  // and HIP launches that much dynamic LDS without a per-function attribute.)",
             "  a.ws_lds = off > 0 && off <= kLdsWorkspaceBytes;",
-            "  if (a.ws_lds && hipFuncSetAttribute(reinterpret_cast<const void*>(kg_gfx950_generated_kernel),",
-            "                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)off) != hipSuccess) {",
-            "    (void)hipGetLastError();",
-            "    a.ws_lds = 0;",
-            "  }",
             "  const long long ws_block = a.ws_lds ? 0 : off;  // device-memory workspace per workgroup",
         ]
         par = self.plan.parallel
